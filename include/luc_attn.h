@@ -1,0 +1,135 @@
+/*
+ * luc_attn.h -- C ABI of the MI355X (gfx950) paged-attention path for the
+ * lucciola-rs Qwen2 engine.
+ *
+ * The library (liblucattn.so) loads gfx950 code objects with hipModuleLoad and
+ * launches hand-written HIP kernels on the caller's stream.  It replaces the
+ * engine's NVRTC/PTX loader (build.rs:14-42, src/ptx.rs:1-22,
+ * src/utils.rs:10-18) and three CUDA kernels: rope (src/kernels/rope.cu:3-54),
+ * update_kv_cache_kernel (src/kernels/kv_cache.cu:3-59) and
+ * flash_decoding_kernel_{64,128} (src/kernels/attention.cu:4-240).
+ *
+ * Conventions (all entry points):
+ *  - Plain pointers and sizes.  Device pointers are hipMalloc'd memory owned by
+ *    the caller; the library never allocates or frees caller memory, and the
+ *    split-K workspace is caller-provided.
+ *  - `stream` is a hipStream_t passed as void*; NULL means the null stream.
+ *    Launches are asynchronous; no entry point synchronises.
+ *  - Return 0 (LUC_OK) or a negative luc_status.  luc_last_error() returns a
+ *    thread-local message for the last failure on the calling thread.
+ *  - 16-bit storage (bf16 or fp16, luc_dtype), f32 arithmetic.
+ *  - KV pools use the engine's layout [phys_block][num_layers][Hkv][16][head_dim]
+ *    (src/layers/kv_cache.rs:50-68); block tables are int32 [rows][table_stride].
+ *  - Positions are device int32 arrays: the position of the current token, so a
+ *    sequence attends to positions 0..pos (ctx = pos + 1), as the reference's
+ *    device-resident pos_ptr (src/models.rs:489-493, :715).
+ *  - Only block_size 16 (kv_cache.rs:35) and head_dim 64/128
+ *    (kernels.rs:37-46) are supported; Hq must be a multiple of Hkv with
+ *    Hq/Hkv <= 8.
+ */
+#ifndef LUC_ATTN_H
+#define LUC_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LUC_ABI_VERSION 1
+#define LUC_BLOCK_SIZE 16
+
+typedef struct luc_ctx luc_ctx;
+
+typedef enum luc_dtype { LUC_BF16 = 0, LUC_F16 = 1 } luc_dtype;
+
+typedef enum luc_status {
+    LUC_OK = 0,
+    LUC_E_INVALID = -1,     /* bad argument (null pointer, bad size, misalignment) */
+    LUC_E_UNSUPPORTED = -2, /* head_dim / block_size / group size outside what is built */
+    LUC_E_LOAD = -3,        /* code object or kernel symbol could not be loaded */
+    LUC_E_HIP = -4,         /* a HIP runtime call failed */
+    LUC_E_WORKSPACE = -5    /* workspace missing or smaller than required */
+} luc_status;
+
+/* ABI version compiled into the library (LUC_ABI_VERSION). */
+int luc_abi_version(void);
+
+/* Thread-local description of the last error on this thread ("" if none). */
+const char* luc_last_error(void);
+
+/* Load the gfx950 code objects for `device` and resolve every kernel.
+ * `code_object_dir` is the directory holding the .hsaco files; NULL means the
+ * directory of the loaded library.  Replaces CudaFunctions::load
+ * (src/kernels.rs:32-107) and load_cuda_funtion (src/utils.rs:10-18). */
+int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx);
+void luc_destroy(luc_ctx* ctx);
+
+/* Host-side RoPE table, f32 [max_pos][head_dim/2] each, from the same f32
+ * formula as RopeCache::new (src/layers/rope.rs:11-40).  scale_factor <= 0
+ * means no rope_scaling (factor 1).  The caller copies it to the device. */
+int luc_rope_table(float* cos_out, float* sin_out, int max_pos, int head_dim, float base,
+                   float scale_factor);
+
+/* RoPE with q/k bias, in place, for num_tokens rows -- rope
+ * (src/kernels/rope.cu:3-54) as launched by CudaFunctions::apply_rope
+ * (src/kernels.rs:203-246).  Row r of q is q + r*row_stride, likewise k; the
+ * engine passes views into qkv_states, so row_stride = (Hq + 2*Hkv)*head_dim.
+ * positions[r] selects the cos/sin row.  Biases may be NULL (read as zero). */
+int luc_rope(luc_ctx* ctx, void* stream, int dtype, void* q, const void* q_bias, void* k,
+             const void* k_bias, int64_t row_stride, const float* cos_table,
+             const float* sin_table, const int32_t* positions, int num_tokens, int num_q_heads,
+             int num_kv_heads, int head_dim);
+
+/* Paged cache write of one token per row -- update_kv_cache_kernel
+ * (src/kernels/kv_cache.cu:3-59) as launched by KVCache::update
+ * (src/layers/kv_cache.rs:124-173).  Row r writes k (bit copy) and v + v_bias
+ * at slot positions[r] of table row r.  v_bias may be NULL. */
+int luc_kv_cache_update(luc_ctx* ctx, void* stream, int dtype, void* k_pool, void* v_pool,
+                        const void* k, const void* v, const void* v_bias, int64_t row_stride,
+                        const int32_t* block_tables, int table_stride,
+                        const int32_t* positions, int num_tokens, int layer, int num_layers,
+                        int num_kv_heads, int head_dim, int block_size);
+
+/* Fused RoPE + cache write: the two calls above in one launch, with the same
+ * results (q and k roped in place, roped k and v + v_bias written to the
+ * pools).  This is what the engine's per-layer step src/models.rs:505-534
+ * becomes. */
+int luc_rope_append(luc_ctx* ctx, void* stream, int dtype, void* q, const void* q_bias,
+                    void* k, const void* k_bias, const void* v, const void* v_bias,
+                    int64_t row_stride, const float* cos_table, const float* sin_table,
+                    const int32_t* positions, const int32_t* block_tables, int table_stride,
+                    void* k_pool, void* v_pool, int num_tokens, int layer, int num_layers,
+                    int num_q_heads, int num_kv_heads, int head_dim, int block_size);
+
+/* Bytes of f32 split-K workspace luc_paged_decode needs for these sizes (0
+ * when every sequence fits one split; the workspace may then be NULL).
+ * split_tokens: tokens per split-K chunk, rounded up to a multiple of 64
+ * (head_dim 64) or 32 (head_dim 128); 0 = the library's choice. */
+size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
+                                       int head_dim, int max_ctx, int split_tokens);
+
+/* Batched paged decode attention: flash_decoding_kernel_{64,128}
+ * (src/kernels/attention.cu:4-240) as launched by
+ * CudaFunctions::apply_flash_decoding (src/kernels.rs:248-320), for `batch`
+ * sequences at once.  Sequence b attends with q row b (q + b*q_row_stride,
+ * [Hq][head_dim]) to positions 0..positions[b] through table row b, and writes
+ * out row b (out + b*out_row_stride).  max_ctx is a host-side upper bound of
+ * positions[b]+1 (the reference's host `pos`, kernels.rs:266); a sequence
+ * whose context exceeds it, or is empty, gets NaN outputs, as the reference
+ * yields NaN for an empty context.  sm_scale is 1/sqrt(head_dim) in the
+ * engine (kernels.rs:264).  Work is split into split-K chunks whose partials
+ * go to `workspace` (see luc_paged_decode_workspace_size) and are merged by a
+ * log-sum-exp combine launch on the same stream. */
+int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t out_row_stride,
+                     const void* q, int64_t q_row_stride, const void* k_pool, const void* v_pool,
+                     const int32_t* block_tables, int table_stride, const int32_t* positions,
+                     int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
+                     int num_kv_heads, int head_dim, int block_size, float sm_scale,
+                     int split_tokens, void* workspace, size_t workspace_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LUC_ATTN_H */

@@ -1,0 +1,98 @@
+// Shared device helpers for the gfx950 paged-attention kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace luc {
+
+enum : int { kBF16 = 0, kF16 = 1 };
+constexpr int kPage = 16;  // tokens per KV page (block_size)
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
+
+// 16-bit storage <-> f32.  Rounding is round-to-nearest-even in both formats.
+template <int DT> struct St;
+
+template <> struct St<kBF16> {
+  __device__ static inline float load(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+  // low / high half of a packed pair
+  __device__ static inline float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ static inline float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  __device__ static inline uint16_t store(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+  }
+  // f32 dot of two packed pairs, accumulated into c
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf162_t, a),
+                                           __builtin_bit_cast(bf162_t, b), c, false);
+  }
+};
+
+template <> struct St<kF16> {
+  __device__ static inline float load(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+  __device__ static inline float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  __device__ static inline float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  __device__ static inline uint16_t store(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b), c,
+                                  false);
+  }
+};
+
+// ---- wave64 reductions -------------------------------------------------
+// DPP controls (GFX9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ inline float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Max over the 16 lanes of each DPP row; every lane of the row gets it.
+__device__ inline float row_max16(float x) {
+  x = fmaxf(x, dpp_mov<kDppQuadXor1>(x));
+  x = fmaxf(x, dpp_mov<kDppQuadXor2>(x));
+  x = fmaxf(x, dpp_mov<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp_mov<kDppMirror>(x));
+  return x;
+}
+__device__ inline float row_sum16(float x) {
+  x += dpp_mov<kDppQuadXor1>(x);
+  x += dpp_mov<kDppQuadXor2>(x);
+  x += dpp_mov<kDppHalfMirror>(x);
+  x += dpp_mov<kDppMirror>(x);
+  return x;
+}
+__device__ inline float readlane(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+// Wave-uniform max / sum over all 64 lanes.
+__device__ inline float wave_max(float x) {
+  x = row_max16(x);
+  return fmaxf(fmaxf(readlane(x, 0), readlane(x, 16)), fmaxf(readlane(x, 32), readlane(x, 48)));
+}
+__device__ inline float wave_sum(float x) {
+  x = row_sum16(x);
+  return (readlane(x, 0) + readlane(x, 16)) + (readlane(x, 32) + readlane(x, 48));
+}
+
+// Orders this wave's LDS accesses at this point (DS operations of one wave
+// complete in issue order, so a code-motion barrier is all that is needed).
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+}  // namespace luc

@@ -1,0 +1,393 @@
+// luc_attn.cpp -- host side of the C ABI declared in include/luc_attn.h.
+//
+// Loads the gfx950 code objects (hipModuleLoad), resolves every kernel once at
+// init (hipModuleGetFunction), validates arguments on the host and launches on
+// the caller's stream (hipModuleLaunchKernel).  It replaces the reference's
+// NVRTC build + PTX loader (build.rs:14-42, src/ptx.rs:1-22,
+// src/utils.rs:10-18) and the launch code in src/kernels.rs:203-320 and
+// src/layers/kv_cache.rs:124-173.
+//
+// After luc_init the context is read-only, so one context may be used from
+// several threads, each with its own stream.  Nothing here allocates device
+// memory or synchronises.
+#include "luc_attn.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <dlfcn.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+struct luc_ctx {
+  int device = 0;
+  std::vector<hipModule_t> modules;
+  std::unordered_map<std::string, hipFunction_t> fns;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define LUC_HIP(expr)                                                                  \
+  do {                                                                                 \
+    hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess) return fail(LUC_E_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+constexpr const char* kCodeObjects[] = {"rope_append.hsaco", "paged_decode.hsaco"};
+
+// Kernel-side constants (kept in step with csrc/kernels/paged_decode.hip).
+constexpr int kDecodeWaves = 4;
+int decode_tile(int head_dim) { return head_dim == 64 ? 64 : 32; }
+// Number of compute units the automatic split choice plans for (MI355X).
+constexpr int kPlanCUs = 256;
+
+const char* dt_name(int dtype) { return dtype == LUC_F16 ? "f16" : "bf16"; }
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+std::string self_dir() {
+  Dl_info info;
+  if (dladdr(reinterpret_cast<void*>(&luc_init), &info) && info.dli_fname) {
+    std::string p = info.dli_fname;
+    size_t s = p.rfind('/');
+    return s == std::string::npos ? std::string(".") : p.substr(0, s);
+  }
+  return ".";
+}
+
+int get_fn(const luc_ctx* ctx, const std::string& name, hipFunction_t* fn) {
+  auto it = ctx->fns.find(name);
+  if (it == ctx->fns.end()) return fail(LUC_E_LOAD, "kernel %s not loaded", name.c_str());
+  *fn = it->second;
+  return LUC_OK;
+}
+
+int check_device(const luc_ctx* ctx) {
+  int cur = -1;
+  LUC_HIP(hipGetDevice(&cur));
+  if (cur != ctx->device)
+    return fail(LUC_E_INVALID, "current device %d differs from the context's device %d", cur,
+                ctx->device);
+  return LUC_OK;
+}
+
+int check_common(const luc_ctx* ctx, int dtype, int head_dim) {
+  if (!ctx) return fail(LUC_E_INVALID, "null context");
+  if (dtype != LUC_BF16 && dtype != LUC_F16) return fail(LUC_E_INVALID, "bad dtype %d", dtype);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(LUC_E_UNSUPPORTED, "unsupported head_dim %d (64 or 128)", head_dim);
+  return LUC_OK;
+}
+
+int check_heads(int hq, int hkv) {
+  if (hq <= 0 || hkv <= 0) return fail(LUC_E_INVALID, "head counts must be positive");
+  if (hq % hkv) return fail(LUC_E_INVALID, "num_q_heads %d not a multiple of num_kv_heads %d", hq, hkv);
+  if (hq / hkv > 8) return fail(LUC_E_UNSUPPORTED, "group size %d > 8", hq / hkv);
+  return LUC_OK;
+}
+
+int launch(hipFunction_t fn, dim3 grid, dim3 block, void* stream, void** args) {
+  LUC_HIP(hipModuleLaunchKernel(fn, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0,
+                                reinterpret_cast<hipStream_t>(stream), args, nullptr));
+  return LUC_OK;
+}
+
+enum : int { kRopeQ = 1, kRopeK = 2, kWriteKV = 4 };
+
+struct AppendArgs {
+  void* q = nullptr;
+  const void* q_bias = nullptr;
+  void* k = nullptr;
+  const void* k_bias = nullptr;
+  const void* v = nullptr;
+  const void* v_bias = nullptr;
+  int64_t row_stride = 0;
+  const float* cos_t = nullptr;
+  const float* sin_t = nullptr;
+  const int32_t* positions = nullptr;
+  const int32_t* cu_seqlens = nullptr;
+  const int32_t* start_pos = nullptr;
+  int batch = 0;
+  const int32_t* tables = nullptr;
+  int table_stride = 0;
+  void* k_pool = nullptr;
+  void* v_pool = nullptr;
+  int layer = 0, num_layers = 1, hq = 0, hkv = 0, head_dim = 0, flags = 0;
+};
+
+int launch_append(const luc_ctx* ctx, void* stream, int dtype, int rows, AppendArgs a) {
+  hipFunction_t fn;
+  if (int rc = get_fn(ctx, std::string("luc_rope_append_") + dt_name(dtype), &fn)) return rc;
+  void* args[] = {&a.q,         &a.q_bias,    &a.k,          &a.k_bias,   &a.v,
+                  &a.v_bias,    &a.row_stride, &a.cos_t,     &a.sin_t,    &a.positions,
+                  &a.cu_seqlens, &a.start_pos, &a.batch,     &a.tables,   &a.table_stride,
+                  &a.k_pool,    &a.v_pool,    &a.layer,      &a.num_layers, &a.hq,
+                  &a.hkv,       &a.head_dim,  &a.flags};
+  return launch(fn, dim3(rows), dim3(128), stream, args);
+}
+
+int check_rows(int num_tokens, int64_t row_stride, int min_row) {
+  if (num_tokens < 0) return fail(LUC_E_INVALID, "num_tokens %d < 0", num_tokens);
+  if (row_stride < min_row)
+    return fail(LUC_E_INVALID, "row_stride %lld smaller than a row (%d)", (long long)row_stride, min_row);
+  return LUC_OK;
+}
+
+int check_cache(const void* k_pool, const void* v_pool, const int32_t* tables, int table_stride,
+                int layer, int num_layers, int block_size) {
+  if (block_size != LUC_BLOCK_SIZE)
+    return fail(LUC_E_UNSUPPORTED, "block_size %d (only %d)", block_size, LUC_BLOCK_SIZE);
+  if (!k_pool || !v_pool || !tables) return fail(LUC_E_INVALID, "null pool or block table");
+  if (!aligned(k_pool, 16) || !aligned(v_pool, 16))
+    return fail(LUC_E_INVALID, "KV pools must be 16-byte aligned");
+  if (num_layers <= 0 || layer < 0 || layer >= num_layers)
+    return fail(LUC_E_INVALID, "layer %d outside [0, %d)", layer, num_layers);
+  if (table_stride <= 0) return fail(LUC_E_INVALID, "table_stride %d <= 0", table_stride);
+  return LUC_OK;
+}
+
+int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requested) {
+  const int tile = decode_tile(head_dim);
+  if (requested > 0) return (int)ceil_div(requested, tile) * tile;
+  // Plan for ~4 active workgroups per CU, assuming the average context is
+  // half of max_ctx; each wave then walks `tpw` tiles of its split.
+  const int64_t wg_tokens = (int64_t)kDecodeWaves * tile;
+  const int64_t est = (int64_t)batch * hkv * ceil_div(std::max(max_ctx / 2, 1), wg_tokens);
+  int64_t tpw = est / (4 * kPlanCUs);
+  if (tpw < 1) tpw = 1;
+  if (tpw > 64) tpw = 64;
+  return (int)(tpw * wg_tokens);
+}
+
+size_t workspace_bytes_for(int batch, int hq, int head_dim, int max_ctx, int split_tokens) {
+  const int64_t max_splits = ceil_div(max_ctx, split_tokens);
+  if (max_splits <= 1) return 0;
+  return (size_t)batch * hq * max_splits * (head_dim + 2) * sizeof(float);
+}
+
+}  // namespace
+
+extern "C" {
+
+int luc_abi_version(void) { return LUC_ABI_VERSION; }
+
+const char* luc_last_error(void) { return g_err.c_str(); }
+
+int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
+  if (!out_ctx) return fail(LUC_E_INVALID, "out_ctx is null");
+  *out_ctx = nullptr;
+  int count = 0;
+  LUC_HIP(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count)
+    return fail(LUC_E_INVALID, "device %d outside [0, %d)", device, count);
+  LUC_HIP(hipSetDevice(device));
+  const std::string dir = code_object_dir ? std::string(code_object_dir) : self_dir();
+  auto* ctx = new luc_ctx;
+  ctx->device = device;
+  for (const char* name : kCodeObjects) {
+    const std::string path = dir + "/" + name;
+    hipModule_t mod;
+    hipError_t e = hipModuleLoad(&mod, path.c_str());
+    if (e != hipSuccess) {
+      luc_destroy(ctx);
+      return fail(LUC_E_LOAD, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
+    }
+    ctx->modules.push_back(mod);
+  }
+  std::vector<std::string> names;
+  for (const char* dt : {"bf16", "f16"}) {
+    names.push_back(std::string("luc_rope_append_") + dt);
+    for (int d : {64, 128}) {
+      for (int g = 1; g <= 8; ++g)
+        names.push_back(std::string("luc_decode_") + dt + "_d" + std::to_string(d) + "_g" +
+                        std::to_string(g));
+      names.push_back(std::string("luc_decode_combine_") + dt + "_d" + std::to_string(d));
+    }
+  }
+  for (const auto& n : names) {
+    hipFunction_t fn = nullptr;
+    for (hipModule_t m : ctx->modules)
+      if (hipModuleGetFunction(&fn, m, n.c_str()) == hipSuccess) break;
+    if (!fn) {
+      luc_destroy(ctx);
+      return fail(LUC_E_LOAD, "kernel %s not found in %s", n.c_str(), dir.c_str());
+    }
+    ctx->fns[n] = fn;
+  }
+  (void)hipGetLastError();  // clear the misses from probing several modules
+  *out_ctx = ctx;
+  return LUC_OK;
+}
+
+void luc_destroy(luc_ctx* ctx) {
+  if (!ctx) return;
+  for (hipModule_t m : ctx->modules) (void)hipModuleUnload(m);
+  delete ctx;
+}
+
+int luc_rope_table(float* cos_out, float* sin_out, int max_pos, int head_dim, float base,
+                   float scale_factor) {
+  if (!cos_out || !sin_out) return fail(LUC_E_INVALID, "null output");
+  if (max_pos < 0 || head_dim <= 0 || head_dim % 2) return fail(LUC_E_INVALID, "bad sizes");
+  if (!(base > 0.0f)) return fail(LUC_E_INVALID, "rope base must be positive");
+  const int half = head_dim / 2;
+  const float scale = scale_factor > 0.0f ? scale_factor : 1.0f;
+  for (int pos = 0; pos < max_pos; ++pos) {
+    for (int i = 0; i < half; ++i) {
+      // f32 throughout, in the order of src/layers/rope.rs:26-29
+      const float t = (float)pos / scale;
+      const float theta = t / powf(base, (float)(2 * i) / (float)head_dim);
+      cos_out[(int64_t)pos * half + i] = cosf(theta);
+      sin_out[(int64_t)pos * half + i] = sinf(theta);
+    }
+  }
+  return LUC_OK;
+}
+
+int luc_rope(luc_ctx* ctx, void* stream, int dtype, void* q, const void* q_bias, void* k,
+             const void* k_bias, int64_t row_stride, const float* cos_table,
+             const float* sin_table, const int32_t* positions, int num_tokens, int num_q_heads,
+             int num_kv_heads, int head_dim) {
+  if (int rc = check_common(ctx, dtype, head_dim)) return rc;
+  if (int rc = check_heads(num_q_heads, num_kv_heads)) return rc;
+  if (int rc = check_rows(num_tokens, row_stride, num_q_heads * head_dim)) return rc;
+  if (num_tokens == 0) return LUC_OK;
+  if (!q || !k || !cos_table || !sin_table || !positions)
+    return fail(LUC_E_INVALID, "null q, k, rope table or positions");
+  if (int rc = check_device(ctx)) return rc;
+  AppendArgs a;
+  a.q = q; a.q_bias = q_bias; a.k = k; a.k_bias = k_bias;
+  a.row_stride = row_stride; a.cos_t = cos_table; a.sin_t = sin_table; a.positions = positions;
+  a.hq = num_q_heads; a.hkv = num_kv_heads; a.head_dim = head_dim;
+  a.flags = kRopeQ | kRopeK;
+  return launch_append(ctx, stream, dtype, num_tokens, a);
+}
+
+int luc_kv_cache_update(luc_ctx* ctx, void* stream, int dtype, void* k_pool, void* v_pool,
+                        const void* k, const void* v, const void* v_bias, int64_t row_stride,
+                        const int32_t* block_tables, int table_stride,
+                        const int32_t* positions, int num_tokens, int layer, int num_layers,
+                        int num_kv_heads, int head_dim, int block_size) {
+  if (int rc = check_common(ctx, dtype, head_dim)) return rc;
+  if (num_kv_heads <= 0) return fail(LUC_E_INVALID, "num_kv_heads %d <= 0", num_kv_heads);
+  if (int rc = check_rows(num_tokens, row_stride, num_kv_heads * head_dim)) return rc;
+  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers, block_size))
+    return rc;
+  if (num_tokens == 0) return LUC_OK;
+  if (!k || !v || !positions) return fail(LUC_E_INVALID, "null k, v or positions");
+  if (int rc = check_device(ctx)) return rc;
+  AppendArgs a;
+  a.k = const_cast<void*>(k); a.v = v; a.v_bias = v_bias; a.row_stride = row_stride;
+  a.positions = positions; a.tables = block_tables; a.table_stride = table_stride;
+  a.k_pool = k_pool; a.v_pool = v_pool; a.layer = layer; a.num_layers = num_layers;
+  a.hq = num_kv_heads; a.hkv = num_kv_heads; a.head_dim = head_dim;
+  a.flags = kWriteKV;
+  return launch_append(ctx, stream, dtype, num_tokens, a);
+}
+
+int luc_rope_append(luc_ctx* ctx, void* stream, int dtype, void* q, const void* q_bias,
+                    void* k, const void* k_bias, const void* v, const void* v_bias,
+                    int64_t row_stride, const float* cos_table, const float* sin_table,
+                    const int32_t* positions, const int32_t* block_tables, int table_stride,
+                    void* k_pool, void* v_pool, int num_tokens, int layer, int num_layers,
+                    int num_q_heads, int num_kv_heads, int head_dim, int block_size) {
+  if (int rc = check_common(ctx, dtype, head_dim)) return rc;
+  if (int rc = check_heads(num_q_heads, num_kv_heads)) return rc;
+  if (int rc = check_rows(num_tokens, row_stride, num_q_heads * head_dim)) return rc;
+  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers, block_size))
+    return rc;
+  if (num_tokens == 0) return LUC_OK;
+  if (!q || !k || !v || !cos_table || !sin_table || !positions)
+    return fail(LUC_E_INVALID, "null q, k, v, rope table or positions");
+  if (int rc = check_device(ctx)) return rc;
+  AppendArgs a;
+  a.q = q; a.q_bias = q_bias; a.k = k; a.k_bias = k_bias; a.v = v; a.v_bias = v_bias;
+  a.row_stride = row_stride; a.cos_t = cos_table; a.sin_t = sin_table; a.positions = positions;
+  a.tables = block_tables; a.table_stride = table_stride; a.k_pool = k_pool; a.v_pool = v_pool;
+  a.layer = layer; a.num_layers = num_layers; a.hq = num_q_heads; a.hkv = num_kv_heads;
+  a.head_dim = head_dim; a.flags = kRopeQ | kRopeK | kWriteKV;
+  return launch_append(ctx, stream, dtype, num_tokens, a);
+}
+
+size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
+                                       int head_dim, int max_ctx, int split_tokens) {
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_ctx <= 0) return 0;
+  if (head_dim != 64 && head_dim != 128) return 0;
+  const int st = split_tokens_for(batch, num_kv_heads, head_dim, max_ctx, split_tokens);
+  return workspace_bytes_for(batch, num_q_heads, head_dim, max_ctx, st);
+}
+
+int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t out_row_stride,
+                     const void* q, int64_t q_row_stride, const void* k_pool, const void* v_pool,
+                     const int32_t* block_tables, int table_stride, const int32_t* positions,
+                     int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
+                     int num_kv_heads, int head_dim, int block_size, float sm_scale,
+                     int split_tokens, void* workspace, size_t workspace_bytes) {
+  if (int rc = check_common(ctx, dtype, head_dim)) return rc;
+  if (int rc = check_heads(num_q_heads, num_kv_heads)) return rc;
+  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers, block_size))
+    return rc;
+  if (batch < 0) return fail(LUC_E_INVALID, "batch %d < 0", batch);
+  if (batch == 0) return LUC_OK;
+  if (max_ctx <= 0) return fail(LUC_E_INVALID, "max_ctx %d <= 0", max_ctx);
+  if (split_tokens < 0) return fail(LUC_E_INVALID, "split_tokens %d < 0", split_tokens);
+  if (!out || !q || !positions) return fail(LUC_E_INVALID, "null out, q or positions");
+  const int row = num_q_heads * head_dim;
+  if (q_row_stride < row || out_row_stride < row)
+    return fail(LUC_E_INVALID, "q/out row stride smaller than Hq*head_dim (%d)", row);
+  if (!aligned(q, 4) || (q_row_stride % 2))
+    return fail(LUC_E_INVALID, "q must be 4-byte aligned with an even row stride");
+  if ((int64_t)table_stride * LUC_BLOCK_SIZE < max_ctx)
+    return fail(LUC_E_INVALID, "table_stride %d pages cannot hold max_ctx %d", table_stride, max_ctx);
+  if (int rc = check_device(ctx)) return rc;
+
+  const int st = split_tokens_for(batch, num_kv_heads, head_dim, max_ctx, split_tokens);
+  const int max_splits = (int)ceil_div(max_ctx, st);
+  const size_t need = workspace_bytes_for(batch, num_q_heads, head_dim, max_ctx, st);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(LUC_E_WORKSPACE, "workspace %zu bytes, %zu needed", workspace_bytes, need);
+  if (need && !aligned(workspace, 16)) return fail(LUC_E_INVALID, "workspace must be 16-byte aligned");
+
+  const int group = num_q_heads / num_kv_heads;
+  hipFunction_t fdec, fcomb;
+  const std::string dsuffix = std::string(dt_name(dtype)) + "_d" + std::to_string(head_dim);
+  if (int rc = get_fn(ctx, "luc_decode_" + dsuffix + "_g" + std::to_string(group), &fdec)) return rc;
+  if (int rc = get_fn(ctx, "luc_decode_combine_" + dsuffix, &fcomb)) return rc;
+
+  float* ws_ml = static_cast<float*>(workspace);
+  float* ws_o = need ? ws_ml + (size_t)batch * num_q_heads * max_splits * 2 : nullptr;
+  float qk_scale_log2 = sm_scale * 1.4426950408889634f;
+  int hkv = num_kv_heads, hq = num_q_heads;
+  void* args[] = {const_cast<void**>(&q), &q_row_stride, const_cast<void**>(&k_pool),
+                  const_cast<void**>(&v_pool), const_cast<int32_t**>(&block_tables),
+                  &table_stride, const_cast<int32_t**>(&positions), &layer, &num_layers, &hkv,
+                  &qk_scale_log2, &max_ctx, const_cast<int*>(&st), const_cast<int*>(&max_splits),
+                  &ws_ml, &ws_o, &out, &out_row_stride};
+  if (int rc = launch(fdec, dim3(max_splits, num_kv_heads, batch), dim3(kDecodeWaves * 64), stream, args))
+    return rc;
+  void* cargs[] = {&ws_ml, &ws_o, const_cast<int32_t**>(&positions), &hq, &max_ctx,
+                   const_cast<int*>(&st), const_cast<int*>(&max_splits), &out, &out_row_stride};
+  return launch(fcomb, dim3(num_q_heads, batch), dim3(head_dim), stream, cargs);
+}
+
+}  // extern "C"

@@ -1,0 +1,179 @@
+"""ctypes binding of liblucattn.so (include/luc_attn.h) over torch tensors.
+
+torch is imported first so that the library binds to the HIP runtime torch has
+already loaded (both name it libamdhip64.so.7): device pointers and streams
+from torch are then valid in the library.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+
+LUC_BF16 = 0
+LUC_F16 = 1
+STATUS = {0: "LUC_OK", -1: "LUC_E_INVALID", -2: "LUC_E_UNSUPPORTED", -3: "LUC_E_LOAD",
+          -4: "LUC_E_HIP", -5: "LUC_E_WORKSPACE"}
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); every function declared in include/luc_attn.h
+SIGNATURES = {
+    "luc_abi_version": (_i32, []),
+    "luc_last_error": (ctypes.c_char_p, []),
+    "luc_init": (_i32, [_i32, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "luc_destroy": (None, [_vp]),
+    "luc_rope_table": (_i32, [_vp, _vp, _i32, _i32, _f32, _f32]),
+    "luc_rope": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32,
+                        _i32]),
+    "luc_kv_cache_update": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i32, _vp,
+                                   _i32, _i32, _i32, _i32, _i32, _i32]),
+    "luc_rope_append": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
+                               _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "luc_paged_decode_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "luc_paged_decode": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i32, _vp,
+                                _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp,
+                                _sz]),
+}
+
+
+def lib_dir() -> str:
+    return os.path.join(_HERE, "lib")
+
+
+def lib_path() -> str:
+    return os.path.join(lib_dir(), "liblucattn.so")
+
+
+class LucError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"{STATUS.get(code, code)}: {msg}")
+        self.code = code
+
+
+_CDLL = None
+
+
+def load_cdll() -> ctypes.CDLL:
+    """Load liblucattn.so and declare its signatures (no GPU call)."""
+    global _CDLL
+    if _CDLL is None:
+        path = lib_path()
+        if not os.path.exists(path):
+            raise LucError(-3, f"{path} is not built (run lucciola-rs_amd/build.py)")
+        cdll = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(cdll, name)
+            fn.restype = res
+            fn.argtypes = args
+        _CDLL = cdll
+    return _CDLL
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return LUC_BF16
+    if t.dtype == torch.float16:
+        return LUC_F16
+    raise TypeError(f"unsupported storage dtype {t.dtype}")
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+class LucAttn:
+    """One luc_ctx (code objects loaded on one device) and its entry points."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_cdll()
+        self.device = device
+        self.ctx = ctypes.c_void_p()
+        with torch.cuda.device(device):
+            rc = self.lib.luc_init(device, lib_dir().encode(), ctypes.byref(self.ctx))
+        self._check(rc)
+
+    def close(self):
+        if self.ctx:
+            self.lib.luc_destroy(self.ctx)
+            self.ctx = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc):
+        if rc != 0:
+            raise LucError(rc, self.lib.luc_last_error().decode())
+
+    # ---- host helpers --------------------------------------------------
+    def rope_table(self, max_pos, head_dim, base=1e6, scale_factor=None):
+        cos = torch.empty((max_pos, head_dim // 2), dtype=torch.float32)
+        sin = torch.empty((max_pos, head_dim // 2), dtype=torch.float32)
+        self._check(self.lib.luc_rope_table(_p(cos), _p(sin), max_pos, head_dim, base,
+                                            scale_factor or 0.0))
+        return cos, sin
+
+    def workspace_size(self, batch, hq, hkv, head_dim, max_ctx, split_tokens=0):
+        return self.lib.luc_paged_decode_workspace_size(batch, hq, hkv, head_dim, max_ctx,
+                                                        split_tokens)
+
+    # ---- launches ------------------------------------------------------
+    def rope(self, q, q_bias, k, k_bias, row_stride, cos, sin, positions, num_tokens, hq, hkv,
+             head_dim, stream=None):
+        self._check(self.lib.luc_rope(self.ctx, _stream(stream), dtype_code(q), _p(q), _p(q_bias),
+                                      _p(k), _p(k_bias), row_stride, _p(cos), _p(sin),
+                                      _p(positions), num_tokens, hq, hkv, head_dim))
+
+    def kv_cache_update(self, k_pool, v_pool, k, v, v_bias, row_stride, tables, positions,
+                        num_tokens, layer, num_layers, hkv, head_dim, block_size=16,
+                        stream=None):
+        self._check(self.lib.luc_kv_cache_update(
+            self.ctx, _stream(stream), dtype_code(k_pool), _p(k_pool), _p(v_pool), _p(k), _p(v),
+            _p(v_bias), row_stride, _p(tables), tables.shape[-1], _p(positions), num_tokens,
+            layer, num_layers, hkv, head_dim, block_size))
+
+    def rope_append(self, q, q_bias, k, k_bias, v, v_bias, row_stride, cos, sin, positions,
+                    tables, k_pool, v_pool, num_tokens, layer, num_layers, hq, hkv, head_dim,
+                    block_size=16, stream=None):
+        self._check(self.lib.luc_rope_append(
+            self.ctx, _stream(stream), dtype_code(k_pool), _p(q), _p(q_bias), _p(k), _p(k_bias),
+            _p(v), _p(v_bias), row_stride, _p(cos), _p(sin), _p(positions), _p(tables),
+            tables.shape[-1], _p(k_pool), _p(v_pool), num_tokens, layer, num_layers, hq, hkv,
+            head_dim, block_size))
+
+    def paged_decode(self, out, q, k_pool, v_pool, tables, positions, batch, max_ctx, layer,
+                     num_layers, hq, hkv, head_dim, sm_scale, split_tokens=0, workspace=None,
+                     out_row_stride=None, q_row_stride=None, block_size=16, stream=None):
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        self._check(self.lib.luc_paged_decode(
+            self.ctx, _stream(stream), dtype_code(k_pool), _p(out),
+            out_row_stride if out_row_stride is not None else hq * head_dim, _p(q),
+            q_row_stride if q_row_stride is not None else hq * head_dim, _p(k_pool), _p(v_pool),
+            _p(tables), tables.shape[-1], _p(positions), batch, max_ctx, layer, num_layers, hq,
+            hkv, head_dim, block_size, sm_scale, split_tokens, _p(workspace), ws_bytes))
+
+
+_DEFAULT = {}
+
+
+def default(device: int = 0) -> LucAttn:
+    """Process-wide LucAttn for `device` (created on first use)."""
+    if device not in _DEFAULT:
+        _DEFAULT[device] = LucAttn(device)
+    return _DEFAULT[device]

@@ -1,0 +1,378 @@
+/*
+ * luc_oracle.c -- CPU restatement of lucciola-rs's paged-attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker, never the product.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ *
+ * Built with -ffp-contract=off so every multiply and add rounds where written.
+ * Where the reference's CUDA source has a multiply-add that NVRTC contracts by
+ * default (build.rs:32-40 uses default CompileOptions, i.e. --fmad=true), the
+ * restatement writes fmaf() explicitly; where the contraction is ambiguous the
+ * choice is noted.  Those choices, and CUDA's expf versus glibc's expf, are
+ * the parts no available reference output pins.
+ *
+ * ORC_MUTANT (compile-time, 0 = off) plants one known mistake; the test suite
+ * builds each mutant and checks that its pinning checks reject it.
+ */
+#include "luc_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#ifndef ORC_MUTANT
+#define ORC_MUTANT 0
+#endif
+
+/* ------------------------------------------------------------------ */
+/* Conversions                                                         */
+/* ------------------------------------------------------------------ */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u)          /* NaN: keep sign, force quiet */
+        return (uint16_t)((u >> 16) | 0x0040u);
+    uint32_t lsb = (u >> 16) & 1u;                 /* round to nearest, ties to even */
+    u += 0x7fffu + lsb;
+    return (uint16_t)(u >> 16);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    if (exp == 0x1fu)                              /* inf / NaN */
+        return u2f(sign | 0x7f800000u | (man << 13));
+    if (exp == 0) {
+        if (man == 0) return u2f(sign);
+        /* subnormal: man * 2^-24, exact in f32 */
+        float v = (float)man * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    return u2f(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x = f2u(f);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+    if (ax == 0x7f800000u) return (uint16_t)(sign | 0x7c00u);
+    uint32_t e = ax >> 23;                         /* biased f32 exponent */
+    uint32_t m = (ax & 0x7fffffu) | 0x800000u;     /* 24-bit significand */
+    if (e < 113u) {                                /* |f| < 2^-14: f16 subnormal or zero */
+        if (e == 0) return sign;                   /* f32 zero/subnormal -> 0 */
+        uint32_t s = 126u - e;                     /* value / 2^-24 = m >> s */
+        if (s > 24u) return sign;
+        uint32_t q = m >> s;
+        uint32_t rem = m & ((1u << s) - 1u);
+        uint32_t half = 1u << (s - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t r = ((e - 112u) << 10) | ((m >> 13) & 0x3ffu);
+    uint32_t rem = m & 0x1fffu;
+    if (ORC_MUTANT != 10 && (rem > 0x1000u || (rem == 0x1000u && (r & 1u)))) r++;
+    if (r >= 0x7c00u) return (uint16_t)(sign | 0x7c00u);   /* overflow -> inf */
+    return (uint16_t)(sign | r);
+}
+
+static inline float ld(uint16_t h, int dtype) {
+    return dtype == ORC_F16 ? orc_f16_to_f32(h) : orc_bf16_to_f32(h);
+}
+static inline uint16_t st(float f, int dtype) {
+    return dtype == ORC_F16 ? orc_f32_to_f16(f) : orc_f32_to_bf16(f);
+}
+
+void orc_convert_f32_to_storage(const float* src, uint16_t* dst, int64_t n, int dtype) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = st(src[i], dtype);
+}
+void orc_convert_storage_to_f32(const uint16_t* src, float* dst, int64_t n, int dtype) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = ld(src[i], dtype);
+}
+
+/* ------------------------------------------------------------------ */
+/* RoPE table: src/layers/rope.rs:21-31                                 */
+/* ------------------------------------------------------------------ */
+void orc_rope_table(float* cos_out, float* sin_out, int max_pos, int head_dim, float base,
+                    float scale_factor) {
+    const int half = head_dim / 2;
+    const float scale = scale_factor > 0.0f ? scale_factor : 1.0f;     /* rope.rs:21 */
+    for (int pos = 0; pos < max_pos; ++pos) {
+        for (int i = 0; i < half; ++i) {
+            float t = (float)pos / scale;                                /* rope.rs:26 */
+            float theta = t / powf(base, (float)(2 * i) / (float)head_dim); /* rope.rs:27 */
+            cos_out[(int64_t)pos * half + i] = cosf(theta);              /* rope.rs:28 */
+            sin_out[(int64_t)pos * half + i] = sinf(theta);              /* rope.rs:29 */
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* rope kernel: src/kernels/rope.cu:3-53                               */
+/* ------------------------------------------------------------------ */
+static inline void rotate_pair(uint16_t* x, const uint16_t* bias, int i1, int i2, float c,
+                               float s, int dtype) {
+    float b1 = bias ? ld(bias[i1], dtype) : 0.0f;                       /* rope.cu:32-33 */
+    float b2 = bias ? ld(bias[i2], dtype) : 0.0f;
+    float v1 = ld(x[i1], dtype) + (ORC_MUTANT == 2 ? 0.0f : b1);         /* rope.cu:34-35 */
+    float v2 = ld(x[i2], dtype) + (ORC_MUTANT == 2 ? 0.0f : b2);
+    /* rope.cu:38-39.  Written uncontracted: each product rounds, then the
+     * sum rounds (NVRTC may fuse one product; that choice is unpinned). */
+    float a = v1 * c, b = v2 * s;
+    float e = v1 * s, f = v2 * c;
+#if ORC_MUTANT == 2
+    x[i1] = st(a - b + b1, dtype);
+    x[i2] = st(e + f + b2, dtype);
+#elif ORC_MUTANT == 3
+    x[i1] = st(a + b, dtype);
+    x[i2] = st(e - f, dtype);
+#else
+    x[i1] = st(a - b, dtype);
+    x[i2] = st(e + f, dtype);
+#endif
+}
+
+void orc_rope(uint16_t* q, const uint16_t* q_bias, uint16_t* k, const uint16_t* k_bias,
+              const float* cos_t, const float* sin_t, int pos, int head_dim, int num_q_heads,
+              int num_kv_heads, int dtype) {
+    const int half = head_dim / 2;
+    for (int idx = 0; idx < num_q_heads * half; ++idx) {                /* rope.cu:15-23 */
+        int head = idx / half, dim = idx % half;
+        float c = cos_t[(int64_t)pos * half + dim];                      /* rope.cu:25-26 */
+        float s = sin_t[(int64_t)pos * half + dim];
+        int i1 = head * head_dim + dim, i2 = i1 + half;
+        rotate_pair(q, q_bias, i1, i2, c, s, dtype);
+        if (head < num_kv_heads)                                         /* rope.cu:42-52 */
+            rotate_pair(k, k_bias, i1, i2, c, s, dtype);
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* Cache write: src/kernels/kv_cache.cu:3-59                           */
+/* ------------------------------------------------------------------ */
+int64_t orc_slot_offset(const int32_t* block_table, int pos, int layer, int kv_head,
+                        int num_layers, int num_kv_heads, int head_dim, int block_size) {
+    int logical = pos / block_size;                                      /* kv_cache.cu:24 */
+    int offset = pos % block_size;                                       /* kv_cache.cu:25 */
+    int64_t phys = block_table[logical];                                 /* kv_cache.cu:28 */
+    int64_t stride_block = (int64_t)num_layers * num_kv_heads * block_size * head_dim;
+    int64_t stride_layer = (int64_t)num_kv_heads * block_size * head_dim;
+    int64_t stride_head = (int64_t)block_size * head_dim;
+#if ORC_MUTANT == 4
+    return phys * stride_block + (int64_t)layer * stride_layer + (int64_t)kv_head * head_dim +
+           (int64_t)offset * stride_head;
+#else
+    return phys * stride_block + (int64_t)layer * stride_layer + (int64_t)kv_head * stride_head +
+           (int64_t)offset * head_dim;                                   /* kv_cache.cu:45-48 */
+#endif
+}
+
+void orc_kv_update(uint16_t* k_pool, uint16_t* v_pool, const uint16_t* new_k,
+                   const uint16_t* new_v, const uint16_t* v_bias, const int32_t* block_table,
+                   int layer, int pos, int num_layers, int num_kv_heads, int head_dim,
+                   int block_size, int dtype) {
+    for (int h = 0; h < num_kv_heads; ++h) {
+        int64_t base = orc_slot_offset(block_table, pos, layer, h, num_layers, num_kv_heads,
+                                       head_dim, block_size);
+        for (int d = 0; d < head_dim; ++d) {
+            int idx = h * head_dim + d;                                  /* kv_cache.cu:50 */
+            k_pool[base + d] = new_k[idx];                               /* kv_cache.cu:53 bit copy */
+            float v = ld(new_v[idx], dtype);                             /* kv_cache.cu:56-58 */
+            float b = (v_bias && ORC_MUTANT != 6) ? ld(v_bias[idx], dtype) : 0.0f;
+            v_pool[base + d] = st(v + b, dtype);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* Decode attention: src/kernels/attention.cu:4-176                     */
+/* ------------------------------------------------------------------ */
+#define ORC_WARPS 32   /* kernels.rs:269: 1024 threads -> 32 warps */
+#define ORC_LANES 32
+#define ORC_MAXD 256
+
+/* One q-head: returns the f32 result before the final rounding in o_out. */
+static void attend_head(float* o_out, const uint16_t* q_head, const uint16_t* k_pool,
+                        const uint16_t* v_pool, const int32_t* table, int layer, int kv_head,
+                        int num_kv_heads, int head_dim, int pos, float sm_scale, int block_size,
+                        int num_layers, int dtype) {
+    float sq[ORC_MAXD];
+    for (int i = 0; i < head_dim; ++i) sq[i] = ld(q_head[i], dtype);  /* attention.cu:49-51 */
+
+    float pm[ORC_WARPS], pl[ORC_WARPS];
+    static __thread float po[ORC_WARPS][ORC_MAXD];
+
+    const int64_t stride_block = (int64_t)num_layers * num_kv_heads * block_size * head_dim;
+    const int64_t stride_layer = (int64_t)num_kv_heads * block_size * head_dim;
+    const int64_t stride_head = (int64_t)block_size * head_dim;
+    const int64_t layer_head = (int64_t)layer * stride_layer + (int64_t)kv_head * stride_head;
+
+    for (int w = 0; w < ORC_WARPS; ++w) {
+        float m = -1e20f, l = 0.0f;                                      /* attention.cu:61-62 */
+        float* o = po[w];
+        for (int i = 0; i < head_dim; ++i) o[i] = 0.0f;
+        for (int t = w; ORC_MUTANT == 7 ? t < pos : t <= pos; t += ORC_WARPS) { /* attention.cu:80 */
+            int64_t phys = table[t / block_size];
+            int64_t off = phys * stride_block + layer_head + (int64_t)(t % block_size) * head_dim;
+            /* attention.cu:93-96: lane j sums dims j, j+32, ... (fused mul-add) */
+            float lane[ORC_LANES];
+            for (int j = 0; j < ORC_LANES; ++j) {
+                float s = 0.0f;
+                for (int i = j; i < head_dim; i += ORC_LANES)
+                    s = fmaf(sq[i], ld((ORC_MUTANT == 8 ? v_pool : k_pool)[off + i], dtype), s);
+                lane[j] = s;
+            }
+            /* attention.cu:99-102: shfl_down tree 16,8,4,2,1; lane 0's value */
+            for (int step = ORC_LANES / 2; step > 0; step /= 2)
+                for (int j = 0; j < step; ++j) lane[j] += lane[j + step];
+            float score = ORC_MUTANT == 1 ? lane[0] : lane[0] * sm_scale; /* attention.cu:103 */
+            float m_prev = m;                                            /* attention.cu:106-111 */
+            m = fmaxf(m_prev, score);
+            float exp_m = expf(m_prev - m);
+            float exp_s = expf(score - m);
+            l = fmaf(l, exp_m, exp_s);
+            for (int i = 0; i < head_dim; ++i) {                         /* attention.cu:115-119 */
+                float v = ld(v_pool[off + i], dtype);
+                o[i] = fmaf(o[i], exp_m, v * exp_s);
+            }
+        }
+        pm[w] = m;
+        pl[w] = l;
+    }
+    /* attention.cu:140-174: warp 0 merges the 32 partitions */
+    float gm = -1e20f;
+    for (int w = 0; w < ORC_WARPS; ++w) gm = fmaxf(gm, pm[w]);
+    float gl = 0.0f;
+    for (int w = 0; w < ORC_WARPS; ++w) {
+        if (pm[w] <= -1e19f) continue;
+        gl = fmaf(pl[w], ORC_MUTANT == 5 ? 1.0f : expf(pm[w] - gm), gl);
+    }
+    for (int i = 0; i < head_dim; ++i) {
+        float so = 0.0f;
+        for (int w = 0; w < ORC_WARPS; ++w) {
+            if (pm[w] <= -1e19f) continue;
+            so = fmaf(po[w][i], expf(pm[w] - gm), so);
+        }
+        o_out[i] = so / gl;
+    }
+}
+
+void orc_flash_decoding(uint16_t* out, const uint16_t* q, const uint16_t* k_pool,
+                        const uint16_t* v_pool, const int32_t* block_table, int layer,
+                        int num_q_heads, int num_kv_heads, int head_dim, int pos,
+                        float sm_scale, int block_size, int num_layers, int dtype) {
+    float o[ORC_MAXD];
+    const int group = num_q_heads / num_kv_heads;                        /* attention.cu:23 */
+    for (int h = 0; h < num_q_heads; ++h) {
+        attend_head(o, q + (int64_t)h * head_dim, k_pool, v_pool, block_table, layer,
+                    ORC_MUTANT == 9 ? h % num_kv_heads : h / group, num_kv_heads, head_dim, pos, sm_scale, block_size, num_layers,
+                    dtype);
+        for (int i = 0; i < head_dim; ++i)
+            out[(int64_t)h * head_dim + i] = st(o[i], dtype);           /* attention.cu:173 */
+    }
+}
+
+static void set_threads(int num_threads) {
+#ifdef _OPENMP
+    if (num_threads > 0) omp_set_num_threads(num_threads);
+#else
+    (void)num_threads;
+#endif
+}
+
+void orc_decode_batch(uint16_t* out, int64_t out_stride, const uint16_t* q, int64_t q_stride,
+                      const uint16_t* k_pool, const uint16_t* v_pool,
+                      const int32_t* block_tables, int table_stride, const int32_t* positions,
+                      int batch, int layer, int num_q_heads, int num_kv_heads, int head_dim,
+                      float sm_scale, int block_size, int num_layers, int dtype,
+                      int num_threads) {
+    set_threads(num_threads);
+    const int group = num_q_heads / num_kv_heads;
+    const int64_t items = (int64_t)batch * num_q_heads;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t it = 0; it < items; ++it) {
+        int b = (int)(it / num_q_heads), h = (int)(it % num_q_heads);
+        float o[ORC_MAXD];
+        attend_head(o, q + b * q_stride + (int64_t)h * head_dim, k_pool, v_pool,
+                    block_tables + (int64_t)b * table_stride, layer, ORC_MUTANT == 9 ? h % num_kv_heads : h / group, num_kv_heads,
+                    head_dim, positions[b], sm_scale, block_size, num_layers, dtype);
+        for (int i = 0; i < head_dim; ++i)
+            out[b * out_stride + (int64_t)h * head_dim + i] = st(o[i], dtype);
+    }
+}
+
+void orc_decode_step(uint16_t* out, int64_t out_stride, uint16_t* qkv, int64_t qkv_stride,
+                     const uint16_t* q_bias, const uint16_t* k_bias, const uint16_t* v_bias,
+                     const float* cos_t, const float* sin_t, uint16_t* k_pool, uint16_t* v_pool,
+                     const int32_t* block_tables, int table_stride, const int32_t* positions,
+                     int batch, int layer, int num_q_heads, int num_kv_heads, int head_dim,
+                     float sm_scale, int block_size, int num_layers, int dtype,
+                     int num_threads) {
+    const int64_t q_dim = (int64_t)num_q_heads * head_dim;
+    const int64_t kv_dim = (int64_t)num_kv_heads * head_dim;
+    /* models.rs:505-534: rope then cache write, per sequence */
+    for (int b = 0; b < batch; ++b) {
+        uint16_t* row = qkv + b * qkv_stride;
+        const int32_t* table = block_tables + (int64_t)b * table_stride;
+        orc_rope(row, q_bias, row + q_dim, k_bias, cos_t, sin_t, positions[b], head_dim,
+                 num_q_heads, num_kv_heads, dtype);
+        orc_kv_update(k_pool, v_pool, row + q_dim, row + q_dim + kv_dim, v_bias, table, layer,
+                      positions[b], num_layers, num_kv_heads, head_dim, block_size, dtype);
+    }
+    /* models.rs:536-549 */
+    orc_decode_batch(out, out_stride, qkv, qkv_stride, k_pool, v_pool, block_tables,
+                     table_stride, positions, batch, layer, num_q_heads, num_kv_heads, head_dim,
+                     sm_scale, block_size, num_layers, dtype, num_threads);
+}
+
+void orc_prefill(uint16_t* out, int64_t out_stride, uint16_t* qkv, int64_t qkv_stride,
+                 const uint16_t* q_bias, const uint16_t* k_bias, const uint16_t* v_bias,
+                 const float* cos_t, const float* sin_t, uint16_t* k_pool, uint16_t* v_pool,
+                 const int32_t* block_tables, int table_stride, const int32_t* cu_seqlens,
+                 const int32_t* start_pos, int batch, int layer, int num_q_heads,
+                 int num_kv_heads, int head_dim, float sm_scale, int block_size,
+                 int num_layers, int dtype, int num_threads) {
+    set_threads(num_threads);
+    const int64_t q_dim = (int64_t)num_q_heads * head_dim;
+    const int64_t kv_dim = (int64_t)num_kv_heads * head_dim;
+    /* models.rs:486-534, serial per token.  The attention of token t reads
+     * only cache slots <= its own position, all written by then, so the
+     * attention calls can run after all writes without changing any value. */
+    for (int b = 0; b < batch; ++b) {
+        const int32_t* table = block_tables + (int64_t)b * table_stride;
+        for (int r = cu_seqlens[b]; r < cu_seqlens[b + 1]; ++r) {
+            int pos = start_pos[b] + (r - cu_seqlens[b]);
+            uint16_t* row = qkv + r * qkv_stride;
+            orc_rope(row, q_bias, row + q_dim, k_bias, cos_t, sin_t, pos, head_dim,
+                     num_q_heads, num_kv_heads, dtype);
+            orc_kv_update(k_pool, v_pool, row + q_dim, row + q_dim + kv_dim, v_bias, table,
+                          layer, pos, num_layers, num_kv_heads, head_dim, block_size, dtype);
+        }
+    }
+    const int group = num_q_heads / num_kv_heads;
+    const int64_t total_rows = cu_seqlens[batch];
+    const int64_t items = total_rows * num_q_heads;
+#pragma omp parallel for schedule(dynamic, 4)
+    for (int64_t it = 0; it < items; ++it) {
+        int64_t r = it / num_q_heads;
+        int h = (int)(it % num_q_heads);
+        int b = 0;
+        while (cu_seqlens[b + 1] <= r) ++b;
+        int pos = start_pos[b] + (int)(r - cu_seqlens[b]);
+        float o[ORC_MAXD];
+        attend_head(o, qkv + r * qkv_stride + (int64_t)h * head_dim, k_pool, v_pool,
+                    block_tables + (int64_t)b * table_stride, layer, ORC_MUTANT == 9 ? h % num_kv_heads : h / group, num_kv_heads,
+                    head_dim, pos, sm_scale, block_size, num_layers, dtype);
+        for (int i = 0; i < head_dim; ++i)
+            out[r * out_stride + (int64_t)h * head_dim + i] = st(o[i], dtype);
+    }
+}

@@ -1,0 +1,290 @@
+"""Independent checks that pin the oracle (oracle/luc_oracle.c).
+
+Each check computes the same quantity a different way -- f64 closed forms,
+a textbook attention in numpy float64, torch's scaled_dot_product_attention,
+or an index computed from a numpy reshape of the pool -- and returns the worst
+error relative to its tolerance (<= 1 passes).  The checks are written so a
+plausible mistake in the oracle (a dropped term, a wrong sign or index, a
+swapped operand) exceeds the tolerance; tests/test_oracle_mutants.py builds
+such mistakes into the oracle and confirms each check catches them.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+PAGE = 16
+
+
+def ulp(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Spacing of the 16-bit storage format at |x| (subnormal floor included)."""
+    mant = 10 if dtype == "f16" else 7
+    emin = -14 if dtype == "f16" else -126
+    a = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** emin)))
+    return 2.0 ** (e - mant)
+
+
+def store(x, dtype):
+    t = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32))
+    return t.to(torch.float16 if dtype == "f16" else torch.bfloat16).float().numpy()
+
+
+def bits(x, dtype):
+    t = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32))
+    return t.to(torch.float16 if dtype == "f16" else torch.bfloat16).view(
+        torch.int16).numpy().view(np.uint16)
+
+
+def f32(b, dtype):
+    t = torch.from_numpy(np.ascontiguousarray(b).view(np.int16))
+    return t.view(torch.float16 if dtype == "f16" else torch.bfloat16).float().numpy()
+
+
+# ---------------------------------------------------------------- RoPE table
+def check_rope_table(orc, max_pos=4096, head_dim=64, base=1e6, scale=None):
+    """Table vs the f64 closed form theta = (pos/scale) / base^(2i/d).
+    f32 evaluation of theta (a pow, two divides) is within a few f32 ulp of
+    the exact theta; cos/sin are then within |theta| * 2^-21 + 2^-23."""
+    cos, sin = orc.rope_table(max_pos, head_dim, base, scale)
+    pos = np.arange(max_pos, dtype=np.float64)[:, None]
+    i = np.arange(head_dim // 2, dtype=np.float64)[None, :]
+    s = scale or 1.0
+    theta = (pos / s) / np.power(float(np.float32(base)), 2 * i / head_dim)
+    tol = np.abs(theta) * 2.0 ** -21 + 2.0 ** -23
+    err = np.maximum(np.abs(cos - np.cos(theta)), np.abs(sin - np.sin(theta)))
+    return float(np.max(err / tol))
+
+
+# ---------------------------------------------------------------- RoPE apply
+def check_rope(orc, dtype, head_dim=64, hq=14, hkv=2, seed=0, with_bias=True):
+    """Apply the oracle's rope at random positions; compare with the f64
+    rotation of (x + bias) by the table's own cos/sin, rounded once."""
+    rng = np.random.default_rng(seed)
+    cos, sin = orc.rope_table(2048, head_dim, 1e6)
+    worst = 0.0
+    for pos in [0, 1, 15, 16, 17, 511, 2047] + list(rng.integers(0, 2048, 5)):
+        q = bits(rng.standard_normal((hq, head_dim)) * 0.7, dtype)
+        k = bits(rng.standard_normal((hkv, head_dim)) * 0.7, dtype)
+        qb = bits(rng.standard_normal((hq, head_dim)) * 0.3, dtype) if with_bias else None
+        kb = bits(rng.standard_normal((hkv, head_dim)) * 0.3, dtype) if with_bias else None
+        q2, k2 = q.copy(), k.copy()
+        orc.rope(q2, qb, k2, kb, cos, sin, int(pos), head_dim, hq, hkv, dtype)
+        for x, b, got in ((q, qb, q2), (k, kb, k2)):
+            xv = f32(x, dtype).astype(np.float64)
+            if b is not None:
+                xv = xv + f32(b, dtype)
+            h = head_dim // 2
+            c = cos[pos].astype(np.float64)
+            s = sin[pos].astype(np.float64)
+            want = np.concatenate([xv[:, :h] * c - xv[:, h:] * s, xv[:, :h] * s + xv[:, h:] * c],
+                                  axis=1)
+            g = f32(got, dtype).astype(np.float64)
+            # f32 products/sums then one rounding: <= 1 storage ulp (+ f32 slack)
+            tol = ulp(want, dtype) * 1.01 + np.abs(want) * 2.0 ** -22 + 1e-30
+            worst = max(worst, float(np.max(np.abs(g - want) / tol)))
+    return worst
+
+
+# ------------------------------------------------------------ cache slots
+def check_kv_update(orc, dtype, num_layers=3, hkv=2, head_dim=64, pool=20, seed=0):
+    """Write tagged tokens through orc_kv_update and read the pool back with
+    a numpy view [page][layer][head][slot][dim]: every written slot holds its
+    token (K bit-exact, V = round(v + bias)); every other slot is untouched.
+    Returns the number of wrong entries."""
+    rng = np.random.default_rng(seed)
+    table = rng.permutation(pool).astype(np.int32)[:8]  # 8 pages -> 128 positions
+    shape = (pool, num_layers, hkv, PAGE, head_dim)
+    sentinel = bits(np.full(shape, 3.0), dtype)
+    kp, vp = sentinel.copy(), sentinel.copy()
+    written = {}
+    positions = [0, 1, 14, 15, 16, 17, 31, 32, 33, 47, 48, 100, 127]
+    vb = bits(rng.standard_normal((hkv, head_dim)), dtype)
+    for layer in range(num_layers):
+        for pos in positions:
+            k = bits(rng.standard_normal((hkv, head_dim)), dtype)
+            v = bits(rng.standard_normal((hkv, head_dim)), dtype)
+            orc.kv_update(kp, vp, k, v, vb, table, layer, pos, num_layers, hkv, head_dim, PAGE,
+                          dtype)
+            written[(layer, pos)] = (k, v)
+    bad = 0
+    expect_k, expect_v = sentinel.copy(), sentinel.copy()
+    for (layer, pos), (k, v) in written.items():
+        page, slot = table[pos // PAGE], pos % PAGE
+        expect_k[page, layer, :, slot, :] = k
+        expect_v[page, layer, :, slot, :] = bits(
+            f32(v, dtype).astype(np.float64) + f32(vb, dtype), dtype)
+    bad += int(np.count_nonzero(kp != expect_k))
+    bad += int(np.count_nonzero(vp != expect_v))
+    # the closed-form slot offset agrees with the numpy view
+    for pos in positions:
+        for layer in range(num_layers):
+            for h in range(hkv):
+                off = orc.slot_offset(table, pos, layer, h, num_layers, hkv, head_dim, PAGE)
+                idx = np.ravel_multi_index((table[pos // PAGE], layer, h, pos % PAGE, 0), shape)
+                bad += int(off != idx)
+    return bad
+
+
+# ------------------------------------------------------------- attention
+def gather_kv(k_pool, v_pool, table, layer, kv_head, ctx, dtype):
+    pages = table[: (ctx + PAGE - 1) // PAGE]
+    k = f32(k_pool[pages, layer, kv_head].reshape(-1, k_pool.shape[-1])[:ctx], dtype)
+    v = f32(v_pool[pages, layer, kv_head].reshape(-1, v_pool.shape[-1])[:ctx], dtype)
+    return k.astype(np.float64), v.astype(np.float64)
+
+
+def textbook_attention(q, k, v, scale):
+    """f64 softmax(q k^T * scale) v for one head; q [d], k/v [ctx, d]."""
+    s = (k @ q) * scale
+    s = s - s.max()
+    p = np.exp(s)
+    return (p @ v) / p.sum()
+
+
+def attention_inputs(dtype, ctx, hq, hkv, head_dim, pool, seed, num_layers=1, sigma=0.5,
+                     outliers=0.0):
+    rng = np.random.default_rng(seed)
+    npages = (ctx + PAGE - 1) // PAGE
+    table = np.zeros(max(npages, 1) + 4, dtype=np.int32)
+    table[:npages] = rng.permutation(pool)[:npages]
+    shape = (pool, num_layers, hkv, PAGE, head_dim)
+    kf = rng.standard_normal(shape) * sigma
+    vf = rng.standard_normal(shape) * sigma
+    if outliers:
+        kf[rng.random(shape) < outliers] *= 8
+        vf[rng.random(shape) < outliers] *= 8
+    q = bits(rng.standard_normal((hq, head_dim)) * sigma, dtype)
+    return q, bits(kf, dtype), bits(vf, dtype), table
+
+
+def check_attention(orc, dtype, ctx, hq=14, hkv=2, head_dim=64, seed=0, layer=0, num_layers=1,
+                    outliers=0.0):
+    """Oracle flash_decoding vs f64 textbook attention on the same rounded
+    inputs.  The oracle's f32 pipeline adds a few f32 ulps of relative error
+    before the single rounding to storage, so the bound is one storage ulp of
+    the f64 value plus an f32-level slack."""
+    pool = (ctx + PAGE - 1) // PAGE + 7
+    q, kp, vp, table = attention_inputs(dtype, ctx, hq, hkv, head_dim, pool, seed, num_layers,
+                                        outliers=outliers)
+    scale = float(np.float32(1) / np.sqrt(np.float32(head_dim)))
+    got = f32(orc.flash_decoding(q, kp, vp, table, layer, hq, hkv, head_dim, ctx - 1, scale,
+                                 PAGE, num_layers, dtype), dtype)
+    worst = 0.0
+    g = hq // hkv
+    qf = f32(q, dtype).astype(np.float64)
+    for h in range(hq):
+        k, v = gather_kv(kp, vp, table, layer, h // g, ctx, dtype)
+        want = textbook_attention(qf[h], k, v, scale)
+        vmax = np.abs(v).max()
+        tol = ulp(want, dtype) * 1.01 + vmax * 2.0 ** -16
+        worst = max(worst, float(np.max(np.abs(got[h] - want) / tol)))
+    return worst
+
+
+def check_attention_sdpa(orc, dtype, ctx, hq=14, hkv=2, head_dim=64, seed=1):
+    """Oracle vs torch.nn.functional.scaled_dot_product_attention (float64,
+    CPU, GQA expanded) -- an independent library implementation."""
+    pool = (ctx + PAGE - 1) // PAGE + 3
+    q, kp, vp, table = attention_inputs(dtype, ctx, hq, hkv, head_dim, pool, seed)
+    scale = float(np.float32(1) / np.sqrt(np.float32(head_dim)))
+    got = f32(orc.flash_decoding(q, kp, vp, table, 0, hq, hkv, head_dim, ctx - 1, scale, PAGE, 1,
+                                 dtype), dtype)
+    g = hq // hkv
+    ks, vs = zip(*[gather_kv(kp, vp, table, 0, h, ctx, dtype) for h in range(hkv)])
+    K = torch.from_numpy(np.stack(ks)).repeat_interleave(g, 0)[None]
+    V = torch.from_numpy(np.stack(vs)).repeat_interleave(g, 0)[None]
+    Q = torch.from_numpy(f32(q, dtype).astype(np.float64))[None, :, None, :]
+    want = torch.nn.functional.scaled_dot_product_attention(Q, K, V, scale=scale)[0, :, 0].numpy()
+    tol = ulp(want, dtype) * 1.01 + np.abs(V.numpy()).max() * 2.0 ** -16
+    return float(np.max(np.abs(got - want) / tol))
+
+
+def check_attention_invariants(orc, dtype, head_dim=64, seed=3):
+    """Closed-form special cases:
+      ctx == 1           -> output == V[0] exactly
+      K == 0             -> output == mean(V) (to one storage ulp)
+      q == 0             -> output == mean(V)
+      pages permuted together with the table -> bit-identical output
+    Returns the number of failed cases."""
+    hq, hkv = 4, 2
+    fails = 0
+    scale = float(np.float32(1) / np.sqrt(np.float32(head_dim)))
+    q, kp, vp, table = attention_inputs(dtype, 1, hq, hkv, head_dim, 5, seed)
+    out = orc.flash_decoding(q, kp, vp, table, 0, hq, hkv, head_dim, 0, scale, PAGE, 1, dtype)
+    for h in range(hq):
+        fails += int(not np.array_equal(out[h], vp[table[0], 0, h // 2, 0]))
+    ctx = 77
+    q, kp, vp, table = attention_inputs(dtype, ctx, hq, hkv, head_dim, 12, seed + 1)
+    for mode in ("k0", "q0"):
+        kk, qq = kp.copy(), q.copy()
+        if mode == "k0":
+            kk[:] = 0
+        else:
+            qq[:] = 0
+        out = f32(orc.flash_decoding(qq, kk, vp, table, 0, hq, hkv, head_dim, ctx - 1, scale, PAGE,
+                                     1, dtype), dtype)
+        for h in range(hq):
+            _, v = gather_kv(kk, vp, table, 0, h // 2, ctx, dtype)
+            want = v.mean(axis=0)
+            tol = ulp(want, dtype) * 1.01 + 1e-7
+            fails += int(np.any(np.abs(out[h] - want) > tol))
+    # permute physical pages and remap the table
+    perm = np.random.default_rng(seed).permutation(kp.shape[0])
+    inv = np.argsort(perm)
+    kp2, vp2 = kp[perm].copy(), vp[perm].copy()   # new page j holds old page perm[j]
+    table2 = inv[table].astype(np.int32)
+    a = orc.flash_decoding(q, kp, vp, table, 0, hq, hkv, head_dim, ctx - 1, scale, PAGE, 1, dtype)
+    b = orc.flash_decoding(q, kp2, vp2, table2, 0, hq, hkv, head_dim, ctx - 1, scale, PAGE, 1,
+                           dtype)
+    fails += int(not np.array_equal(a, b))
+    return fails
+
+
+def check_prefill(orc, dtype, lens=(37, 64, 1), start=(0, 5, 130), hq=14, hkv=2, head_dim=64,
+                  seed=5):
+    """Oracle prefill vs f64 causal attention: each prompt row attends to the
+    cache prefix [0, start) (pre-filled) plus prompt rows up to itself, with
+    K roped at its position.  RoPE/cache-write are pinned separately, so the
+    expected values take the oracle's written pool as the K/V source and
+    check the causal structure and the attention itself."""
+    rng = np.random.default_rng(seed)
+    B = len(lens)
+    row = (hq + 2 * hkv) * head_dim
+    max_pages = max((s + n + PAGE - 1) // PAGE for s, n in zip(start, lens)) + 1
+    pool = B * max_pages + 2
+    perm = rng.permutation(pool).astype(np.int32)
+    tables = perm[: B * max_pages].reshape(B, max_pages).copy()
+    shape = (pool, 1, hkv, PAGE, head_dim)
+    kp = bits(rng.standard_normal(shape) * 0.5, dtype)
+    vp = bits(rng.standard_normal(shape) * 0.5, dtype)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    qkv = bits(rng.standard_normal((int(cu[-1]), row)) * 0.5, dtype)
+    cos, sin = orc.rope_table(1024, head_dim, 1e6)
+    scale = float(np.float32(1) / np.sqrt(np.float32(head_dim)))
+    qkv2, kp2, vp2 = qkv.copy(), kp.copy(), vp.copy()
+    out = f32(orc.prefill(qkv2, None, None, None, cos, sin, kp2, vp2, tables, cu,
+                          np.array(start, np.int32), 0, hq, hkv, head_dim, scale, PAGE, 1, dtype),
+              dtype)
+    worst = 0.0
+    g = hq // hkv
+    for b in range(B):
+        for t in range(lens[b]):
+            r = cu[b] + t
+            pos = start[b] + t
+            qf = f32(qkv2[r, : hq * head_dim].reshape(hq, head_dim), dtype).astype(np.float64)
+            for h in range(hq):
+                k, v = gather_kv(kp2, vp2, tables[b], 0, h // g, pos + 1, dtype)
+                want = textbook_attention(qf[h], k, v, scale)
+                tol = ulp(want, dtype) * 1.01 + np.abs(v).max() * 2.0 ** -16
+                worst = max(worst, float(np.max(np.abs(out[r, h] - want) / tol)))
+            # the prompt's own K/V landed at its position (roped k row, v row)
+            page, slot = tables[b][pos // PAGE], pos % PAGE
+            kd = hq * head_dim
+            kv_dim = hkv * head_dim
+            if not np.array_equal(kp2[page, 0, :, slot].reshape(-1), qkv2[r, kd: kd + kv_dim]):
+                worst = max(worst, 1e9)
+            if not np.array_equal(vp2[page, 0, :, slot].reshape(-1),
+                                  qkv2[r, kd + kv_dim: kd + 2 * kv_dim]):
+                worst = max(worst, 1e9)
+    return worst

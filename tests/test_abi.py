@@ -1,0 +1,118 @@
+"""The C-ABI library loads and exports every declared entry point; host-side
+argument checks reject bad calls before any GPU work (CPU only)."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+import torch
+
+from lucciola_rs_amd import library
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(luc_\w+)\s*\(", text))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "luc_paged_decode" in names and "luc_rope_append" in names
+    assert len(names) >= 10
+
+
+def test_library_exports_every_declared_symbol():
+    cdll = library.load_cdll()
+    missing = [n for n in declared_functions() if not hasattr(cdll, n)]
+    assert not missing, missing
+    # and the ctypes signature table covers them all
+    assert set(declared_functions()) <= set(library.SIGNATURES)
+
+
+def test_code_objects_built_for_gfx950():
+    for name in ("rope_append", "paged_decode"):
+        path = os.path.join(library.lib_dir(), name + ".hsaco")
+        data = open(path, "rb").read()
+        assert data[:4] == b"\x7fELF"
+        assert b"gfx950" in data
+
+
+def test_abi_version_and_error_string():
+    cdll = library.load_cdll()
+    assert cdll.luc_abi_version() == 1
+    rc = cdll.luc_paged_decode(None, None, 0, None, 0, None, 0, None, None, None, 0, None, 1,
+                               1, 0, 1, 14, 2, 64, 16, 0.125, 0, None, 0)
+    assert rc == -1
+    assert b"null context" in cdll.luc_last_error()
+
+
+class FakeCtx:
+    """Host checks run before the context is dereferenced for any GPU call;
+    a non-null dummy handle reaches them."""
+
+
+@pytest.fixture
+def cdll():
+    return library.load_cdll()
+
+
+def _decode(cdll, **kw):
+    args = dict(ctx=ctypes.c_void_p(1), stream=None, dtype=0, out=ctypes.c_void_p(16),
+                out_stride=14 * 64, q=ctypes.c_void_p(16), q_stride=14 * 64,
+                k_pool=ctypes.c_void_p(256), v_pool=ctypes.c_void_p(512),
+                tables=ctypes.c_void_p(16), table_stride=256, positions=ctypes.c_void_p(16),
+                batch=32, max_ctx=4096, layer=0, num_layers=24, hq=14, hkv=2, head_dim=64,
+                block_size=16, scale=0.125, split=0, ws=None, ws_bytes=0)
+    args.update(kw)
+    rc = cdll.luc_paged_decode(*args.values())
+    return rc, cdll.luc_last_error().decode()
+
+
+def test_decode_argument_checks(cdll):
+    assert _decode(cdll, head_dim=96)[0] == -2             # kernels.rs:37-46
+    assert _decode(cdll, block_size=32)[0] == -2           # kv_cache.rs:35
+    assert _decode(cdll, hq=18, hkv=2)[0] == -2            # group 9 > 8
+    assert _decode(cdll, hq=15, hkv=2)[0] == -1            # not a multiple
+    assert _decode(cdll, k_pool=ctypes.c_void_p(8))[0] == -1   # misaligned pool
+    assert _decode(cdll, layer=24)[0] == -1
+    assert _decode(cdll, table_stride=100)[0] == -1        # 100 pages < 4096 tokens
+    assert _decode(cdll, q_stride=100)[0] == -1
+    assert _decode(cdll, dtype=7)[0] == -1
+    assert _decode(cdll, positions=None)[0] == -1
+    assert _decode(cdll, batch=0)[0] == 0                  # empty batch: no-op
+    assert _decode(cdll, max_ctx=0)[0] == -1
+
+
+def test_workspace_size_policy(cdll):
+    ws = cdll.luc_paged_decode_workspace_size
+    # one split per sequence -> no workspace
+    assert ws(32, 14, 2, 64, 100, 0) == 0
+    # explicit split size: B*Hq*splits*(d+2)*4
+    assert ws(2, 14, 2, 64, 1000, 256) == 2 * 14 * 4 * 66 * 4
+    # rounding of the requested split to the tile (64 for d=64)
+    assert ws(2, 14, 2, 64, 1000, 250) == ws(2, 14, 2, 64, 1000, 256)
+    assert ws(1, 4, 1, 96, 1000, 0) == 0
+
+
+def test_rope_table_entry_point_matches_oracle(orc, cdll):
+    cos = torch.empty(512, 32)
+    sin = torch.empty(512, 32)
+    assert cdll.luc_rope_table(ctypes.c_void_p(cos.data_ptr()), ctypes.c_void_p(sin.data_ptr()),
+                               512, 64, 1e6, 0.0) == 0
+    oc, os_ = orc.rope_table(512, 64, 1e6)
+    assert torch.equal(cos, torch.from_numpy(oc)) and torch.equal(sin, torch.from_numpy(os_))
+    assert cdll.luc_rope_table(None, None, 512, 64, 1e6, 0.0) == -1
+
+
+def test_init_without_device_fails_cleanly(cdll):
+    if torch.cuda.is_available():
+        pytest.skip("a device is present")
+    ctx = ctypes.c_void_p()
+    rc = cdll.luc_init(0, None, ctypes.byref(ctx))
+    assert rc in (-1, -4) and not ctx.value

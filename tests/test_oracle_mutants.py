@@ -1,0 +1,56 @@
+"""Each planted oracle mistake (ORC_MUTANT=n in oracle/luc_oracle.c) must be
+rejected by at least one of the pinning checks in tests/pins.py.  This shows
+the checks pin the oracle rather than restate it."""
+import os
+import subprocess
+
+import pytest
+
+import oracle
+import pins
+
+SRC = os.path.join(os.path.dirname(oracle.__file__), "luc_oracle.c")
+
+MUTANTS = {
+    1: "score not scaled by sm_scale",
+    2: "bias added after the rotation",
+    3: "rotation sign flipped",
+    4: "slot offset: head and token strides swapped",
+    5: "partition merge without exp rescale",
+    6: "V bias dropped in the cache write",
+    7: "last context token dropped",
+    8: "scores read from the V pool",
+    9: "wrong GQA head -> kv head mapping",
+    10: "fp16 rounding truncates",
+}
+
+
+def all_checks(o):
+    """(name, passed) for every pinning check, on small inputs."""
+    res = []
+    res.append(("rope_table", pins.check_rope_table(o, max_pos=256) <= 1))
+    for dt in ("f16", "bf16"):
+        res.append((f"rope_{dt}", pins.check_rope(o, dt) <= 1))
+        res.append((f"kv_{dt}", pins.check_kv_update(o, dt) == 0))
+        res.append((f"attn_{dt}", pins.check_attention(o, dt, 100) <= 1))
+        res.append((f"sdpa_{dt}", pins.check_attention_sdpa(o, dt, 70) <= 1))
+        res.append((f"inv_{dt}", pins.check_attention_invariants(o, dt) == 0))
+    import numpy as np
+    x = np.linspace(-3, 3, 10001, dtype=np.float32)
+    res.append(("conv_f16", np.array_equal(o.to_storage(x, "f16"), pins.bits(x, "f16"))))
+    return res
+
+
+def test_unmutated_oracle_passes_all(orc):
+    failed = [n for n, ok in all_checks(orc) if not ok]
+    assert not failed, failed
+
+
+@pytest.mark.parametrize("mutant", sorted(MUTANTS))
+def test_mutant_is_caught(mutant, tmp_path):
+    so = tmp_path / f"mutant{mutant}.so"
+    subprocess.run(["gcc", "-O2", "-std=c11", "-fPIC", "-fopenmp", "-ffp-contract=off",
+                    f"-DORC_MUTANT={mutant}", "-shared", "-o", str(so), SRC, "-lm"], check=True)
+    o = oracle.Oracle(str(so))
+    failed = [n for n, ok in all_checks(o) if not ok]
+    assert failed, f"mutant {mutant} ({MUTANTS[mutant]}) passed every check"
