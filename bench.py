@@ -1,0 +1,225 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X paged decode attention path.
+
+Metric: paged decode attn -- us/step and achieved HBM GB/s (% of the 8 TB/s
+peak) at B=32, one MI355X.
+
+Workload (default `batch32_mixed`): B=32 sequences, Qwen2.5-0.5B heads
+(14 q / 2 kv, head_dim 64), fp16, contexts U{128..4096} (seeded), page size 16,
+16384-page pool handed out by a seeded shuffle, 24 layers.  A step is one
+layer's decode step for the whole batch: RoPE(q, k) + paged append of one new
+token per sequence, split-K paged attention, log-sum-exp combine.  Successive
+steps walk the 24 layers so the working set (~830 MB) does not fit the
+256 MB Infinity Cache.  Inputs are resident in HBM before timing; the K steps
+are replayed from a HIP graph, bracketed by torch.cuda.synchronize().
+
+Also reported:
+  roofline      the decode kernel alone: algorithmic bytes per launch
+                (K+V over every context token, q, output, block table) over
+                its average duration, measured with HIP events around a graph
+                of back-to-back decode launches on the launch stream;
+                `traffic` is the HBM bytes per launch read from the committed
+                rocprofv3 PMC summary, if present;
+  cpu_baseline  the oracle (C restatement of the reference's attention, OpenMP)
+                on one full layer step of the same workload on the host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_batch32_mixed_traffic.json")
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=480)
+    ap.add_argument("--warmup", type=int, default=48)
+    ap.add_argument("--layers", type=int, default=24)
+    ap.add_argument("--workload", default="batch32_mixed")
+    ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--eager", action="store_true", help="launch eagerly instead of a HIP graph")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 1 GiB device copy (reference for PMC byte counters)")
+    return ap.parse_args()
+
+
+def cpu_baseline(cfg, seed, budget_s=10.0):
+    """Time the oracle's decode step (one layer, the whole batch) on the host."""
+    import oracle
+    from lucciola_rs_amd import workloads as wl
+    from lucciola_rs_amd.engine import sm_scale
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+    h = wl.host_decode_inputs(cfg, seed, num_layers=1, poison=False)
+    orc = oracle.get()
+    cos, sin = orc.rope_table(cfg.ctx_hi + 1, cfg.head_dim, cfg.rope_theta)
+
+    def run():
+        qkv, kp, vp = h.qkv.copy(), h.k_pool.copy(), h.v_pool.copy()
+        t0 = time.perf_counter()
+        orc.decode_step(qkv, None, None, None, cos, sin, kp, vp, h.tables, h.positions, 0, cfg.hq,
+                        cfg.hkv, cfg.head_dim, sm_scale(cfg.head_dim), 16, 1, cfg.dtype,
+                        threads)
+        return time.perf_counter() - t0
+
+    run()  # warm-up
+    times, start = [], time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < 20):
+        times.append(run())
+    t = statistics.median(times)
+    return dict(t=t, threads=threads, reps=len(times), ctx=h.ctx)
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the paged decode path is a single-GPU kernel and no multi-GPU run is provided.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    from lucciola_rs_amd import workloads as wl
+    from lucciola_rs_amd.engine import RopeCache, decode_step, sm_scale
+
+    cfg = wl.CONFIGS[args.workload]
+    L = args.layers
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = pkg.library.default(0)
+    inp = wl.device_decode_inputs(cfg, args.seed, L, device=dev)
+    ctx = inp["ctx"]
+    max_ctx = int(ctx.max())
+    rope = RopeCache(max(max_ctx, 4096), cfg.head_dim, cfg.rope_theta, lib=lib, device=dev)
+    out = torch.empty((cfg.batch, cfg.hq * cfg.head_dim), dtype=cfg.torch_dtype, device=dev)
+    ws = lib.workspace(cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, max_ctx, args.split_tokens)
+    qkv, kp, vp = inp["qkv"], inp["k_pool"], inp["v_pool"]
+    tables, pos = inp["tables"], inp["positions"]
+
+    def step(i):
+        decode_step(qkv, None, None, None, rope, kp, vp, tables, pos, max_ctx, i % L, L, cfg.hq,
+                    cfg.hkv, cfg.head_dim, out, ws, args.split_tokens, lib=lib)
+
+    def decode_only(i):
+        lib.paged_decode(out, qkv, kp, vp, tables, pos, cfg.batch, max_ctx, i % L, L, cfg.hq,
+                         cfg.hkv, cfg.head_dim, sm_scale(cfg.head_dim), args.split_tokens, ws,
+                         out_row_stride=out.shape[-1], q_row_stride=cfg.row)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    def timed(fn, n):
+        """Milliseconds for n calls of fn, launched eagerly or replayed from a graph."""
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        if args.eager:
+            torch.cuda.synchronize()
+            e0.record()
+            for i in range(n):
+                fn(i)
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn(i)
+        g.replay()  # first replay uploads the graph
+        torch.cuda.synchronize()
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    # --- the K timed steps ---
+    step_ms_total = timed(step, args.steps)
+    ms_per_step = step_ms_total / args.steps
+    # --- the decode kernel alone (graph of back-to-back launches) ---
+    dec_runs = [timed(decode_only, args.steps) / args.steps for _ in range(3)]
+    dec_ms = statistics.median(dec_runs)
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
+    eb = 2
+    step_bytes = wl.decode_bytes(cfg, ctx)
+    append_bytes = cfg.batch * cfg.hkv * cfg.head_dim * 2 * eb
+    dec_bytes = step_bytes - append_bytes
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    achieved = dec_bytes / (dec_ms * 1e-3) / 1e9
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            tr = json.load(f)
+        if tr.get("workload") == args.workload and tr.get("split_tokens", 0) == args.split_tokens:
+            traffic = tr.get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline(cfg, args.seed)
+        cpu_bytes = wl.decode_bytes(cfg, cb["ctx"])
+        cpu = {"value": round(cpu_bytes / cb["t"] / 1e9, 3), "unit": "GB/s",
+               "cores": cb["threads"], "kind": "port",
+               "sample": (f"one full layer step of {cfg.name} (B={cfg.batch}, RoPE + append + "
+                          f"attention of every sequence), oracle C restatement with OpenMP, "
+                          f"median of {cb['reps']} runs, {cb['t'] * 1e3:.1f} ms/step")}
+
+    res = {
+        "metric": "paged decode attn: µs/step + achieved HBM GB/s (% peak) at B=32, 1 MI355X",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "us_per_step": round(ms_per_step * 1e3, 3),
+        "pct_of_peak_hbm": round(100 * value / PEAK_HBM_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg.dtype,
+        "data": "synthetic (seeded N(0,1)*sigma pools and queries, shuffled page allocation)",
+        "config": {"workload": cfg.name, "batch": cfg.batch, "q_heads": cfg.hq,
+                   "kv_heads": cfg.hkv, "head_dim": cfg.head_dim,
+                   "ctx": f"U{{{cfg.ctx_lo}..{cfg.ctx_hi}}}", "mean_ctx": float(np.mean(ctx)),
+                   "page_size": 16, "pool_pages": cfg.pool_pages, "layers_rotated": L,
+                   "step": "one launch: rope+append, split-K decode, combine (one layer)",
+                   "bytes_per_step": int(step_bytes),
+                   "launch": "eager" if args.eager else "hip graph",
+                   "split_tokens": args.split_tokens or "auto"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": traffic, "kernel": "luc_decode (split-K + in-kernel combine)",
+                     "us_per_launch": round(dec_ms * 1e3, 3),
+                     "algorithmic_bytes_per_launch": int(dec_bytes)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -103,10 +103,13 @@ int luc_rope_append(luc_ctx* ctx, void* stream, int dtype, void* q, const void* 
                     void* k_pool, void* v_pool, int num_tokens, int layer, int num_layers,
                     int num_q_heads, int num_kv_heads, int head_dim, int block_size);
 
-/* Bytes of f32 split-K workspace luc_paged_decode needs for these sizes (0
- * when every sequence fits one split; the workspace may then be NULL).
- * split_tokens: tokens per split-K chunk, rounded up to a multiple of 64
- * (head_dim 64) or 32 (head_dim 128); 0 = the library's choice. */
+/* Bytes of split-K workspace luc_paged_decode / luc_decode_step need for these
+ * sizes (0 when every sequence fits one split; the workspace may then be
+ * NULL).  split_tokens: tokens per split-K chunk, rounded up to a multiple of
+ * 64 (head_dim 64) or 32 (head_dim 128); 0 = the library's choice.
+ * The workspace must be 256-byte aligned and zero-filled before its first
+ * use; every launch leaves it ready for the next one.  Launches that may run
+ * concurrently (different streams) need separate workspaces. */
 size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                        int head_dim, int max_ctx, int split_tokens);
 
@@ -120,14 +123,35 @@ size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_he
  * whose context exceeds it, or is empty, gets NaN outputs, as the reference
  * yields NaN for an empty context.  sm_scale is 1/sqrt(head_dim) in the
  * engine (kernels.rs:264).  Work is split into split-K chunks whose partials
- * go to `workspace` (see luc_paged_decode_workspace_size) and are merged by a
- * log-sum-exp combine launch on the same stream. */
+ * go to `workspace` (see luc_paged_decode_workspace_size); the last chunk of
+ * each (sequence, kv head) to finish merges them with a log-sum-exp combine
+ * inside the same launch. */
 int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t out_row_stride,
                      const void* q, int64_t q_row_stride, const void* k_pool, const void* v_pool,
                      const int32_t* block_tables, int table_stride, const int32_t* positions,
                      int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
                      int num_kv_heads, int head_dim, int block_size, float sm_scale,
                      int split_tokens, void* workspace, size_t workspace_bytes);
+
+/* One whole decode step of the attention path for a batch, in one launch:
+ * per sequence b, bias + RoPE of q and k at positions[b] (in place in the qkv
+ * row), the cache write of the roped k and v + v_bias at that position, and
+ * paged attention over positions 0..positions[b] into out row b.  This is the
+ * engine's per-layer sequence apply_rope -> KVCache::update ->
+ * apply_flash_decoding (src/models.rs:505-549, src/kernels.rs:203-320,
+ * src/layers/kv_cache.rs:124-173) for a batch, with the same results as
+ * luc_rope_append followed by luc_paged_decode.
+ * qkv rows are the engine's qkv_states rows [q (Hq*d) | k (Hkv*d) | v (Hkv*d)]
+ * at qkv + b*qkv_row_stride.  Biases may be NULL.  A sequence whose context is
+ * empty or exceeds max_ctx gets NaN outputs and no cache write. */
+int luc_decode_step(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qkv_row_stride,
+                    const void* q_bias, const void* k_bias, const void* v_bias,
+                    const float* cos_table, const float* sin_table, void* k_pool, void* v_pool,
+                    const int32_t* block_tables, int table_stride, const int32_t* positions,
+                    int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
+                    int num_kv_heads, int head_dim, int block_size, float sm_scale,
+                    int split_tokens, void* out, int64_t out_row_stride, void* workspace,
+                    size_t workspace_bytes);
 
 #ifdef __cplusplus
 }

@@ -1,34 +1,46 @@
-// Split-K paged decode attention for gfx950 (HBM-bound; no MFMA).
+// Split-K paged decode attention for gfx950 (HBM-bound; no MFMA), one launch.
 //
 // Semantics: for sequence b and q-head qh, attend with q[b][qh] to positions
 // 0..positions[b] of the paged cache through table row b, scale sm_scale,
-// softmax, weighted sum of V, round to storage.  This is the single-query
-// attention of the reference's flash_decoding_impl
-// (src/kernels/attention.cu:4-176) applied to every sequence of a batch.  The
-// reference merges 32 interleaved partitions with a log-sum-exp merge
-// (attention.cu:122-175); this kernel partitions into contiguous splits
-// instead and merges with the same log-sum-exp rule.
+// softmax, weighted sum of V, round to storage -- the single-query attention
+// of the reference's flash_decoding_impl (src/kernels/attention.cu:4-176)
+// applied to every sequence of a batch.  The reference merges 32 interleaved
+// partitions with a log-sum-exp merge (attention.cu:122-175); this kernel
+// partitions each context into contiguous splits and merges them with the
+// same rule.
+//
+// With APPEND the same launch first does the engine's per-token prologue
+// (src/models.rs:505-534): q and k of the new token get bias + RoPE
+// (src/kernels/rope.cu), the roped k and v + v_bias go to the cache slot at
+// positions[b] (src/kernels/kv_cache.cu), and the roped q/k are written back
+// in place.  Attention uses the new token's K/V from LDS, so no ordering
+// against the cache write is needed.
 //
 // Work decomposition:
-//   workgroup  = (split, kv head h, sequence b); 4 waves.
-//   The G = Hq/Hkv q-heads of kv head h are processed together, so each KV
-//   page is read from HBM once per kv head (GQA grouping).
-//   A wave processes 64-token tiles (32 for head_dim 128) of its split:
-//     1. 16-byte coalesced loads: every load instruction of the wave covers
-//        1 KB of one page (pages are contiguous [16][D] slabs).
-//     2. K is staged through LDS and read back one token per lane; scores
-//        for all G heads use v_dot2_f32_{f16,bf16} with q broadcast from LDS.
-//     3. Online softmax in the exp2 domain: wave-wide max by DPP row
-//        reductions + readlane, per-lane partial sums of p.
+//   workgroup = (split, kv head h, sequence b), 4 waves.  The G = Hq/Hkv
+//   q-heads of kv head h are processed together, so each KV page is read from
+//   HBM once per kv head (GQA grouping).  A wave walks 64-token tiles (32 for
+//   head_dim 128) of its split:
+//     1. 16-byte loads; each load instruction of the wave covers 1 KB of one
+//        page (pages are contiguous [16][D] slabs).  The first tile's loads
+//        are issued before any other setup.
+//     2. K is staged through LDS and read back one token per lane; scores for
+//        all G heads use v_dot2_f32_{f16,bf16} with q broadcast from LDS.
+//     3. Online softmax in the exp2 domain: wave max by DPP row reductions +
+//        readlane, per-lane partial sums of p.
 //     4. V stays in registers in its load layout (lane = token group x 8
 //        dims); p is broadcast through LDS; f32 FMA accumulation.
-//   The 4 waves' partials (and the token groups inside each wave) are merged
-//   through LDS into one (m, l, o[D]) per q-head; with one split the kernel
-//   writes the final output, otherwise the partial goes to the workspace and
-//   luc_decode_combine_* merges the splits.
+//   The waves' partials are merged through LDS into one (m, l, o[D]) per
+//   q-head.  With one split the workgroup writes the output; otherwise it
+//   writes its partial to the workspace and takes a ticket, and the last
+//   workgroup of (b, h) merges all splits, writes the output and resets the
+//   ticket counter to zero for the next launch.
+#include "decode_args.h"
 #include "luc_common.h"
 
 namespace luc {
+
+using DecodeArgs = ::luc_decode_args;
 
 template <int D>
 struct DecodeShape {
@@ -43,42 +55,117 @@ struct DecodeShape {
   static constexpr int STAGE = TILE * KROW + TILE * 32;  // per-wave LDS: K tile + p tile
 };
 
-template <int DT, int D, int G>
-__device__ void decode_impl(const uint16_t* __restrict__ q, int64_t q_stride,
-                            const uint16_t* __restrict__ k_pool,
-                            const uint16_t* __restrict__ v_pool, const int* __restrict__ tables,
-                            int table_stride, const int* __restrict__ positions, int layer,
-                            int num_layers, int hkv, float qk_scale_log2, int max_ctx,
-                            int split_tokens, int max_splits, float* __restrict__ ws_ml,
-                            float* __restrict__ ws_o, uint16_t* __restrict__ out,
-                            int64_t out_stride) {
+template <int DT>
+__device__ inline void rot_pair(const uint16_t* x, const uint16_t* bias, int i1, int i2, float c,
+                                float s, uint16_t& o1, uint16_t& o2) {
+#pragma clang fp contract(off)
+  const float v1 = St<DT>::load(x[i1]) + (bias ? St<DT>::load(bias[i1]) : 0.0f);
+  const float v2 = St<DT>::load(x[i2]) + (bias ? St<DT>::load(bias[i2]) : 0.0f);
+  const float a = v1 * c, bb = v2 * s, e = v1 * s, f = v2 * c;
+  o1 = St<DT>::store(a - bb);
+  o2 = St<DT>::store(e + f);
+}
+
+template <int DT, int D, int G, bool APPEND>
+__device__ void decode_impl(const DecodeArgs& A) {
   using S = DecodeShape<D>;
+  constexpr int NT = S::NW * 64;
   constexpr int MERGE = S::NW * S::GROUPS * G * D * 4;
   constexpr int BIG = (S::NW * S::STAGE > MERGE) ? S::NW * S::STAGE : MERGE;
   __shared__ __attribute__((aligned(16))) char smem[BIG];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[G * D];
+  __shared__ __attribute__((aligned(16))) uint16_t s_knew[D];
+  __shared__ __attribute__((aligned(16))) uint16_t s_vnew[D];
   __shared__ float s_m[S::NW][8];
   __shared__ float s_l[S::NW][8];
+  __shared__ int s_ticket;
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int ctx = positions[b] + 1;
-  const int s_begin = split * split_tokens;
-  // Nothing to do past the context; a context beyond the host bound max_ctx
-  // (which the table row is sized for) is left to the combine, which flags it.
-  if (s_begin >= ctx || ctx > max_ctx) return;  // uniform over the workgroup
-  const int s_end = min(ctx, s_begin + split_tokens);
-  const int nsplit = (ctx + split_tokens - 1) / split_tokens;
-  const int* table = tables + (int64_t)b * table_stride;
-  const int64_t page_stride = (int64_t)num_layers * hkv * kPage * D;
-  const int64_t head_off = ((int64_t)layer * hkv + h) * kPage * D;
+  const int hq = A.hkv * G;
+  const int pos = A.positions[b];
+  const int ctx = pos + 1;
+  uint16_t* out_row = A.out + (int64_t)b * A.out_stride + (int64_t)h * G * D;
+  if (ctx <= 0 || ctx > A.max_ctx) {
+    // empty context (0/0 in the reference) or beyond the host bound: NaN
+    if (split == 0)
+      for (int i = threadIdx.x; i < G * D; i += NT) out_row[i] = St<DT>::store(__builtin_nanf(""));
+    return;
+  }
+  const int s_begin = split * A.split_tokens;
+  if (s_begin >= ctx) return;  // uniform over the workgroup
+  const int s_end = min(ctx, s_begin + A.split_tokens);
+  const int nsplit = (ctx + A.split_tokens - 1) / A.split_tokens;
+  const int* table = A.tables + (int64_t)b * A.table_stride;
+  const int64_t page_stride = (int64_t)A.num_layers * A.hkv * kPage * D;
+  const int64_t head_off = ((int64_t)A.layer * A.hkv + h) * kPage * D;
+  const bool owns_pos = APPEND && pos >= s_begin && pos < s_end;
 
-  {  // q rows of the G heads of this kv head -> LDS
-    const uint32_t* src = (const uint32_t*)(q + (int64_t)b * q_stride + (int64_t)h * G * D);
-    for (int i = threadIdx.x; i < G * D / 2; i += S::NW * 64) ((uint32_t*)s_q)[i] = src[i];
+  const int tq = lane % S::TILE;          // QK: token of this lane
+  const int qhalf = lane / S::TILE;       // QK: which 64 dims (head_dim 128)
+  const int pv_tok = lane / S::CH;        // load layout: token within a load group
+  const int pv_chunk = lane % S::CH;      // load layout: 16-byte chunk of the row
+
+  uint4 kr[S::LOADS], vr[S::LOADS];
+  auto load_tile = [&](int t0) {
+#pragma unroll
+    for (int r = 0; r < S::LOADS; ++r) {
+      const int page_tok = t0 + (r / S::LPP) * kPage;
+      if (page_tok < s_end) {
+        const int64_t phys = table[page_tok / kPage];
+        const int64_t off = phys * page_stride + head_off + (int64_t)((r % S::LPP) * 64 + lane) * 8;
+        kr[r] = *(const uint4*)(A.k_pool + off);
+        vr[r] = *(const uint4*)(A.v_pool + off);
+      } else {
+        kr[r] = make_uint4(0, 0, 0, 0);
+        vr[r] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+
+  // ---- 1. the first tile's loads go out before anything else ----
+  const int t_first = s_begin + w * S::TILE;
+  if (t_first < s_end) load_tile(t_first);
+
+  // ---- 2. q for the G heads (roped with APPEND) and the new token's k, v ----
+  const uint16_t* qrow = A.q + (int64_t)b * A.q_stride + (int64_t)h * G * D;
+  if constexpr (APPEND) {
+    constexpr int HALF = D / 2;
+    const float* crow = A.cos_t + (int64_t)pos * HALF;
+    const float* srow = A.sin_t + (int64_t)pos * HALF;
+    const uint16_t* qb = A.q_bias ? A.q_bias + (int64_t)h * G * D : nullptr;
+    const uint16_t* krow = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
+    const uint16_t* kb = A.k_bias ? A.k_bias + (int64_t)h * D : nullptr;
+    for (int idx = threadIdx.x; idx < (G + 1) * HALF; idx += NT) {
+      const int g = idx / HALF, i = idx % HALF;
+      uint16_t o1, o2;
+      if (g < G) {
+        rot_pair<DT>(qrow, qb, g * D + i, g * D + i + HALF, crow[i], srow[i], o1, o2);
+        s_q[g * D + i] = o1;
+        s_q[g * D + i + HALF] = o2;
+      } else {
+        rot_pair<DT>(krow, kb, i, i + HALF, crow[i], srow[i], o1, o2);
+        s_knew[i] = o1;
+        s_knew[i + HALF] = o2;
+      }
+    }
+    if (threadIdx.x < D) {
+      const int64_t vi = (int64_t)b * A.q_stride + (int64_t)h * D + threadIdx.x;
+      const float vb = A.v_bias ? St<DT>::load(A.v_bias[(int64_t)h * D + threadIdx.x]) : 0.0f;
+      s_vnew[threadIdx.x] = St<DT>::store(St<DT>::load(A.v_new[vi]) + vb);
+    }
+  } else {
+    const uint32_t* src = (const uint32_t*)qrow;
+    for (int i = threadIdx.x; i < G * D / 2; i += NT) ((uint32_t*)s_q)[i] = src[i];
   }
   __syncthreads();
+  if (owns_pos && threadIdx.x < D) {  // the cache write of the new token
+    const int64_t slot = (int64_t)table[pos / kPage] * page_stride + head_off +
+                         (int64_t)(pos % kPage) * D + threadIdx.x;
+    A.k_pool[slot] = s_knew[threadIdx.x];
+    A.v_pool[slot] = s_vnew[threadIdx.x];
+  }
 
   char* s_k = smem + w * S::STAGE;
   float* s_p = (float*)(s_k + S::TILE * S::KROW);
@@ -92,30 +179,18 @@ __device__ void decode_impl(const uint16_t* __restrict__ q, int64_t q_stride,
     for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
   }
 
-  const int tq = lane % S::TILE;          // QK: token of this lane
-  const int qhalf = lane / S::TILE;       // QK: which 64 dims (head_dim 128)
-  const int pv_tok = lane / S::CH;        // load layout: token within a load group
-  const int pv_chunk = lane % S::CH;      // load layout: 16-byte chunk of the row
-
-  for (int t0 = s_begin + w * S::TILE; t0 < s_end; t0 += S::NW * S::TILE) {
-    uint4 kr[S::LOADS], vr[S::LOADS];
-#pragma unroll
-    for (int r = 0; r < S::LOADS; ++r) {
-      const int page_tok = t0 + (r / S::LPP) * kPage;
-      if (page_tok < s_end) {
-        const int64_t phys = table[page_tok / kPage];
-        const int64_t off = phys * page_stride + head_off + (int64_t)((r % S::LPP) * 64 + lane) * 8;
-        kr[r] = *(const uint4*)(k_pool + off);
-        vr[r] = *(const uint4*)(v_pool + off);
-      } else {
-        kr[r] = make_uint4(0, 0, 0, 0);
-        vr[r] = make_uint4(0, 0, 0, 0);
-      }
-    }
+  for (int t0 = t_first; t0 < s_end; t0 += S::NW * S::TILE) {
+    if (t0 != t_first) load_tile(t0);
+    const bool sub = owns_pos && pos >= t0 && pos < t0 + S::TILE;  // tile holds the new token
 #pragma unroll
     for (int r = 0; r < S::LOADS; ++r) {
       const int tok = r * S::GROUPS + pv_tok;
-      *(uint4*)(s_k + tok * S::KROW + pv_chunk * 16) = kr[r];
+      uint4 kv = kr[r];
+      if (sub && t0 + tok == pos) {
+        kv = *(const uint4*)(s_knew + pv_chunk * 8);
+        vr[r] = *(const uint4*)(s_vnew + pv_chunk * 8);
+      }
+      *(uint4*)(s_k + tok * S::KROW + pv_chunk * 16) = kv;
       // tokens past the split: V must contribute exactly zero (p is 0 there,
       // and 0 * stale data must not produce NaN)
       if (t0 + tok >= s_end) vr[r] = make_uint4(0, 0, 0, 0);
@@ -156,7 +231,7 @@ __device__ void decode_impl(const uint16_t* __restrict__ q, int64_t q_stride,
     float p[8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float s = valid ? acc[g] * qk_scale_log2 : -INFINITY;
+      const float s = valid ? acc[g] * A.qk_scale_log2 : -INFINITY;
       const float mn = fmaxf(m_run[g], wave_max(s));
       const float alpha = __builtin_amdgcn_exp2f(m_run[g] - mn);
       p[g] = __builtin_amdgcn_exp2f(s - mn);
@@ -218,8 +293,9 @@ __device__ void decode_impl(const uint16_t* __restrict__ q, int64_t q_stride,
   }
   __syncthreads();
 
-  const int hq = hkv * G;
-  for (int idx = threadIdx.x; idx < G * D; idx += S::NW * 64) {
+  // workspace slots of (b, q-head h*G + g, split)
+  const int64_t ws_base = ((int64_t)b * hq + (int64_t)h * G) * A.max_splits;
+  for (int idx = threadIdx.x; idx < G * D; idx += NT) {
     const int g = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
@@ -234,69 +310,65 @@ __device__ void decode_impl(const uint16_t* __restrict__ q, int64_t q_stride,
       L = fmaf(sc, s_l[w2][g], L);
       acc = fmaf(sc, part, acc);
     }
-    const int qhead = h * G + g;
     if (nsplit == 1) {
-      out[(int64_t)b * out_stride + (int64_t)qhead * D + d] = St<DT>::store(acc / L);
+      out_row[idx] = St<DT>::store(acc / L);
     } else {
-      const int64_t ws = ((int64_t)b * hq + qhead) * max_splits + split;
-      ws_o[ws * D + d] = acc;
+      const int64_t ws = ws_base + (int64_t)g * A.max_splits + split;
+      A.ws_o[ws * D + d] = acc;
       if (d == 0) {
-        ws_ml[ws * 2] = M;
-        ws_ml[ws * 2 + 1] = L;
+        A.ws_ml[ws * 2] = M;
+        A.ws_ml[ws * 2 + 1] = L;
       }
     }
   }
-}
 
-// Log-sum-exp merge of the split partials of one (sequence, q-head); one
-// thread per output dim.  Sequences with a single split were finished by the
-// decode kernel.  Empty contexts and contexts beyond max_ctx get NaN (an
-// empty softmax is 0/0, as in the reference).
-template <int DT, int D>
-__device__ void combine_impl(const float* __restrict__ ws_ml, const float* __restrict__ ws_o,
-                             const int* __restrict__ positions, int hq, int max_ctx,
-                             int split_tokens, int max_splits, uint16_t* __restrict__ out,
-                             int64_t out_stride) {
-  const int qhead = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int ctx = positions[b] + 1;
-  const int nsplit = ctx > 0 ? (ctx + split_tokens - 1) / split_tokens : 0;
-  if (nsplit == 1 && ctx <= max_ctx) return;
-  uint16_t* dst = out + (int64_t)b * out_stride + (int64_t)qhead * D + d;
-  if (nsplit == 0 || ctx > max_ctx) {
-    *dst = St<DT>::store(__builtin_nanf(""));
-    return;
+  bool last = nsplit == 1;
+  if (nsplit > 1) {
+    // publish the partial; the last workgroup of (b, h) merges all splits
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_ticket = __hip_atomic_fetch_add(A.counters + (int64_t)b * A.hkv + h, 1, __ATOMIC_ACQ_REL,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    last = s_ticket == nsplit - 1;
+    if (!last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    for (int idx = threadIdx.x; idx < G * D; idx += NT) {
+      const int g = idx / D, d = idx % D;
+      const int64_t base = ws_base + (int64_t)g * A.max_splits;
+      float M = -INFINITY;
+      for (int s = 0; s < nsplit; ++s) M = fmaxf(M, A.ws_ml[(base + s) * 2]);
+      float L = 0.0f, acc = 0.0f;
+      for (int s = 0; s < nsplit; ++s) {
+        const float sc = __builtin_amdgcn_exp2f(A.ws_ml[(base + s) * 2] - M);
+        L = fmaf(sc, A.ws_ml[(base + s) * 2 + 1], L);
+        acc = fmaf(sc, A.ws_o[(base + s) * D + d], acc);
+      }
+      out_row[idx] = St<DT>::store(acc / L);
+    }
+    if (threadIdx.x == 0) A.counters[(int64_t)b * A.hkv + h] = 0;  // ready for the next launch
   }
-  const int64_t base = ((int64_t)b * hq + qhead) * max_splits;
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ws_ml[(base + s) * 2]);
-  float L = 0.0f, acc = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float sc = __builtin_amdgcn_exp2f(ws_ml[(base + s) * 2] - M);
-    L = fmaf(sc, ws_ml[(base + s) * 2 + 1], L);
-    acc = fmaf(sc, ws_o[(base + s) * D + d], acc);
+  if constexpr (APPEND) {
+    // every split of (b, h) has read q and k by now: write the roped values back
+    if (last) {
+      uint16_t* qdst = A.q + (int64_t)b * A.q_stride + (int64_t)h * G * D;
+      for (int i = threadIdx.x; i < G * D; i += NT) qdst[i] = s_q[i];
+      if (threadIdx.x < D)
+        A.k_new[(int64_t)b * A.q_stride + (int64_t)h * D + threadIdx.x] = s_knew[threadIdx.x];
+    }
   }
-  *dst = St<DT>::store(acc / L);
 }
 
 }  // namespace luc
 
 #define LUC_DECODE(DTN, DT, D, G)                                                                  \
-  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void luc_decode_##DTN##_d##D##_g##G(                \
-      const uint16_t* q, int64_t q_stride, const uint16_t* k_pool, const uint16_t* v_pool,         \
-      const int* tables, int table_stride, const int* positions, int layer, int num_layers,        \
-      int hkv, float qk_scale_log2, int max_ctx, int split_tokens, int max_splits, float* ws_ml,   \
-      float* ws_o, uint16_t* out, int64_t out_stride) {                                            \
-    luc::decode_impl<DT, D, G>(q, q_stride, k_pool, v_pool, tables, table_stride, positions,       \
-                               layer, num_layers, hkv, qk_scale_log2, max_ctx, split_tokens,       \
-                               max_splits, ws_ml, ws_o, out, out_stride);                          \
-  }
-
-#define LUC_COMBINE(DTN, DT, D)                                                                    \
-  extern "C" __global__ __launch_bounds__(128) void luc_decode_combine_##DTN##_d##D(               \
-      const float* ws_ml, const float* ws_o, const int* positions, int hq, int max_ctx,            \
-      int split_tokens, int max_splits, uint16_t* out, int64_t out_stride) {                       \
-    luc::combine_impl<DT, D>(ws_ml, ws_o, positions, hq, max_ctx, split_tokens, max_splits, out,   \
-                             out_stride);                                                          \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void     \
+      luc_decode_##DTN##_d##D##_g##G(luc::DecodeArgs a) {                                          \
+    luc::decode_impl<DT, D, G, false>(a);                                                          \
+  }                                                                                                \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void     \
+      luc_decode_step_##DTN##_d##D##_g##G(luc::DecodeArgs a) {                                     \
+    luc::decode_impl<DT, D, G, true>(a);                                                           \
   }
 
 #define LUC_DECODE_GROUPS(DTN, DT, D)                                                              \
@@ -307,8 +379,7 @@ __device__ void combine_impl(const float* __restrict__ ws_ml, const float* __res
   LUC_DECODE(DTN, DT, D, 5)                                                                        \
   LUC_DECODE(DTN, DT, D, 6)                                                                        \
   LUC_DECODE(DTN, DT, D, 7)                                                                        \
-  LUC_DECODE(DTN, DT, D, 8)                                                                        \
-  LUC_COMBINE(DTN, DT, D)
+  LUC_DECODE(DTN, DT, D, 8)
 
 LUC_DECODE_GROUPS(bf16, luc::kBF16, 64)
 LUC_DECODE_GROUPS(bf16, luc::kBF16, 128)

@@ -11,6 +11,7 @@
 // several threads, each with its own stream.  Nothing here allocates device
 // memory or synchronises.
 #include "luc_attn.h"
+#include "kernels/decode_args.h"
 
 #include <hip/hip_runtime_api.h>
 
@@ -179,10 +180,92 @@ int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requeste
   return (int)(tpw * wg_tokens);
 }
 
-size_t workspace_bytes_for(int batch, int hq, int head_dim, int max_ctx, int split_tokens) {
+// Workspace layout: [split tickets: batch*Hkv int32, padded to 256 B]
+// [(max, sum) per (b, q-head, split): f32 x2] [o per (b, q-head, split): f32 x head_dim]
+size_t counters_bytes(int batch, int hkv) {
+  return (size_t)ceil_div((int64_t)batch * hkv * 4, 256) * 256;
+}
+
+size_t workspace_bytes_for(int batch, int hq, int hkv, int head_dim, int max_ctx,
+                           int split_tokens) {
   const int64_t max_splits = ceil_div(max_ctx, split_tokens);
   if (max_splits <= 1) return 0;
-  return (size_t)batch * hq * max_splits * (head_dim + 2) * sizeof(float);
+  return counters_bytes(batch, hkv) +
+         (size_t)batch * hq * max_splits * (head_dim + 2) * sizeof(float);
+}
+
+struct DecodeLaunch {
+  luc_decode_args a{};
+  hipFunction_t fn = nullptr;
+  dim3 grid;
+};
+
+// Shared argument checks and argument block of the two decode entry points.
+int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t out_row_stride,
+                   const void* q, int64_t q_row_stride, const void* k_pool, const void* v_pool,
+                   const int32_t* block_tables, int table_stride, const int32_t* positions,
+                   int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
+                   int num_kv_heads, int head_dim, int block_size, float sm_scale,
+                   int split_tokens, void* workspace, size_t workspace_bytes, DecodeLaunch* L) {
+  if (int rc = check_common(ctx, dtype, head_dim)) return rc;
+  if (int rc = check_heads(num_q_heads, num_kv_heads)) return rc;
+  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers, block_size))
+    return rc;
+  if (batch < 0) return fail(LUC_E_INVALID, "batch %d < 0", batch);
+  if (max_ctx <= 0) return fail(LUC_E_INVALID, "max_ctx %d <= 0", max_ctx);
+  if (split_tokens < 0) return fail(LUC_E_INVALID, "split_tokens %d < 0", split_tokens);
+  if (!out || !q || !positions) return fail(LUC_E_INVALID, "null out, q or positions");
+  const int row = num_q_heads * head_dim;
+  const int need_q = step ? (num_q_heads + 2 * num_kv_heads) * head_dim : row;
+  if (q_row_stride < need_q || out_row_stride < row)
+    return fail(LUC_E_INVALID, "q/out row stride smaller than a row (%d / %d)", need_q, row);
+  if (!aligned(q, 4) || (q_row_stride % 2))
+    return fail(LUC_E_INVALID, "q must be 4-byte aligned with an even row stride");
+  if ((int64_t)table_stride * LUC_BLOCK_SIZE < max_ctx)
+    return fail(LUC_E_INVALID, "table_stride %d pages cannot hold max_ctx %d", table_stride, max_ctx);
+
+  const int st = split_tokens_for(batch, num_kv_heads, head_dim, max_ctx, split_tokens);
+  const int max_splits = (int)ceil_div(max_ctx, st);
+  const size_t need = workspace_bytes_for(batch, num_q_heads, num_kv_heads, head_dim, max_ctx, st);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(LUC_E_WORKSPACE, "workspace %zu bytes, %zu needed", workspace_bytes, need);
+  if (need && !aligned(workspace, 256)) return fail(LUC_E_INVALID, "workspace must be 256-byte aligned");
+
+  if (batch == 0) return LUC_OK;  // nothing to launch
+  const int group = num_q_heads / num_kv_heads;
+  const std::string name = std::string(step ? "luc_decode_step_" : "luc_decode_") + dt_name(dtype) +
+                           "_d" + std::to_string(head_dim) + "_g" + std::to_string(group);
+  if (int rc = get_fn(ctx, name, &L->fn)) return rc;
+  luc_decode_args& a = L->a;
+  a.q = static_cast<uint16_t*>(const_cast<void*>(q));
+  a.q_stride = q_row_stride;
+  a.k_pool = static_cast<uint16_t*>(const_cast<void*>(k_pool));
+  a.v_pool = static_cast<uint16_t*>(const_cast<void*>(v_pool));
+  a.tables = block_tables;
+  a.table_stride = table_stride;
+  a.positions = positions;
+  a.layer = layer;
+  a.num_layers = num_layers;
+  a.hkv = num_kv_heads;
+  a.qk_scale_log2 = sm_scale * 1.4426950408889634f;
+  a.max_ctx = max_ctx;
+  a.split_tokens = st;
+  a.max_splits = max_splits;
+  if (need) {
+    char* ws = static_cast<char*>(workspace);
+    a.counters = reinterpret_cast<int32_t*>(ws);
+    a.ws_ml = reinterpret_cast<float*>(ws + counters_bytes(batch, num_kv_heads));
+    a.ws_o = a.ws_ml + (size_t)batch * num_q_heads * max_splits * 2;
+  }
+  a.out = static_cast<uint16_t*>(out);
+  a.out_stride = out_row_stride;
+  L->grid = dim3(max_splits, num_kv_heads, batch);
+  return LUC_OK;
+}
+
+int launch_decode(DecodeLaunch& L, void* stream) {
+  void* args[] = {&L.a};
+  return launch(L.fn, L.grid, dim3(kDecodeWaves * 64), stream, args);
 }
 
 }  // namespace
@@ -217,12 +300,11 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
   std::vector<std::string> names;
   for (const char* dt : {"bf16", "f16"}) {
     names.push_back(std::string("luc_rope_append_") + dt);
-    for (int d : {64, 128}) {
+    for (int d : {64, 128})
       for (int g = 1; g <= 8; ++g)
-        names.push_back(std::string("luc_decode_") + dt + "_d" + std::to_string(d) + "_g" +
-                        std::to_string(g));
-      names.push_back(std::string("luc_decode_combine_") + dt + "_d" + std::to_string(d));
-    }
+        for (const char* kind : {"luc_decode_", "luc_decode_step_"})
+          names.push_back(std::string(kind) + dt + "_d" + std::to_string(d) + "_g" +
+                          std::to_string(g));
   }
   for (const auto& n : names) {
     hipFunction_t fn = nullptr;
@@ -334,7 +416,7 @@ size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_he
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_ctx <= 0) return 0;
   if (head_dim != 64 && head_dim != 128) return 0;
   const int st = split_tokens_for(batch, num_kv_heads, head_dim, max_ctx, split_tokens);
-  return workspace_bytes_for(batch, num_q_heads, head_dim, max_ctx, st);
+  return workspace_bytes_for(batch, num_q_heads, num_kv_heads, head_dim, max_ctx, st);
 }
 
 int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t out_row_stride,
@@ -343,51 +425,43 @@ int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t o
                      int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
                      int num_kv_heads, int head_dim, int block_size, float sm_scale,
                      int split_tokens, void* workspace, size_t workspace_bytes) {
-  if (int rc = check_common(ctx, dtype, head_dim)) return rc;
-  if (int rc = check_heads(num_q_heads, num_kv_heads)) return rc;
-  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers, block_size))
+  DecodeLaunch L;
+  if (int rc = prepare_decode(ctx, dtype, false, out, out_row_stride, q, q_row_stride, k_pool,
+                              v_pool, block_tables, table_stride, positions, batch, max_ctx, layer,
+                              num_layers, num_q_heads, num_kv_heads, head_dim, block_size, sm_scale,
+                              split_tokens, workspace, workspace_bytes, &L))
     return rc;
-  if (batch < 0) return fail(LUC_E_INVALID, "batch %d < 0", batch);
   if (batch == 0) return LUC_OK;
-  if (max_ctx <= 0) return fail(LUC_E_INVALID, "max_ctx %d <= 0", max_ctx);
-  if (split_tokens < 0) return fail(LUC_E_INVALID, "split_tokens %d < 0", split_tokens);
-  if (!out || !q || !positions) return fail(LUC_E_INVALID, "null out, q or positions");
-  const int row = num_q_heads * head_dim;
-  if (q_row_stride < row || out_row_stride < row)
-    return fail(LUC_E_INVALID, "q/out row stride smaller than Hq*head_dim (%d)", row);
-  if (!aligned(q, 4) || (q_row_stride % 2))
-    return fail(LUC_E_INVALID, "q must be 4-byte aligned with an even row stride");
-  if ((int64_t)table_stride * LUC_BLOCK_SIZE < max_ctx)
-    return fail(LUC_E_INVALID, "table_stride %d pages cannot hold max_ctx %d", table_stride, max_ctx);
   if (int rc = check_device(ctx)) return rc;
+  return launch_decode(L, stream);
+}
 
-  const int st = split_tokens_for(batch, num_kv_heads, head_dim, max_ctx, split_tokens);
-  const int max_splits = (int)ceil_div(max_ctx, st);
-  const size_t need = workspace_bytes_for(batch, num_q_heads, head_dim, max_ctx, st);
-  if (need && (!workspace || workspace_bytes < need))
-    return fail(LUC_E_WORKSPACE, "workspace %zu bytes, %zu needed", workspace_bytes, need);
-  if (need && !aligned(workspace, 16)) return fail(LUC_E_INVALID, "workspace must be 16-byte aligned");
-
-  const int group = num_q_heads / num_kv_heads;
-  hipFunction_t fdec, fcomb;
-  const std::string dsuffix = std::string(dt_name(dtype)) + "_d" + std::to_string(head_dim);
-  if (int rc = get_fn(ctx, "luc_decode_" + dsuffix + "_g" + std::to_string(group), &fdec)) return rc;
-  if (int rc = get_fn(ctx, "luc_decode_combine_" + dsuffix, &fcomb)) return rc;
-
-  float* ws_ml = static_cast<float*>(workspace);
-  float* ws_o = need ? ws_ml + (size_t)batch * num_q_heads * max_splits * 2 : nullptr;
-  float qk_scale_log2 = sm_scale * 1.4426950408889634f;
-  int hkv = num_kv_heads, hq = num_q_heads;
-  void* args[] = {const_cast<void**>(&q), &q_row_stride, const_cast<void**>(&k_pool),
-                  const_cast<void**>(&v_pool), const_cast<int32_t**>(&block_tables),
-                  &table_stride, const_cast<int32_t**>(&positions), &layer, &num_layers, &hkv,
-                  &qk_scale_log2, &max_ctx, const_cast<int*>(&st), const_cast<int*>(&max_splits),
-                  &ws_ml, &ws_o, &out, &out_row_stride};
-  if (int rc = launch(fdec, dim3(max_splits, num_kv_heads, batch), dim3(kDecodeWaves * 64), stream, args))
+int luc_decode_step(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qkv_row_stride,
+                    const void* q_bias, const void* k_bias, const void* v_bias,
+                    const float* cos_table, const float* sin_table, void* k_pool, void* v_pool,
+                    const int32_t* block_tables, int table_stride, const int32_t* positions,
+                    int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
+                    int num_kv_heads, int head_dim, int block_size, float sm_scale,
+                    int split_tokens, void* out, int64_t out_row_stride, void* workspace,
+                    size_t workspace_bytes) {
+  if (!cos_table || !sin_table) return fail(LUC_E_INVALID, "null rope table");
+  DecodeLaunch L;
+  if (int rc = prepare_decode(ctx, dtype, true, out, out_row_stride, qkv, qkv_row_stride, k_pool,
+                              v_pool, block_tables, table_stride, positions, batch, max_ctx, layer,
+                              num_layers, num_q_heads, num_kv_heads, head_dim, block_size, sm_scale,
+                              split_tokens, workspace, workspace_bytes, &L))
     return rc;
-  void* cargs[] = {&ws_ml, &ws_o, const_cast<int32_t**>(&positions), &hq, &max_ctx,
-                   const_cast<int*>(&st), const_cast<int*>(&max_splits), &out, &out_row_stride};
-  return launch(fcomb, dim3(num_q_heads, batch), dim3(head_dim), stream, cargs);
+  if (batch == 0) return LUC_OK;
+  if (int rc = check_device(ctx)) return rc;
+  uint16_t* base = static_cast<uint16_t*>(qkv);
+  L.a.q_bias = static_cast<const uint16_t*>(q_bias);
+  L.a.k_new = base + (int64_t)num_q_heads * head_dim;
+  L.a.k_bias = static_cast<const uint16_t*>(k_bias);
+  L.a.v_new = base + (int64_t)(num_q_heads + num_kv_heads) * head_dim;
+  L.a.v_bias = static_cast<const uint16_t*>(v_bias);
+  L.a.cos_t = cos_table;
+  L.a.sin_t = sin_table;
+  return launch_decode(L, stream);
 }
 
 }  // extern "C"

@@ -90,11 +90,12 @@ class KVCache:
                                  self.block_size, stream)
 
     def workspace(self, num_q_heads, max_ctx):
+        """Zero-filled split-K workspace for one sequence, grown on demand."""
         need = self.lib.workspace_size(1, num_q_heads, self.num_kv_heads, self.head_dim, max_ctx)
         if need == 0:
             return None
         if self._workspace is None or self._workspace.numel() * 4 < need:
-            self._workspace = torch.empty(need // 4, dtype=torch.float32,
+            self._workspace = torch.zeros(need // 4, dtype=torch.float32,
                                           device=self.k_pool.device)
         return self._workspace
 
@@ -125,23 +126,34 @@ def apply_flash_decoding(output, out_offset, q, q_offset, cache, layer_idx, pos,
 def decode_step(qkv, q_bias, k_bias, v_bias, rope, k_pool, v_pool, block_tables, positions,
                 max_ctx, layer, num_layers, num_q_heads, num_kv_heads, head_dim, out,
                 workspace=None, split_tokens=0, lib=None, stream=None):
-    """One batched decode step of the attention path for one layer: RoPE(q, k)
-    and cache append for one new token per sequence, then paged attention.
+    """One batched decode step of the attention path for one layer, in one
+    launch (luc_decode_step): RoPE(q, k) and cache append of one new token per
+    sequence, then paged attention.
 
     qkv: [B, (Hq + 2*Hkv)*head_dim], rows as the engine's qkv_states
     (src/models.rs:467-503); out: [B, Hq*head_dim]; positions: int32 [B] on
-    the device (position of the new token); block_tables: int32 [B, pages]."""
+    the device (position of the new token); block_tables: int32 [B, pages];
+    workspace: from LucAttn.workspace (zero-filled once, reusable)."""
+    lib = _lib(lib)
+    batch, row = qkv.shape
+    lib.decode_step(qkv, q_bias, k_bias, v_bias, rope.cos, rope.sin, k_pool, v_pool, block_tables,
+                    positions, batch, max_ctx, layer, num_layers, num_q_heads, num_kv_heads,
+                    head_dim, sm_scale(head_dim), out, workspace, split_tokens,
+                    qkv_row_stride=row, out_row_stride=out.shape[-1], stream=stream)
+
+
+def decode_step_unfused(qkv, q_bias, k_bias, v_bias, rope, k_pool, v_pool, block_tables,
+                        positions, max_ctx, layer, num_layers, num_q_heads, num_kv_heads,
+                        head_dim, out, workspace=None, split_tokens=0, lib=None, stream=None):
+    """The same step as two launches: luc_rope_append, then luc_paged_decode."""
     lib = _lib(lib)
     batch, row = qkv.shape
     qd = num_q_heads * head_dim
     kd = num_kv_heads * head_dim
-    q = qkv
-    k = qkv[:, qd:]
-    v = qkv[:, qd + kd:]
-    lib.rope_append(q, q_bias, k, k_bias, v, v_bias, row, rope.cos, rope.sin, positions,
-                    block_tables, k_pool, v_pool, batch, layer, num_layers, num_q_heads,
-                    num_kv_heads, head_dim, stream=stream)
-    lib.paged_decode(out, q, k_pool, v_pool, block_tables, positions, batch, max_ctx, layer,
+    lib.rope_append(qkv, q_bias, qkv[:, qd:], k_bias, qkv[:, qd + kd:], v_bias, row, rope.cos,
+                    rope.sin, positions, block_tables, k_pool, v_pool, batch, layer, num_layers,
+                    num_q_heads, num_kv_heads, head_dim, stream=stream)
+    lib.paged_decode(out, qkv, k_pool, v_pool, block_tables, positions, batch, max_ctx, layer,
                      num_layers, num_q_heads, num_kv_heads, head_dim, sm_scale(head_dim),
                      split_tokens, workspace, out_row_stride=out.shape[-1], q_row_stride=row,
                      stream=stream)
@@ -152,4 +164,5 @@ def ceil_div(a, b):
 
 
 __all__ = ["RopeCache", "KVCache", "apply_rope", "apply_flash_decoding", "decode_step",
+           "decode_step_unfused",
            "sm_scale", "BLOCK_SIZE"]

@@ -41,6 +41,9 @@ SIGNATURES = {
     "luc_paged_decode": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i32, _vp,
                                 _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp,
                                 _sz]),
+    "luc_decode_step": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                               _i32, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+                               _i32, _vp, _i64, _vp, _sz]),
 }
 
 
@@ -167,6 +170,29 @@ class LucAttn:
             q_row_stride if q_row_stride is not None else hq * head_dim, _p(k_pool), _p(v_pool),
             _p(tables), tables.shape[-1], _p(positions), batch, max_ctx, layer, num_layers, hq,
             hkv, head_dim, block_size, sm_scale, split_tokens, _p(workspace), ws_bytes))
+
+
+    def decode_step(self, qkv, q_bias, k_bias, v_bias, cos, sin, k_pool, v_pool, tables,
+                    positions, batch, max_ctx, layer, num_layers, hq, hkv, head_dim, sm_scale,
+                    out, workspace=None, split_tokens=0, qkv_row_stride=None,
+                    out_row_stride=None, block_size=16, stream=None):
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        self._check(self.lib.luc_decode_step(
+            self.ctx, _stream(stream), dtype_code(k_pool), _p(qkv),
+            qkv_row_stride if qkv_row_stride is not None else (hq + 2 * hkv) * head_dim,
+            _p(q_bias), _p(k_bias), _p(v_bias), _p(cos), _p(sin), _p(k_pool), _p(v_pool),
+            _p(tables), tables.shape[-1], _p(positions), batch, max_ctx, layer, num_layers, hq, hkv,
+            head_dim, block_size, sm_scale, split_tokens, _p(out),
+            out_row_stride if out_row_stride is not None else hq * head_dim, _p(workspace),
+            ws_bytes))
+
+    def workspace(self, batch, hq, hkv, head_dim, max_ctx, split_tokens=0, device=None):
+        """A zero-filled decode workspace (None when no split-K is needed)."""
+        need = self.workspace_size(batch, hq, hkv, head_dim, max_ctx, split_tokens)
+        if need == 0:
+            return None
+        return torch.zeros(need // 4, dtype=torch.float32,
+                           device=device if device is not None else f"cuda:{self.device}")
 
 
 _DEFAULT = {}

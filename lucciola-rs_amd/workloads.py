@@ -3,7 +3,7 @@
 Shapes (Qwen2.5 head layouts):
   single_512    B=1,  14q/2kv, d=64,  fp16, ctx 512, 32 pages (table permuted)
   batch32_mixed B=32, 14q/2kv, d=64,  fp16, ctx U{128..4096}, pool 16384 pages
-  batch64_long  B=64, 28q/4kv, d=128, bf16, ctx U{1024..16384}, pool 36864 pages
+  batch64_long  B=64, 28q/4kv, d=128, bf16, ctx U{1024..16384}, pool 40960 pages
   batch8_32k    B=8,  12q/2kv, d=128, bf16, ctx 32768, 16384 pages, 1% x8 outliers
 Values are N(0,1)*sigma rounded to the storage type.  Pages are handed out by
 a seeded shuffle of the pool and dealt to the sequences in order.  One extra
@@ -49,7 +49,7 @@ class DecodeConfig:
 CONFIGS = {
     "single_512": DecodeConfig("single_512", 1, 14, 2, 64, "f16", 512, 512, 32, 0.5),
     "batch32_mixed": DecodeConfig("batch32_mixed", 32, 14, 2, 64, "f16", 128, 4096, 16384, 0.5),
-    "batch64_long": DecodeConfig("batch64_long", 64, 28, 4, 128, "bf16", 1024, 16384, 36864, 0.3),
+    "batch64_long": DecodeConfig("batch64_long", 64, 28, 4, 128, "bf16", 1024, 16384, 40960, 0.3),
     "batch8_32k": DecodeConfig("batch8_32k", 8, 12, 2, 128, "bf16", 32768, 32768, 16384, 0.3,
                                outlier_frac=0.01, outlier_scale=8.0),
 }

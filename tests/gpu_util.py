@@ -8,7 +8,7 @@ import numpy as np
 import torch
 
 from lucciola_rs_amd import workloads as wl
-from lucciola_rs_amd.engine import RopeCache, decode_step, sm_scale
+from lucciola_rs_amd.engine import RopeCache, decode_step, decode_step_unfused, sm_scale
 
 # north-star tolerance on attention outputs (max-abs vs the reference algorithm)
 TOL = {"f16": 2e-3, "bf16": 1e-2}
@@ -37,8 +37,10 @@ def rope_cache(luc, head_dim, max_pos=32768, theta=1e6):
     return _ROPE[key]
 
 
-def gpu_step(luc, h: wl.HostDecode, split_tokens=0, layer=0, max_ctx=None, positions=None):
-    """One decode step through the C ABI on fresh device copies of h."""
+def gpu_step(luc, h: wl.HostDecode, split_tokens=0, layer=0, max_ctx=None, positions=None,
+             fused=True):
+    """One decode step through the C ABI on fresh device copies of h: the fused
+    single launch (luc_decode_step) or luc_rope_append + luc_paged_decode."""
     cfg = h.cfg
     rope = rope_cache(luc, cfg.head_dim)
     qkv = to_dev(h.qkv, cfg.dtype)
@@ -50,12 +52,13 @@ def gpu_step(luc, h: wl.HostDecode, split_tokens=0, layer=0, max_ctx=None, posit
     max_ctx = int(h.ctx.max()) if max_ctx is None else max_ctx
     out = torch.full((cfg.batch, cfg.hq * cfg.head_dim), 7.0, dtype=cfg.torch_dtype,
                      device="cuda")
-    nbytes = luc.workspace_size(cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, max_ctx, split_tokens)
-    ws = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device="cuda") if nbytes else None
-    say(f"  [gpu] decode_step {cfg.name} B={cfg.batch} hq={cfg.hq} hkv={cfg.hkv} "
-        f"d={cfg.head_dim} {cfg.dtype} max_ctx={max_ctx} split={split_tokens} layer={layer}")
-    decode_step(qkv, None, None, None, rope, kp, vp, tables, pos, max_ctx, layer, h.num_layers,
-                cfg.hq, cfg.hkv, cfg.head_dim, out, ws, split_tokens, lib=luc)
+    ws = luc.workspace(cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, max_ctx, split_tokens)
+    say(f"  [gpu] decode_step{'' if fused else '_unfused'} {cfg.name} B={cfg.batch} hq={cfg.hq} "
+        f"hkv={cfg.hkv} d={cfg.head_dim} {cfg.dtype} max_ctx={max_ctx} split={split_tokens} "
+        f"layer={layer}")
+    fn = decode_step if fused else decode_step_unfused
+    fn(qkv, None, None, None, rope, kp, vp, tables, pos, max_ctx, layer, h.num_layers,
+       cfg.hq, cfg.hkv, cfg.head_dim, out, ws, split_tokens, lib=luc)
     torch.cuda.synchronize()
     return dict(out=from_dev(out).reshape(cfg.batch, cfg.hq, cfg.head_dim), qkv=from_dev(qkv),
                 k_pool=from_dev(kp), v_pool=from_dev(vp))

@@ -93,8 +93,9 @@ def test_workspace_size_policy(cdll):
     ws = cdll.luc_paged_decode_workspace_size
     # one split per sequence -> no workspace
     assert ws(32, 14, 2, 64, 100, 0) == 0
-    # explicit split size: B*Hq*splits*(d+2)*4
-    assert ws(2, 14, 2, 64, 1000, 256) == 2 * 14 * 4 * 66 * 4
+    # explicit split size: tickets (B*Hkv int32, padded to 256 B) + B*Hq*splits*(d+2)*4
+    assert ws(2, 14, 2, 64, 1000, 256) == 256 + 2 * 14 * 4 * 66 * 4
+    assert ws(100, 28, 4, 128, 1000, 128) == 1792 + 100 * 28 * 8 * 130 * 4
     # rounding of the requested split to the tile (64 for d=64)
     assert ws(2, 14, 2, 64, 1000, 250) == ws(2, 14, 2, 64, 1000, 256)
     assert ws(1, 4, 1, 96, 1000, 0) == 0
@@ -116,3 +117,24 @@ def test_init_without_device_fails_cleanly(cdll):
     ctx = ctypes.c_void_p()
     rc = cdll.luc_init(0, None, ctypes.byref(ctx))
     assert rc in (-1, -4) and not ctx.value
+
+
+def test_decode_step_argument_checks(cdll):
+    def call(**kw):
+        args = dict(ctx=ctypes.c_void_p(1), stream=None, dtype=1, qkv=ctypes.c_void_p(16),
+                    qkv_stride=18 * 64, qb=None, kb=None, vb=None, cos=ctypes.c_void_p(16),
+                    sin=ctypes.c_void_p(16), k_pool=ctypes.c_void_p(256),
+                    v_pool=ctypes.c_void_p(512), tables=ctypes.c_void_p(16), table_stride=256,
+                    positions=ctypes.c_void_p(16), batch=32, max_ctx=4096, layer=0,
+                    num_layers=24, hq=14, hkv=2, head_dim=64, block_size=16, scale=0.125,
+                    split=0, out=ctypes.c_void_p(16), out_stride=14 * 64, ws=None, ws_bytes=0)
+        args.update(kw)
+        return cdll.luc_decode_step(*args.values())
+    assert call(qkv_stride=14 * 64) == -1      # a qkv row holds q, k and v
+    assert call(cos=None) == -1
+    assert call(head_dim=80) == -2
+    assert call(ws=None, ws_bytes=0) == -5     # split-K needs the workspace
+    assert call(batch=0) == 0
+    need = cdll.luc_paged_decode_workspace_size(32, 14, 2, 64, 4096, 0)
+    assert need > 0
+    assert call(ws=ctypes.c_void_p(4096 + 8), ws_bytes=need) == -1   # alignment

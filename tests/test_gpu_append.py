@@ -26,13 +26,15 @@ def make_rows(rng, n, hq, hkv, d, dtype):
 @pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (28, 4, 128), (12, 2, 128)])
 def test_rope_append_bit_exact(orc, luc, dtype, hq, hkv, d):
     rng = np.random.default_rng(hq + d)
-    L, layer, pages = 3, 1, 40
     positions = np.array([0, 1, 15, 16, 17, 31, 32, 255, 256, 511, 4095, 639], np.int32)
     n = len(positions)
+    # every row (sequence) owns its pages, so no two rows share a cache slot
+    L, layer, pages = 3, 1, n * 40 + 1
     qkv, qb, kb, vb = make_rows(rng, n, hq, hkv, d, dtype)
-    tables = np.stack([rng.permutation(pages)[:32] for _ in range(n)]).astype(np.int32)
-    tables = np.concatenate([tables, np.zeros((n, 256 - 32), np.int32)], axis=1)
-    tables[10, 255] = 7  # position 4095 -> logical page 255
+    perm = rng.permutation(pages - 1).astype(np.int32)
+    tables = np.full((n, 256), pages - 1, np.int32)
+    tables[:, :40] = perm.reshape(n, 40)
+    tables[10, 255] = tables[10, 39]  # position 4095 -> logical page 255
     kp = pins.bits(rng.standard_normal((pages, L, hkv, 16, d)), dtype)
     vp = pins.bits(rng.standard_normal((pages, L, hkv, 16, d)), dtype)
     rope = rope_cache(luc, d)

@@ -33,12 +33,13 @@ SMALL = [
 
 @pytest.mark.parametrize("name,batch,lo,hi", SMALL)
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-def test_decode_small_configs(orc, luc, name, batch, lo, hi, dtype):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
+def test_decode_small_configs(orc, luc, name, batch, lo, hi, dtype, fused):
     cfg = wl.scaled(wl.CONFIGS[name], batch=batch, ctx_lo=lo, ctx_hi=hi,
                     pool_pages=batch * ((hi + 15) // 16) + 3)
     cfg = wl.replace(cfg, dtype=dtype)
     h = wl.host_decode_inputs(cfg, seed=11)
-    assert_step_matches(orc, gpu_step(luc, h), oracle_step(orc, luc, h), dtype)
+    assert_step_matches(orc, gpu_step(luc, h, fused=fused), oracle_step(orc, luc, h), dtype)
 
 
 @pytest.mark.parametrize("group", [1, 2, 3, 4, 5, 6, 7, 8])
@@ -53,7 +54,7 @@ def test_decode_every_group_size(orc, luc, group, head_dim):
 def test_decode_layers_and_page_boundaries(orc, luc):
     # contexts at page boundaries, a non-zero layer of a 3-layer pool
     cfg = wl.DecodeConfig("bounds", 8, 14, 2, 64, "f16", 1, 1, 8 * 20, 0.5)
-    h = wl.host_decode_inputs(cfg, seed=3, num_layers=3)
+    h = wl.host_decode_inputs(cfg, seed=3, num_layers=3, poison=False)
     ctx = np.array([1, 15, 16, 17, 32, 33, 255, 257], np.int32)
     rng = np.random.default_rng(5)
     tables = np.full((8, 20), cfg.pool_pages, np.int32)
@@ -76,11 +77,12 @@ def test_single_512(orc, luc):
     assert_step_matches(orc, gpu_step(luc, h), oracle_step(orc, luc, h), "f16")
 
 
-def test_batch32_mixed_full(orc, luc):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
+def test_batch32_mixed_full(orc, luc, fused):
     """B=32, ctx U{128..4096}, pool 16384 pages, fp16 -- full size, one layer."""
     cfg = wl.CONFIGS["batch32_mixed"]
     h = wl.host_decode_inputs(cfg, seed=1)
-    assert_step_matches(orc, gpu_step(luc, h), oracle_step(orc, luc, h), "f16")
+    assert_step_matches(orc, gpu_step(luc, h, fused=fused), oracle_step(orc, luc, h), "f16")
 
 
 def test_batch8_32k_full(orc, luc):
@@ -155,14 +157,14 @@ def test_empty_and_overlong_contexts_give_nan(orc, luc):
     tables = torch.from_numpy(h.tables).cuda()
     pos = torch.tensor([499, -1, 499], dtype=torch.int32, device="cuda")
     out = torch.zeros((3, cfg.hq * 64), dtype=torch.float16, device="cuda")
-    ws = torch.empty(luc.workspace_size(3, 14, 2, 64, 300, 64) // 4, device="cuda")
+    ws = luc.workspace(3, 14, 2, 64, 300, 64)
     say("  [gpu] paged_decode max_ctx=300 < ctx=500, split 64")
     luc.paged_decode(out, q, kp, vp, tables, pos, 3, 300, 0, 1, 14, 2, 64, sm_scale(64), 64,
                      ws, q_row_stride=cfg.row)
     torch.cuda.synchronize()
     o = out.float().cpu().numpy()
     assert np.all(np.isnan(o)), "every sequence is empty or over max_ctx"
-    ws = torch.empty(max(luc.workspace_size(3, 14, 2, 64, 500) // 4, 1), device="cuda")
+    ws = luc.workspace(3, 14, 2, 64, 500)
     out.zero_()
     say("  [gpu] paged_decode max_ctx=500")
     luc.paged_decode(out, q, kp, vp, tables, pos, 3, 500, 0, 1, 14, 2, 64, sm_scale(64), 0, ws,
@@ -170,3 +172,32 @@ def test_empty_and_overlong_contexts_give_nan(orc, luc):
     torch.cuda.synchronize()
     o = out.float().cpu().numpy()
     assert np.all(np.isnan(o[1])) and np.all(np.isfinite(o[[0, 2]]))
+
+
+def test_workspace_reuse_across_launches(orc, luc):
+    """The split tickets return to zero after every launch: the same workspace
+    serves many launches (and layers) and gives identical results."""
+    cfg = wl.scaled(wl.CONFIGS["batch32_mixed"], batch=6, ctx_lo=300, ctx_hi=3000,
+                    pool_pages=6 * 188 + 1)
+    h = wl.host_decode_inputs(cfg, seed=51, num_layers=2, poison=False)
+    from gpu_util import to_dev
+    from lucciola_rs_amd.engine import sm_scale
+    kp, vp = to_dev(h.k_pool, "f16"), to_dev(h.v_pool, "f16")
+    q = to_dev(h.qkv, "f16")
+    tables = torch.from_numpy(h.tables).cuda()
+    pos = torch.from_numpy(h.positions).cuda()
+    max_ctx = int(h.ctx.max())
+    ws = luc.workspace(6, 14, 2, 64, max_ctx, 256)
+    outs = []
+    say("  [gpu] paged_decode x8 on one workspace")
+    for i in range(8):
+        out = torch.zeros((6, 14 * 64), dtype=torch.float16, device="cuda")
+        luc.paged_decode(out, q, kp, vp, tables, pos, 6, max_ctx, i % 2, 2, 14, 2, 64,
+                         sm_scale(64), 256, ws, q_row_stride=cfg.row)
+        outs.append(out)
+    torch.cuda.synchronize()
+    counters = ws[: 6 * 2].view(torch.int32).cpu()
+    assert torch.count_nonzero(counters) == 0
+    for i in range(2, 8):
+        assert torch.equal(outs[i], outs[i % 2])
+    assert not torch.equal(outs[0], outs[1])
