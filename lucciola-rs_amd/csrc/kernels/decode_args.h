@@ -22,7 +22,6 @@ struct luc_decode_args {
   int32_t layer, num_layers, hkv;
   float qk_scale_log2;      // sm_scale * log2(e)
   int32_t max_ctx, split_tokens, max_splits;
-  int32_t* counters;        // [batch*Hkv] split tickets, zero between launches
   float* ws_ml;             // [batch*Hq*max_splits][2]  (max, sum) per split
   float* ws_o;              // [batch*Hq*max_splits][head_dim]
   uint16_t* out;            // row b at out + b*out_stride, [Hq*head_dim]

@@ -47,6 +47,14 @@ template <> struct St<kF16> {
   }
 };
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte global load with the non-temporal (streaming) hint.
+__device__ inline uint4 ld_nt16(const uint16_t* p) {
+  const u32x4_t x = __builtin_nontemporal_load((const u32x4_t*)p);
+  return make_uint4(x.x, x.y, x.z, x.w);
+}
+
 // ---- wave64 reductions -------------------------------------------------
 // DPP controls (GFX9 encoding).
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]

@@ -93,9 +93,11 @@ def test_workspace_size_policy(cdll):
     ws = cdll.luc_paged_decode_workspace_size
     # one split per sequence -> no workspace
     assert ws(32, 14, 2, 64, 100, 0) == 0
-    # explicit split size: tickets (B*Hkv int32, padded to 256 B) + B*Hq*splits*(d+2)*4
-    assert ws(2, 14, 2, 64, 1000, 256) == 256 + 2 * 14 * 4 * 66 * 4
-    assert ws(100, 28, 4, 128, 1000, 128) == 1792 + 100 * 28 * 8 * 130 * 4
+    # explicit split size: B*Hq*splits*(d+2)*4
+    assert ws(2, 14, 2, 64, 1000, 256) == 2 * 14 * 4 * 66 * 4
+    assert ws(100, 28, 4, 128, 1000, 128) == 100 * 28 * 8 * 130 * 4
+    # at most 256 splits per sequence: the split grows with the context
+    assert ws(1, 4, 1, 64, 64 * 1024, 64) == 1 * 4 * 256 * 66 * 4
     # rounding of the requested split to the tile (64 for d=64)
     assert ws(2, 14, 2, 64, 1000, 250) == ws(2, 14, 2, 64, 1000, 256)
     assert ws(1, 4, 1, 96, 1000, 0) == 0
@@ -138,3 +140,4 @@ def test_decode_step_argument_checks(cdll):
     need = cdll.luc_paged_decode_workspace_size(32, 14, 2, 64, 4096, 0)
     assert need > 0
     assert call(ws=ctypes.c_void_p(4096 + 8), ws_bytes=need) == -1   # alignment
+    assert call(ws=ctypes.c_void_p(4096), ws_bytes=need - 4) == -5   # too small

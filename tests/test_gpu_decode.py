@@ -175,8 +175,7 @@ def test_empty_and_overlong_contexts_give_nan(orc, luc):
 
 
 def test_workspace_reuse_across_launches(orc, luc):
-    """The split tickets return to zero after every launch: the same workspace
-    serves many launches (and layers) and gives identical results."""
+    """One workspace serves many launches (and layers) with identical results."""
     cfg = wl.scaled(wl.CONFIGS["batch32_mixed"], batch=6, ctx_lo=300, ctx_hi=3000,
                     pool_pages=6 * 188 + 1)
     h = wl.host_decode_inputs(cfg, seed=51, num_layers=2, poison=False)
@@ -196,8 +195,6 @@ def test_workspace_reuse_across_launches(orc, luc):
                          sm_scale(64), 256, ws, q_row_stride=cfg.row)
         outs.append(out)
     torch.cuda.synchronize()
-    counters = ws[: 6 * 2].view(torch.int32).cpu()
-    assert torch.count_nonzero(counters) == 0
     for i in range(2, 8):
         assert torch.equal(outs[i], outs[i % 2])
     assert not torch.equal(outs[0], outs[1])
