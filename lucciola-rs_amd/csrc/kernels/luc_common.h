@@ -85,14 +85,28 @@ __device__ inline float row_sum16(float x) {
 __device__ inline float readlane(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
-// Wave-uniform max / sum over all 64 lanes.
+// Wave-uniform max / sum over all 64 lanes.  A chain of DPP-fused VALU ops
+// (quad swaps, row half-mirror, row mirror, then the row broadcasts of lanes
+// 15 and 31 into the following rows) leaves the result in lane 63.  Each DPP
+// read of a register written by the previous VALU op needs two wait states
+// (s_nop 1); the trailing s_nop covers the readlane of the result.
+#define LUC_DPP_REDUCE(OP)                                                                   \
+  "s_nop 1\n\t" OP " %0, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"          \
+  "s_nop 1\n\t" OP " %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"          \
+  "s_nop 1\n\t" OP " %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"              \
+  "s_nop 1\n\t" OP " %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf\n\t"                   \
+  "s_nop 1\n\t" OP " %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"                 \
+  "s_nop 1\n\t" OP " %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"                 \
+  "s_nop 1"
 __device__ inline float wave_max(float x) {
-  x = row_max16(x);
-  return fmaxf(fmaxf(readlane(x, 0), readlane(x, 16)), fmaxf(readlane(x, 32), readlane(x, 48)));
+  float r;
+  asm volatile(LUC_DPP_REDUCE("v_max_f32_dpp") : "=&v"(r) : "v"(x));
+  return readlane(r, 63);
 }
 __device__ inline float wave_sum(float x) {
-  x = row_sum16(x);
-  return (readlane(x, 0) + readlane(x, 16)) + (readlane(x, 32) + readlane(x, 48));
+  float r;
+  asm volatile(LUC_DPP_REDUCE("v_add_f32_dpp") : "=&v"(r) : "v"(x));
+  return readlane(r, 63);
 }
 
 // Orders this wave's LDS accesses at this point (DS operations of one wave

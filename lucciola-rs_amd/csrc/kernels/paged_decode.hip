@@ -14,319 +14,427 @@
 // v + v_bias (src/kernels/kv_cache.cu).  Attention takes the new token's K/V
 // from LDS, so it does not depend on the order of the cache write.
 //
-// Launches:
-//   luc_decode[_step]_*   partials: one (m, l, o[D]) per (sequence, q-head,
-//                         split), or the final output when a sequence has a
-//                         single split.
-//   luc_decode_combine_*  log-sum-exp merge of the splits; the step variant
-//                         also writes the roped q and k back in place (after
-//                         every split has read them).
-//
-// Work decomposition (decode kernel):
-//   A work item is (sequence b, kv head h, split).  Items are numbered
-//   densely from the device-side positions, so no workgroup is launched for
-//   splits past a context; the grid is persistent (sized to the resident
-//   workgroups) and each workgroup walks items blockIdx.x, +gridDim.x, ...
-//   A workgroup is 4 waves; the G = Hq/Hkv q-heads of kv head h are processed
-//   together, so each KV page is read from HBM once per kv head (GQA).  A wave
-//   walks 64-token tiles (32 for head_dim 128) of the split:
-//     1. 16-byte loads; one load instruction of the wave covers 1 KB of a page
-//        (pages are contiguous [16][D] slabs).  The first tile's loads are
-//        issued before any other per-item setup.
-//     2. K goes through LDS and is read back one token per lane; scores for
-//        all G heads use v_dot2_f32_{f16,bf16} with q broadcast from LDS.
+// One launch per step.  Work decomposition:
+//   Workgroup = (split, sequence b, kv head h), split-major, so the splits
+//   every sequence has (split 0, 1, ...) are dispatched first and the
+//   workgroups of splits past a context exit at once.  A workgroup is 4
+//   waves; the G = Hq/Hkv q-heads of kv head h are processed together, so
+//   each KV page is read from HBM once per kv head (GQA).
+//   Prologue: positions[b], the wave's block-table entries and q are loaded
+//   together (one memory round trip before the KV stream).
+//   A wave walks 8 KB tiles of K (64 tokens at head_dim 64, 32 at 128):
+//     1. K goes straight from HBM into LDS (global_load_lds_dwordx4; one
+//        wave-wide load = 1 KB of a page), each token row XOR-swizzled by
+//        16-byte chunk so the per-token LDS reads are conflict-free; V goes
+//        to registers in the same load layout (lane = token x 16-byte chunk).
+//     2. Scores: lane = token (x2 lanes per token at head_dim 128), all G
+//        heads with v_dot2_f32_{f16,bf16}, q broadcast from LDS.
 //     3. Online softmax in the exp2 domain: wave max by DPP row reductions +
-//        readlane; per-lane partial sums of p; o is rescaled only when the
-//        running max moves.
-//     4. V stays in registers in its load layout (lane = token group x 8
-//        dims); p is broadcast through LDS; f32 FMA accumulation.
-//   Each wave reduces its token groups through LDS, then the 4 waves merge.
+//        readlane; o rescaled only when the running max moves.
+//     4. o += p * V with V in its load layout.  fp16: p of tokens t and
+//        t + TILE/2 packed as an fp16 pair, V of the same two tokens paired by
+//        v_perm, one v_dot2_f32_f16 per (head, dim).  bf16: f32 FMA.
+//   The wave's token groups are reduced with permlane swaps (reduce-scatter)
+//   and the 4 waves merge through LDS.  A sequence with one split writes its
+//   output; otherwise each split writes (m, l, o) to the workspace, and the
+//   last split to arrive (an agent-scope arrival counter per (b, h)) merges
+//   all splits with the log-sum-exp rule and resets the counter.
 #include "decode_args.h"
 #include "luc_common.h"
 
 namespace luc {
 
 using DecodeArgs = ::luc_decode_args;
+typedef __attribute__((address_space(3))) char lds_char;
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <int D>
-struct DecodeShape {
-  static constexpr int NW = 4;                       // waves per workgroup
-  static constexpr int CH = D / 8;                   // 16-byte chunks per token row
-  static constexpr int TILE = (D == 64) ? 64 : 32;   // tokens per wave tile
-  static constexpr int LOADS = TILE * CH / 64;       // 16-byte loads per lane per tile
-  static constexpr int QKL = 64 / TILE;              // lanes per token for QK
-  static constexpr int GROUPS = 64 / CH;             // tokens per load instruction
-  static constexpr int KROW = D * 2 + 16;            // padded LDS row (bytes)
-  static constexpr int LPP = kPage * CH / 64;        // load instructions per page
-  static constexpr int STAGE = TILE * KROW + TILE * 32;  // per-wave LDS: K tile + p tile
-  static constexpr int HP = (D == 64) ? 4 : 2;       // heads per group-reduction pass
-  static constexpr int RES_OFF = GROUPS * HP * D * 4;    // per-wave result after the scratch
+struct DecodeGeo {
+  static constexpr int NW = 4;                 // waves per workgroup
+  static constexpr int CH = D / 8;             // 16-byte chunks per token row
+  static constexpr int TPL = 64 / CH;          // tokens per wave-wide 16-byte load
+  static constexpr int TILE = 512 / CH;        // tokens per wave tile (8 KB of K)
+  static constexpr int LOADS = TILE / TPL;     // K (and V) loads per lane per tile
+  static constexpr int HALF = TILE / 2;        // PV pairs tokens t and t + HALF
+  static constexpr int QKL = 64 / TILE;        // lanes per token for the scores
+  static constexpr int LPP = kPage / TPL;      // load instructions per page
+  static constexpr int PAGES = TILE / kPage;   // pages per tile
+  static constexpr int ROWB = D * 2;           // bytes per token row
+  static constexpr int KBYTES = TILE * ROWB;   // LDS bytes of one wave's K tile
+  static_assert(LOADS == 8 && TPL * ROWB == 1024, "one wave-wide load is 1 KB");
 };
 
+constexpr int kCpolNT = 2;  // non-temporal load: the KV stream is read once per step
+
+#ifndef LUC_SCHED_FENCE
+#define LUC_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+#endif
+
+// Wait until this wave has no vector memory operation in flight (also covers
+// the LDS writes of global_load_lds, which the compiler does not track).
+__device__ inline void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// ... until at most 8 (the V loads of a tile) are still in flight.
+__device__ inline void wait_vmcnt_loads() { asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); }
+
+// 16 bytes per lane from global memory straight into LDS at l + 16*lane + rb;
+// rb (the instruction offset) also moves the global address.  rb must fold
+// to a constant.
+__device__ inline void dma16(const char* g, lds_char* l, int rb) {
+  switch (rb) {
+    case 0: __builtin_amdgcn_global_load_lds(g, (lds_void*)l, 16, 0, kCpolNT); break;
+    case 1024: __builtin_amdgcn_global_load_lds(g, (lds_void*)l, 16, 1024, kCpolNT); break;
+    case 2048: __builtin_amdgcn_global_load_lds(g, (lds_void*)l, 16, 2048, kCpolNT); break;
+    default: __builtin_amdgcn_global_load_lds(g, (lds_void*)l, 16, 3072, kCpolNT); break;
+  }
+}
+
+// Agent-coherent (sc1) f32 store / load: visible across the XCDs' L2 caches
+// without a cache write-back.
+__device__ inline void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline uint4 lds_ld16(const char* base, int off) {
+  return *(const uint4*)(base + off);
+}
+
+// Bias + RoPE of one pair (x1, x2) in f32, each product and the
+// difference/sum rounded separately (contraction off), as rope.cu:31-52.
+// A zero bias pattern is +0.0, so a missing bias adds exactly nothing.
 template <int DT>
-__device__ inline void rot_pair(const uint16_t* x, const uint16_t* bias, int i1, int i2, float c,
+__device__ inline void rot_pair(uint16_t x1, uint16_t b1, uint16_t x2, uint16_t b2, float c,
                                 float s, uint16_t& o1, uint16_t& o2) {
 #pragma clang fp contract(off)
-  const float v1 = St<DT>::load(x[i1]) + (bias ? St<DT>::load(bias[i1]) : 0.0f);
-  const float v2 = St<DT>::load(x[i2]) + (bias ? St<DT>::load(bias[i2]) : 0.0f);
+  const float v1 = St<DT>::load(x1) + St<DT>::load(b1);
+  const float v2 = St<DT>::load(x2) + St<DT>::load(b2);
   const float a = v1 * c, bb = v2 * s, e = v1 * s, f = v2 * c;
   o1 = St<DT>::store(a - bb);
   o2 = St<DT>::store(e + f);
 }
 
-// Number of splits of a sequence whose current position is pos; 0 when the
-// context is empty or beyond max_ctx (such a sequence still gets one item,
-// which writes NaN).
-__device__ inline int splits_of(int pos, int max_ctx, int split_tokens) {
-  const int ctx = pos + 1;
-  return (ctx <= 0 || ctx > max_ctx) ? 0 : (ctx + split_tokens - 1) / split_tokens;
+// Value of the lane TILE/2 tokens further on (valid in lanes < TILE/2).
+template <int D>
+__device__ inline float upper_half_value(float x) {
+  const uint32_t u = __float_as_uint(x);
+  if constexpr (D == 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[1]);
+  }
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
-__device__ inline int wave_incl_scan(int x, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
-
-struct Item {
-  int b, h, split, nsplit;  // nsplit 0: invalid context
-};
-
-// Item `it` of the dense numbering: sequences in order, then kv heads, then
-// splits.  Every lane returns the same item.  Returns false past the last one.
-__device__ inline bool find_item(const DecodeArgs& A, int batch, int it, int lane, Item& out) {
-  int base = 0;  // items before this chunk of sequences
-  for (int b0 = 0; b0 < batch; b0 += 64) {
-    const int b = b0 + lane;
-    int n = 0;
-    if (b < batch) n = max(1, splits_of(A.positions[b], A.max_ctx, A.split_tokens)) * A.hkv;
-    const int incl = wave_incl_scan(n, lane);
-    const int total = __shfl(incl, 63);
-    if (it < base + total) {
-      // the first lane whose inclusive sum exceeds the local index owns it
-      const int local = it - base;
-      const unsigned long long m = __ballot(incl > local && b < batch);
-      const int src = __ffsll((long long)m) - 1;
-      const int bb = b0 + src;
-      const int excl = __shfl(incl - n, src);
-      const int ns = __shfl(n, src) / A.hkv;
-      const int r = local - excl;
-      out.b = bb;
-      out.h = r / ns;
-      out.split = r % ns;
-      out.nsplit = splits_of(A.positions[bb], A.max_ctx, A.split_tokens);
-      return true;
-    }
-    base += total;
-  }
-  return false;
+__device__ inline uint32_t pack_f16(float lo, float hi) {
+  const half2_t v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 template <int DT, int D, int G, bool APPEND>
-__device__ void decode_impl(const DecodeArgs& A, int batch) {
-  using S = DecodeShape<D>;
-  constexpr int NT = S::NW * 64;
-  __shared__ __attribute__((aligned(16))) char smem[S::NW * S::STAGE];
+__device__ void decode_impl(const DecodeArgs& A) {
+  using S = DecodeGeo<D>;
+  constexpr int NW = S::NW, NT = NW * 64;
+  constexpr bool PV_DOT2 = (DT == kF16);
+  constexpr int PWORDS = (PV_DOT2 ? S::HALF : S::TILE) * 8;  // per-wave p exchange, 32-bit words
+  constexpr int HD = D / 2;
+  __shared__ __attribute__((aligned(16))) char s_k[NW * S::KBYTES];
+  __shared__ __attribute__((aligned(16))) uint32_t s_p[NW * PWORDS];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[G * D];
   __shared__ __attribute__((aligned(16))) uint16_t s_knew[D];
   __shared__ __attribute__((aligned(16))) uint16_t s_vnew[D];
-  __shared__ float s_m[S::NW][8];
-  __shared__ float s_l[S::NW][8];
+  __shared__ float s_m[NW][8], s_l[NW][8], s_L[8];
+  __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  const int tq = lane % S::TILE;          // QK: token of this lane
-  const int qhalf = lane / S::TILE;       // QK: which 64 dims (head_dim 128)
-  const int pv_tok = lane / S::CH;        // load layout: token within a load group
-  const int pv_chunk = lane % S::CH;      // load layout: 16-byte chunk of the row
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pairs = A.batch * A.hkv;
+  const int split = blockIdx.x / pairs;
+  const int bh = blockIdx.x - split * pairs;
+  const int b = bh / A.hkv, h = bh - b * A.hkv;
   const int hq = A.hkv * G;
-  char* stage = smem + w * S::STAGE;
-  char* s_k = stage;
-  float* s_p = (float*)(stage + S::TILE * S::KROW);
+  const int ST = A.split_tokens;
+  const int s_begin = split * ST;
   const int64_t page_stride = (int64_t)A.num_layers * A.hkv * kPage * D;
+  const int64_t head_off = ((int64_t)A.layer * A.hkv + h) * kPage * D;
+  const int* trow = A.tables + (int64_t)b * A.table_stride;
+  const int tmax = (int)A.table_stride - 1;
+  uint16_t* out_row = A.out + (int64_t)b * A.out_stride + (int64_t)h * G * D;
+  const uint16_t* qrow = A.q + (int64_t)b * A.q_stride + (int64_t)h * G * D;
 
-  for (int it = blockIdx.x;; it += gridDim.x) {
-    Item item;
-    if (!find_item(A, batch, it, lane, item)) break;  // uniform: every wave finds the same
-    const int b = __builtin_amdgcn_readfirstlane(item.b);
-    const int h = __builtin_amdgcn_readfirstlane(item.h);
-    const int split = __builtin_amdgcn_readfirstlane(item.split);
-    const int nsplit = __builtin_amdgcn_readfirstlane(item.nsplit);
-    uint16_t* out_row = A.out + (int64_t)b * A.out_stride + (int64_t)h * G * D;
-    if (nsplit == 0) {
-      // empty context (0/0 in the reference) or beyond the host bound: NaN
+  // ---- prologue: position, this wave's first table entries and q together ----
+  const int t_first = s_begin + w * S::TILE;
+  int tab = 0;  // lane j < PAGES: physical page j of the wave's current tile
+  if (lane < S::PAGES) tab = trow[min(t_first / kPage + lane, tmax)];
+  uint32_t qv[(G * D / 2 + NT - 1) / NT];
+  if constexpr (!APPEND) {
+#pragma unroll
+    for (int i = 0; i < (G * D / 2 + NT - 1) / NT; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < G * D / 2) qv[i] = ((const uint32_t*)qrow)[idx];
+    }
+  }
+  const int pos = A.positions[b];
+  const int ctx = pos + 1;
+  if (ctx < 1 || ctx > A.max_ctx) {
+    // empty context (0/0 in the reference) or beyond the host bound: NaN
+    if (split == 0)
       for (int i = threadIdx.x; i < G * D; i += NT) out_row[i] = St<DT>::store(__builtin_nanf(""));
-      continue;
-    }
-    const int pos = A.positions[b];
-    const int ctx = pos + 1;
-    const int s_begin = split * A.split_tokens;
-    const int s_end = min(ctx, s_begin + A.split_tokens);
-    const int* table = A.tables + (int64_t)b * A.table_stride;
-    const int64_t head_off = ((int64_t)A.layer * A.hkv + h) * kPage * D;
-    const bool owns_pos = APPEND && pos >= s_begin && pos < s_end;
+    return;
+  }
+  if (s_begin >= ctx) return;  // split past this context
+  const int nsplit = (ctx + ST - 1) / ST;
+  const int s_end = min(ctx, s_begin + ST);
+  const bool owns = APPEND && pos < s_end;  // the split holding the new token
 
-    uint4 kr[S::LOADS], vr[S::LOADS];
-    auto load_tile = [&](int t0) {
-      // The tile's block-table entries with one vector load (lane j: page j);
-      // scalar loads of them queue behind the KV stream of other waves.
-      int my_phys = 0;
-      if (lane < S::TILE / kPage && t0 + lane * kPage < s_end) my_phys = table[t0 / kPage + lane];
+  // The step variant's prologue operands (q and k of the new token with their
+  // biases, the cos/sin row, v + v_bias) are loaded before the KV stream is
+  // issued, so using them does not wait for it.
+  constexpr int NPAIR = APPEND ? ((G + 1) * HD + NT - 1) / NT : 1;
+  uint16_t rx1[NPAIR], rx2[NPAIR], rb1[NPAIR], rb2[NPAIR], rv = 0, rvb = 0;
+  float rc[NPAIR], rs[NPAIR];
+  if constexpr (APPEND) {
+    const float* crow = A.cos_t + (int64_t)pos * HD;
+    const float* srow = A.sin_t + (int64_t)pos * HD;
+    const uint16_t* krow = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
 #pragma unroll
-      for (int r = 0; r < S::LOADS; ++r) {
-        const int page_tok = t0 + (r / S::LPP) * kPage;
-        if (page_tok < s_end) {
-          const int64_t phys = __builtin_amdgcn_readlane(my_phys, r / S::LPP);
-          const int64_t off = phys * page_stride + head_off + (int64_t)((r % S::LPP) * 64 + lane) * 8;
-          // KV is read once per step: non-temporal, so the stream does not
-          // evict the small, reused data (tables, positions, q) from L2
-          kr[r] = ld_nt16(A.k_pool + off);
-          vr[r] = ld_nt16(A.v_pool + off);
-        } else {
-          kr[r] = make_uint4(0, 0, 0, 0);
-          vr[r] = make_uint4(0, 0, 0, 0);
-        }
-      }
-    };
+    for (int i = 0; i < NPAIR; ++i) {
+      const int idx = min(threadIdx.x + i * NT, (G + 1) * HD - 1);
+      const int g = idx / HD, j = idx % HD;
+      const uint16_t* x = g < G ? qrow + g * D : krow;
+      const uint16_t* bias = g < G ? (A.q_bias ? A.q_bias + ((int64_t)h * G + g) * D : nullptr)
+                                   : (A.k_bias ? A.k_bias + (int64_t)h * D : nullptr);
+      rx1[i] = x[j];
+      rx2[i] = x[j + HD];
+      rb1[i] = bias ? bias[j] : 0;
+      rb2[i] = bias ? bias[j + HD] : 0;
+      rc[i] = crow[j];
+      rs[i] = srow[j];
+    }
+    if (threadIdx.x < D) {
+      rv = A.v_new[(int64_t)b * A.q_stride + (int64_t)h * D + threadIdx.x];
+      if (A.v_bias) rvb = A.v_bias[(int64_t)h * D + threadIdx.x];
+    }
+  }
 
-    // ---- 1. the first tile's loads go out before the rest of the setup ----
-    const int t_first = s_begin + w * S::TILE;
-    if (t_first < s_end) load_tile(t_first);
+  const int tq = lane % S::TILE;     // scores: token of this lane
+  const int qh = lane / S::TILE;     // scores: which 64 dims (head_dim 128)
+  const int pv_tok = lane / S::CH;   // load layout: token within a load
+  const int pv_ch = lane % S::CH;    // load layout: 16-byte chunk of the row
+  const int kbase = w * S::KBYTES;   // this wave's K tile in s_k
+  lds_char* const kdma = (lds_char*)s_k + kbase;
 
-    // ---- 2. q of the G heads (roped in the step variant), new token's k, v ----
-    const uint16_t* qrow = A.q + (int64_t)b * A.q_stride + (int64_t)h * G * D;
-    if constexpr (APPEND) {
-      constexpr int HALF = D / 2;
-      const float* crow = A.cos_t + (int64_t)pos * HALF;
-      const float* srow = A.sin_t + (int64_t)pos * HALF;
-      const uint16_t* qb = A.q_bias ? A.q_bias + (int64_t)h * G * D : nullptr;
-      const uint16_t* krow = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
-      const uint16_t* kb = A.k_bias ? A.k_bias + (int64_t)h * D : nullptr;
-      for (int idx = threadIdx.x; idx < (G + 1) * HALF; idx += NT) {
-        const int g = idx / HALF, i = idx % HALF;
+  // Per-lane byte offsets inside a (page, layer, kv head) slab.  Load r reads
+  // page r / LPP at + (r % LPP) * 1KB; the K slot pv_ch of token tl holds
+  // chunk pv_ch ^ (tl & 7), where tl & 7 only depends on the parity of r.
+  auto k_lane_off = [&](int parity) -> uint32_t {
+    const int sw = (S::TPL == 8) ? pv_tok : ((parity * S::TPL + pv_tok) & 7);
+    return (uint32_t)(pv_tok * S::ROWB + ((pv_ch ^ sw) << 4));
+  };
+  const uint32_t koff0 = k_lane_off(0), koff1 = k_lane_off(1);
+  const uint32_t voff = (uint32_t)(pv_tok * S::ROWB + (pv_ch << 4));
+  uint4 vr[S::LOADS];
+  // All K loads of a tile go out before its V loads, so the scores can start
+  // as soon as K has landed (vmcnt <= LOADS) while V is still in flight.  Pages
+  // past the split re-read the tile's last valid page (a cache hit), which
+  // keeps the number of loads per tile fixed.
+  auto issue = [&](int t0) {
+    const int jlast = min(S::PAGES - 1, (s_end - 1 - t0) / kPage);
+#pragma unroll
+    for (int r = 0; r < S::LOADS; ++r) {
+      const int64_t phys = __builtin_amdgcn_readlane(tab, min(r / S::LPP, jlast));
+      // wave-uniform slab base (scalar registers) + 32-bit lane offsets
+      const char* kslab = (const char*)(A.k_pool + phys * page_stride + head_off);
+      dma16(kslab + ((r & 1) ? koff1 : koff0), kdma + (r - r % S::LPP) * 1024, (r % S::LPP) * 1024);
+    }
+#pragma unroll
+    for (int r = 0; r < S::LOADS; ++r) {
+      const int64_t phys = __builtin_amdgcn_readlane(tab, min(r / S::LPP, jlast));
+      const char* vslab = (const char*)(A.v_pool + phys * page_stride + head_off);
+      vr[r] = ld_nt16((const uint16_t*)(vslab + voff + (r % S::LPP) * 1024));
+    }
+  };
+  if (t_first < s_end) issue(t_first);
+
+  // ---- q of the G heads (roped in the step variant), new token's k, v ----
+  if constexpr (APPEND) {
+#pragma unroll
+    for (int i = 0; i < NPAIR; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < (G + 1) * HD) {
+        const int g = idx / HD, j = idx % HD;
         uint16_t o1, o2;
-        if (g < G) {
-          rot_pair<DT>(qrow, qb, g * D + i, g * D + i + HALF, crow[i], srow[i], o1, o2);
-          s_q[g * D + i] = o1;
-          s_q[g * D + i + HALF] = o2;
-        } else {
-          rot_pair<DT>(krow, kb, i, i + HALF, crow[i], srow[i], o1, o2);
-          s_knew[i] = o1;
-          s_knew[i + HALF] = o2;
+        rot_pair<DT>(rx1[i], rb1[i], rx2[i], rb2[i], rc[i], rs[i], o1, o2);
+        uint16_t* dst = g < G ? s_q + g * D : s_knew;
+        dst[j] = o1;
+        dst[j + HD] = o2;
+      }
+    }
+    if (threadIdx.x < D) s_vnew[threadIdx.x] = St<DT>::store(St<DT>::load(rv) + St<DT>::load(rvb));
+  } else {
+#pragma unroll
+    for (int i = 0; i < (G * D / 2 + NT - 1) / NT; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < G * D / 2) ((uint32_t*)s_q)[idx] = qv[i];
+    }
+  }
+  __syncthreads();
+
+  float m_run[G], l_lane[G], o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m_run[g] = -INFINITY;
+    l_lane[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+  }
+  uint32_t* const pw = s_p + w * PWORDS;
+
+  for (int t0 = t_first; t0 < s_end; t0 += NW * S::TILE) {
+    if (t0 != t_first) issue(t0);
+    wait_vmcnt_loads();  // K in LDS (V may still be in flight)
+    if constexpr (APPEND) {
+      if (owns && pos >= t0 && pos < t0 + S::TILE) {  // this tile holds the new token
+        const int t = pos - t0;
+        if (lane < S::CH) {
+          // its K row in LDS, V in registers, and the cache write of both
+          *(uint4*)(s_k + kbase + t * S::ROWB + lane * 16) =
+              *(const uint4*)(s_knew + ((lane ^ (t & 7)) * 8));
+          const int64_t phys = __builtin_amdgcn_readlane(tab, t / kPage);
+          const int64_t slot = phys * page_stride + head_off + (int64_t)(t % kPage) * D + lane * 8;
+          *(uint4*)(A.k_pool + slot) = *(const uint4*)(s_knew + lane * 8);
+          *(uint4*)(A.v_pool + slot) = *(const uint4*)(s_vnew + lane * 8);
         }
+#pragma unroll
+        for (int r = 0; r < S::LOADS; ++r)
+          if (r == t / S::TPL && pv_tok == t % S::TPL) vr[r] = *(const uint4*)(s_vnew + pv_ch * 8);
       }
-      if (threadIdx.x < D) {
-        const int64_t vi = (int64_t)b * A.q_stride + (int64_t)h * D + threadIdx.x;
-        const float vb = A.v_bias ? St<DT>::load(A.v_bias[(int64_t)h * D + threadIdx.x]) : 0.0f;
-        s_vnew[threadIdx.x] = St<DT>::store(St<DT>::load(A.v_new[vi]) + vb);
-      }
-    } else {
-      const uint32_t* src = (const uint32_t*)qrow;
-      for (int i = threadIdx.x; i < G * D / 2; i += NT) ((uint32_t*)s_q)[i] = src[i];
     }
-    __syncthreads();
-    if (owns_pos && threadIdx.x < D) {  // the cache write of the new token
-      const int64_t slot = (int64_t)table[pos / kPage] * page_stride + head_off +
-                           (int64_t)(pos % kPage) * D + threadIdx.x;
-      A.k_pool[slot] = s_knew[threadIdx.x];
-      A.v_pool[slot] = s_vnew[threadIdx.x];
+    {  // the next tile's table entries, while this tile computes
+      const int t_next = t0 + NW * S::TILE;
+      if (t_next < s_end && lane < S::PAGES) tab = trow[min(t_next / kPage + lane, tmax)];
     }
+    wave_lds_sync();
 
-    float m_run[G], l_lane[G], o[G][8];
+    // ---- scores: lane = token (x2 lanes per token at head_dim 128) ----
+    float acc[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      m_run[g] = -INFINITY;
-      l_lane[g] = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
-    }
-
-    for (int t0 = t_first; t0 < s_end; t0 += S::NW * S::TILE) {
-      if (t0 != t_first) load_tile(t0);
-      const bool sub = owns_pos && pos >= t0 && pos < t0 + S::TILE;  // tile holds the new token
-#pragma unroll
-      for (int r = 0; r < S::LOADS; ++r) {
-        const int tok = r * S::GROUPS + pv_tok;
-        uint4 kv = kr[r];
-        if (sub && t0 + tok == pos) {
-          kv = *(const uint4*)(s_knew + pv_chunk * 8);
-          vr[r] = *(const uint4*)(s_vnew + pv_chunk * 8);
-        }
-        *(uint4*)(s_k + tok * S::KROW + pv_chunk * 16) = kv;
-        // tokens past the split: V must contribute exactly zero (p is 0 there,
-        // and 0 * stale data must not produce NaN)
-        if (t0 + tok >= s_end) vr[r] = make_uint4(0, 0, 0, 0);
-      }
-      wave_lds_sync();
-
-      // ---- scores: lane = token (x2 lanes per token for head_dim 128) ----
-      float acc[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) acc[g] = 0.0f;
-      const char* krow = s_k + tq * S::KROW + qhalf * 128;
-      // q is re-read from LDS every tile: an opaque zero offset keeps the
-      // compiler from hoisting G*64 loop-invariant values into registers.
-      int qz;
-      asm volatile("s_mov_b32 %0, 0" : "=s"(qz));
-      const uint16_t* qb = s_q + qhalf * 64 + qz;
-      // Partially unrolled: fully unrolled, the scheduler hoists all 8*(G+1)
-      // LDS reads ahead of the dot products and runs out of registers.
+    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+    const int krow = kbase + tq * S::ROWB;
+    const int sw = tq & 7;
+    // q is re-read from LDS every tile: an opaque zero offset keeps the
+    // compiler from hoisting G*D/8 loop-invariant 16-byte values into registers.
+    int qz;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(qz));
+    const uint16_t* qb = s_q + qz + qh * 64;
 #pragma unroll 2
-      for (int c = 0; c < 8; ++c) {
-        const uint4 kc = *(const uint4*)(krow + c * 16);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const uint4 qc = *(const uint4*)(qb + g * D + c * 8);
-          float a = acc[g];
-          a = St<DT>::dot2(qc.x, kc.x, a);
-          a = St<DT>::dot2(qc.y, kc.y, a);
-          a = St<DT>::dot2(qc.z, kc.z, a);
-          a = St<DT>::dot2(qc.w, kc.w, a);
-          acc[g] = a;
-        }
-      }
-      if constexpr (S::QKL == 2) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) acc[g] += __shfl_xor(acc[g], 32);
-      }
-      const bool valid = (t0 + tq) < s_end;
-      float p[8];
+    for (int c = 0; c < 8; ++c) {
+      const uint4 kc = lds_ld16(s_k, krow + (((qh * 8 + c) ^ sw) << 4));
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float s = valid ? acc[g] * A.qk_scale_log2 : -INFINITY;
-        // wave-uniform: kept in a scalar register
-        const float mn = __builtin_bit_cast(
-            float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fmaxf(m_run[g], wave_max(s)))));
-        p[g] = __builtin_amdgcn_exp2f(s - mn);
-        if (mn != m_run[g]) {  // wave-uniform: rescale only when the max moves
+        const uint4 qc = *(const uint4*)(qb + g * D + c * 8);
+        float a = acc[g];
+        a = St<DT>::dot2(qc.x, kc.x, a);
+        a = St<DT>::dot2(qc.y, kc.y, a);
+        a = St<DT>::dot2(qc.z, kc.z, a);
+        a = St<DT>::dot2(qc.w, kc.w, a);
+        acc[g] = a;
+      }
+      LUC_SCHED_FENCE();
+    }
+    if constexpr (S::QKL == 2) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const uint32_t u = __float_as_uint(acc[g]);
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        acc[g] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      }
+    }
+
+    // ---- online softmax (exp2 domain) ----
+    const bool valid = (t0 + tq) < s_end;
+    float p[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float s = valid ? acc[g] * A.qk_scale_log2 : -INFINITY;
+      // wave-uniform: kept in a scalar register
+      const float mn = __builtin_bit_cast(
+          float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fmaxf(m_run[g], wave_max(s)))));
+      p[g] = __builtin_amdgcn_exp2f(s - mn);
+      if (mn > m_run[g]) {  // wave-uniform: rescale only when the max moves
+        if (m_run[g] > -INFINITY) {  // (nothing accumulated before the first tile)
           const float alpha = __builtin_amdgcn_exp2f(m_run[g] - mn);
           l_lane[g] *= alpha;
 #pragma unroll
           for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
-          m_run[g] = mn;
         }
-        l_lane[g] += qhalf == 0 ? p[g] : 0.0f;
+        m_run[g] = mn;
       }
-#pragma unroll
-      for (int g = G; g < 8; ++g) p[g] = 0.0f;
-      if (qhalf == 0) {
-        *(float4*)(s_p + tq * 8) = make_float4(p[0], p[1], p[2], p[3]);
-        *(float4*)(s_p + tq * 8 + 4) = make_float4(p[4], p[5], p[6], p[7]);
-      }
-      wave_lds_sync();
+      l_lane[g] += qh == 0 ? p[g] : 0.0f;
+    }
 
-      // ---- o += p * V, V in load layout ----
+    // ---- p to the load layout through LDS ----
+    if constexpr (PV_DOT2) {
+      uint32_t pk[8];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) pk[g] = g < G ? pack_f16(p[g], upper_half_value<D>(p[g])) : 0u;
+      if (lane < S::HALF) {
+        *(uint4*)(pw + tq * 8) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        *(uint4*)(pw + tq * 8 + 4) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+      }
+    } else {
+      float pf[8];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) pf[g] = g < G ? p[g] : 0.0f;
+      if (qh == 0) {
+        *(float4*)(pw + tq * 8) = make_float4(pf[0], pf[1], pf[2], pf[3]);
+        *(float4*)(pw + tq * 8 + 4) = make_float4(pf[4], pf[5], pf[6], pf[7]);
+      }
+    }
+    wave_lds_sync();
+
+    // ---- o += p * V, V in its load layout ----
+    // tokens past the split: V must contribute exactly zero (p is 0 there,
+    // and 0 * stale data must not produce NaN)
+    const bool partial = t0 + S::TILE > s_end;
+    if constexpr (PV_DOT2) {
+#pragma unroll
+      for (int r = 0; r < S::LOADS / 2; ++r) {
+        const int t = r * S::TPL + pv_tok;  // vr[r]: token t; vr[r + LOADS/2]: t + HALF
+        uint4 va = vr[r], vb = vr[r + S::LOADS / 2];
+        if (partial) {
+          if (t0 + t >= s_end) va = make_uint4(0, 0, 0, 0);
+          if (t0 + t + S::HALF >= s_end) vb = make_uint4(0, 0, 0, 0);
+        }
+        const uint4 p0 = *(const uint4*)(pw + t * 8);
+        const uint4 p1 = *(const uint4*)(pw + t * 8 + 4);
+        const uint32_t pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        const uint32_t aw[4] = {va.x, va.y, va.z, va.w};
+        const uint32_t bw[4] = {vb.x, vb.y, vb.z, vb.w};
+        uint32_t pr[8];  // (v_t[e], v_{t+HALF}[e]) pairs
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pr[2 * e] = __builtin_amdgcn_perm(bw[e], aw[e], 0x05040100u);
+          pr[2 * e + 1] = __builtin_amdgcn_perm(bw[e], aw[e], 0x07060302u);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[g][e] = St<kF16>::dot2(pr[e], pp[g], o[g][e]);
+        LUC_SCHED_FENCE();
+      }
+    } else {
 #pragma unroll
       for (int r = 0; r < S::LOADS; ++r) {
-        const int tok = r * S::GROUPS + pv_tok;
-        const float4 pa = *(const float4*)(s_p + tok * 8);
-        const float4 pb = *(const float4*)(s_p + tok * 8 + 4);
+        const int t = r * S::TPL + pv_tok;
+        uint4 v = vr[r];
+        if (partial && t0 + t >= s_end) v = make_uint4(0, 0, 0, 0);
+        const float4 pa = *(const float4*)(pw + t * 8);
+        const float4 pb = *(const float4*)(pw + t * 8 + 4);
         const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-        const uint32_t vw[4] = {vr[r].x, vr[r].y, vr[r].z, vr[r].w};
+        const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
         float vv[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -337,170 +445,160 @@ __device__ void decode_impl(const DecodeArgs& A, int batch) {
         for (int g = 0; g < G; ++g)
 #pragma unroll
           for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pv[g], vv[e], o[g][e]);
-      }
-      wave_lds_sync();
-    }
-
-    // ---- reduce the wave's token groups: result [G][D] f32 at RES_OFF ----
-    float* scratch = (float*)stage;           // [GROUPS][HP][D]
-    float* res = (float*)(stage + S::RES_OFF);
-#pragma unroll
-    for (int g0 = 0; g0 < G; g0 += S::HP) {
-#pragma unroll
-      for (int j = 0; j < S::HP; ++j) {
-        if (g0 + j < G) {
-          float* dst = scratch + ((int64_t)pv_tok * S::HP + j) * D + pv_chunk * 8;
-          *(float4*)dst = make_float4(o[g0 + j][0], o[g0 + j][1], o[g0 + j][2], o[g0 + j][3]);
-          *(float4*)(dst + 4) = make_float4(o[g0 + j][4], o[g0 + j][5], o[g0 + j][6], o[g0 + j][7]);
-        }
-      }
-      wave_lds_sync();
-      for (int idx = lane; idx < S::HP * D; idx += 64) {
-        if (g0 + idx / D < G) {
-          float sum = 0.0f;
-#pragma unroll
-          for (int gr = 0; gr < S::GROUPS; ++gr) sum += scratch[gr * S::HP * D + idx];
-          res[g0 * D + idx] = sum;
-        }
-      }
-      wave_lds_sync();
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float l = wave_sum(l_lane[g]);
-      if (lane == 0) {
-        s_m[w][g] = m_run[g];
-        s_l[w][g] = l;
+        LUC_SCHED_FENCE();
       }
     }
-    __syncthreads();
-
-    // ---- merge the waves ----
-    const int64_t ws_base = ((int64_t)b * hq + (int64_t)h * G) * A.max_splits;
-    for (int idx = threadIdx.x; idx < G * D; idx += NT) {
-      const int g = idx / D, d = idx % D;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w2 = 0; w2 < S::NW; ++w2) M = fmaxf(M, s_m[w2][g]);
-      float L = 0.0f, acc = 0.0f;
-#pragma unroll
-      for (int w2 = 0; w2 < S::NW; ++w2) {
-        const float sc = __builtin_amdgcn_exp2f(s_m[w2][g] - M);  // 0 for waves without tiles
-        const float* r2 = (const float*)(smem + w2 * S::STAGE + S::RES_OFF);
-        L = fmaf(sc, s_l[w2][g], L);
-        acc = fmaf(sc, r2[g * D + d], acc);
-      }
-      if (nsplit == 1) {
-        out_row[idx] = St<DT>::store(acc / L);
-      } else {
-        const int64_t ws = ws_base + (int64_t)g * A.max_splits + split;
-        A.ws_o[ws * D + d] = acc;
-        if (d == 0) {
-          A.ws_ml[ws * 2] = M;
-          A.ws_ml[ws * 2 + 1] = L;
-        }
-      }
-    }
-    __syncthreads();  // LDS is reused by the next item
+    wave_lds_sync();
   }
-}
 
-// Split merge for one (sequence, kv head); the step variant also writes the
-// roped q (G heads) and k of the new token back into the qkv row.
-template <int DT, int D, int G, bool APPEND>
-__device__ void combine_impl(const DecodeArgs& A) {
-  constexpr int NT = 256;
-  constexpr int MAXS = 256;  // splits per sequence (host-enforced)
-  __shared__ float s_w[G][MAXS];
-  __shared__ float s_L[G];
-  const int b = blockIdx.y, h = blockIdx.x;
-  const int hq = A.hkv * G;
-  const int pos = A.positions[b];
-  const int nsplit = splits_of(pos, A.max_ctx, A.split_tokens);
-  if constexpr (APPEND) {
-    if (nsplit > 0) {
-      constexpr int HALF = D / 2;
-      const float* crow = A.cos_t + (int64_t)pos * HALF;
-      const float* srow = A.sin_t + (int64_t)pos * HALF;
-      uint16_t* qrow = A.q + (int64_t)b * A.q_stride + (int64_t)h * G * D;
-      uint16_t* krow = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
-      const uint16_t* qb = A.q_bias ? A.q_bias + (int64_t)h * G * D : nullptr;
-      const uint16_t* kb = A.k_bias ? A.k_bias + (int64_t)h * D : nullptr;
-      for (int idx = threadIdx.x; idx < (G + 1) * HALF; idx += NT) {
-        const int g = idx / HALF, i = idx % HALF;
-        uint16_t o1, o2;
-        if (g < G) {
-          rot_pair<DT>(qrow, qb, g * D + i, g * D + i + HALF, crow[i], srow[i], o1, o2);
-          qrow[g * D + i] = o1;
-          qrow[g * D + i + HALF] = o2;
-        } else {
-          rot_pair<DT>(krow, kb, i, i + HALF, crow[i], srow[i], o1, o2);
-          krow[i] = o1;
-          krow[i + HALF] = o2;
-        }
-      }
+  // ---- reduce the wave's token groups (lanes sharing pv_ch): reduce-scatter ----
+  constexpr int NV = 8 * G;
+  float u[NV / 2], y[NV / 4];
+#pragma unroll
+  for (int k = 0; k < NV / 2; ++k) {
+    const int k2 = k + NV / 2;
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(o[k / 8][k % 8]),
+                                                    __float_as_uint(o[k2 / 8][k2 % 8]), false, false);
+    u[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int k = 0; k < NV / 4; ++k) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(u[k]),
+                                                    __float_as_uint(u[k + NV / 4]), false, false);
+    y[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (D == 64) {  // token groups also differ in lane bit 3
+#pragma unroll
+    for (int k = 0; k < NV / 4; ++k) y[k] += dpp_mov<0x128>(y[k]);  // row_ror:8
+  }
+  float* red = (float*)(s_k + kbase);  // this wave's [G][D] result (its K tile is done)
+  if (D == 128 || (lane & 8) == 0) {
+    const int base = ((lane >> 5) & 1) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);
+#pragma unroll
+    for (int k = 0; k < NV / 4; ++k) {
+      const int kk = base + k;
+      red[(kk / 8) * D + pv_ch * 8 + (kk % 8)] = y[k];
     }
   }
-  if (nsplit <= 1) return;  // finished by the decode kernel
-  const int64_t ws_base = ((int64_t)b * hq + (int64_t)h * G) * A.max_splits;
-  // per-split weights exp2(m_s - M) and the merged sum per head
-  for (int g = threadIdx.x >> 6; g < G; g += NT / 64) {
-    const int lane = threadIdx.x & 63;
-    const float* ml = A.ws_ml + (ws_base + (int64_t)g * A.max_splits) * 2;
-    float M = -INFINITY;
-    for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, ml[s * 2]);
-    M = wave_max(M);
-    float L = 0.0f;
-    for (int s = lane; s < nsplit; s += 64) {
-      const float wgt = __builtin_amdgcn_exp2f(ml[s * 2] - M);
-      s_w[g][s] = wgt;
-      L = fmaf(wgt, ml[s * 2 + 1], L);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float l = wave_sum(l_lane[g]);
+    if (lane == 0) {
+      s_m[w][g] = m_run[g];
+      s_l[w][g] = l;
     }
-    L = wave_sum(L);
-    if (lane == 0) s_L[g] = L;
   }
   __syncthreads();
-  uint16_t* out_row = A.out + (int64_t)b * A.out_stride + (int64_t)h * G * D;
+
+  // ---- merge the waves ----
+  const int64_t ws_base = ((int64_t)b * hq + (int64_t)h * G) * A.max_splits;
   for (int idx = threadIdx.x; idx < G * D; idx += NT) {
     const int g = idx / D, d = idx % D;
-    const float* op = A.ws_o + (ws_base + (int64_t)g * A.max_splits) * D + d;
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    int s = 0;
-    for (; s + 4 <= nsplit; s += 4) {
-      a0 = fmaf(s_w[g][s], op[(int64_t)s * D], a0);
-      a1 = fmaf(s_w[g][s + 1], op[(int64_t)(s + 1) * D], a1);
-      a2 = fmaf(s_w[g][s + 2], op[(int64_t)(s + 2) * D], a2);
-      a3 = fmaf(s_w[g][s + 3], op[(int64_t)(s + 3) * D], a3);
+    float M = -INFINITY;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) M = fmaxf(M, s_m[w2][g]);
+    float L = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) {
+      const float sc = __builtin_amdgcn_exp2f(s_m[w2][g] - M);  // 0 for waves without tiles
+      L = fmaf(sc, s_l[w2][g], L);
+      acc = fmaf(sc, ((const float*)(s_k + w2 * S::KBYTES))[g * D + d], acc);
     }
-    for (; s < nsplit; ++s) a0 = fmaf(s_w[g][s], op[(int64_t)s * D], a0);
-    out_row[idx] = St<DT>::store(((a0 + a1) + (a2 + a3)) / s_L[g]);
+    if (nsplit == 1) {
+      out_row[idx] = St<DT>::store(acc / L);
+    } else {
+      const int64_t ws = ws_base + (int64_t)g * A.max_splits + split;
+      st_agent(A.ws_o + ws * D + d, acc);
+      if (d == 0) {
+        st_agent(A.ws_ml + ws * 2, M);
+        st_agent(A.ws_ml + ws * 2 + 1, L);
+      }
+    }
+  }
+
+  if (nsplit > 1) {
+    // ---- arrival: the last split of (b, h) merges them all ----
+    // Partials travel through agent-coherent (sc1) stores and loads, so no
+    // L2 write-back is needed: every store of this workgroup has completed
+    // before its arrival is counted, and the last arrival loads after the
+    // count has returned.
+    wait_vmem_all();
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(A.ws_cnt + bh, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(nsplit - 1);
+    __syncthreads();
+    if (!s_last) return;
+    float* s_wt = (float*)s_k;  // [G][256] split weights
+    for (int g = w; g < G; g += NW) {
+      const float* ml = A.ws_ml + (ws_base + (int64_t)g * A.max_splits) * 2;
+      float mv[4], lv[4];  // splits lane, lane+64, ... (at most 256)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int s = lane + 64 * k;
+        mv[k] = s < nsplit ? ld_agent(ml + s * 2) : -INFINITY;
+        lv[k] = s < nsplit ? ld_agent(ml + s * 2 + 1) : 0.0f;
+      }
+      const float M = wave_max(fmaxf(fmaxf(mv[0], mv[1]), fmaxf(mv[2], mv[3])));
+      float L = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int s = lane + 64 * k;
+        const float wgt = __builtin_amdgcn_exp2f(mv[k] - M);  // 0 past nsplit
+        if (s < nsplit) s_wt[g * 256 + s] = wgt;
+        L = fmaf(wgt, lv[k], L);
+      }
+      L = wave_sum(L);
+      if (lane == 0) s_L[g] = L;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * D; idx += NT) {
+      const int g = idx / D, d = idx % D;
+      const float* op = A.ws_o + (ws_base + (int64_t)g * A.max_splits) * D + d;
+      const float* wt = s_wt + g * 256;
+      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+      int s = 0;
+      for (; s + 4 <= nsplit; s += 4) {
+        a0 = fmaf(wt[s], ld_agent(op + (int64_t)s * D), a0);
+        a1 = fmaf(wt[s + 1], ld_agent(op + (int64_t)(s + 1) * D), a1);
+        a2 = fmaf(wt[s + 2], ld_agent(op + (int64_t)(s + 2) * D), a2);
+        a3 = fmaf(wt[s + 3], ld_agent(op + (int64_t)(s + 3) * D), a3);
+      }
+      for (; s < nsplit; ++s) a0 = fmaf(wt[s], ld_agent(op + (int64_t)s * D), a0);
+      out_row[idx] = St<DT>::store(((a0 + a1) + (a2 + a3)) / s_L[g]);
+    }
+    if (threadIdx.x == 0)  // ready for the next launch
+      __hip_atomic_store(A.ws_cnt + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  if constexpr (APPEND) {
+    // every split has read q and k: write the roped values back in place
+    uint16_t* qw = A.q + (int64_t)b * A.q_stride + (int64_t)h * G * D;
+    uint16_t* kw = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
+    for (int i = threadIdx.x; i < G * D; i += NT) qw[i] = s_q[i];
+    for (int i = threadIdx.x; i < D; i += NT) kw[i] = s_knew[i];
   }
 }
 
 }  // namespace luc
 
-// Two resident waves per SIMD (8 per CU, two workgroups): the register budget
-// the decode loop is written for.
-#ifndef LUC_DECODE_OCC
-#define LUC_DECODE_OCC __attribute__((amdgpu_waves_per_eu(2, 2)))
+// Resident-wave targets (waves per SIMD).  fp16 fits three 4-wave workgroups
+// per CU in registers; the bf16 FMA path needs more registers and runs two.
+#ifndef LUC_DECODE_OCC_f16
+#define LUC_DECODE_OCC_f16 __attribute__((amdgpu_waves_per_eu(3)))
+#endif
+#ifndef LUC_DECODE_OCC_bf16
+#define LUC_DECODE_OCC_bf16 __attribute__((amdgpu_waves_per_eu(2)))
 #endif
 
 #define LUC_DECODE(DTN, DT, D, G)                                                                  \
-  extern "C" __global__ __launch_bounds__(256) LUC_DECODE_OCC void luc_decode_##DTN##_d##D##_g##G( \
-      luc::DecodeArgs a, int batch) {                                                              \
-    luc::decode_impl<DT, D, G, false>(a, batch);                                                   \
-  }                                                                                                \
-  extern "C" __global__ __launch_bounds__(256) LUC_DECODE_OCC void luc_decode_step_##DTN##_d##D##_g##G( \
-      luc::DecodeArgs a, int batch) {                                                              \
-    luc::decode_impl<DT, D, G, true>(a, batch);                                                    \
-  }                                                                                                \
-  extern "C" __global__ __launch_bounds__(256) void luc_decode_combine_##DTN##_d##D##_g##G(        \
+  extern "C" __global__ __launch_bounds__(256) LUC_DECODE_OCC_##DTN void luc_decode_##DTN##_d##D##_g##G( \
       luc::DecodeArgs a) {                                                                         \
-    luc::combine_impl<DT, D, G, false>(a);                                                         \
+    luc::decode_impl<DT, D, G, false>(a);                                                          \
   }                                                                                                \
-  extern "C" __global__ __launch_bounds__(256) void luc_decode_step_combine_##DTN##_d##D##_g##G(   \
-      luc::DecodeArgs a) {                                                                         \
-    luc::combine_impl<DT, D, G, true>(a);                                                          \
+  extern "C" __global__ __launch_bounds__(256) LUC_DECODE_OCC_##DTN void                          \
+      luc_decode_step_##DTN##_d##D##_g##G(luc::DecodeArgs a) {                                     \
+    luc::decode_impl<DT, D, G, true>(a);                                                           \
   }
 
 #define LUC_DECODE_GROUPS(DTN, DT, D)                                                              \

@@ -31,7 +31,6 @@ struct luc_ctx {
   int num_cus = 0;
   std::vector<hipModule_t> modules;
   std::unordered_map<std::string, hipFunction_t> fns;
-  std::unordered_map<std::string, int> resident;  // workgroups per CU, decode kernels
 };
 
 namespace {
@@ -169,38 +168,39 @@ int check_cache(const void* k_pool, const void* v_pool, const int32_t* tables, i
   return LUC_OK;
 }
 
-// Splits per sequence are capped at kMaxSplits (the combine kernel's LDS table).
+// Splits per sequence are capped at kMaxSplits (the merge's LDS weight table).
 constexpr int kMaxSplits = 256;
 
+// Split-K chunk length in tokens: a multiple of the wave tile.  The automatic
+// choice assumes the mean context is half of max_ctx and aims at about two
+// resident workgroups per CU on a kPlanCUs-CU device.  It depends only on the
+// arguments, so luc_paged_decode_workspace_size agrees with the launch.
 int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requested) {
   const int tile = decode_tile(head_dim);
   const int64_t floor_tokens = ceil_div(ceil_div(max_ctx, kMaxSplits), tile) * tile;
   if (requested > 0) return (int)std::max<int64_t>(ceil_div(requested, tile) * tile, floor_tokens);
-  // Plan for ~4 active workgroups per CU, assuming the average context is
-  // half of max_ctx; each wave then walks `tpw` tiles of its split.
   const int64_t wg_tokens = (int64_t)kDecodeWaves * tile;
-  const int64_t est = (int64_t)batch * hkv * ceil_div(std::max(max_ctx / 2, 1), wg_tokens);
-  int64_t tpw = est / (4 * kPlanCUs);
-  if (tpw < 1) tpw = 1;
-  if (tpw > 64) tpw = 64;
-  return (int)std::max<int64_t>(tpw * wg_tokens, floor_tokens);
+  const int64_t est = (int64_t)batch * hkv * std::max<int64_t>(ceil_div(max_ctx, 2), 1);
+  const int64_t st = ceil_div(ceil_div(est, 2 * kPlanCUs), wg_tokens) * wg_tokens;
+  return (int)std::max<int64_t>(st, floor_tokens);
 }
 
-// Workspace layout: [(max, sum) per (b, q-head, split): f32 x2]
+// Workspace layout: [arrival counter per (b, kv head): u32, padded to 256 B]
+//                   [(max, sum) per (b, q-head, split): f32 x2]
 //                   [o per (b, q-head, split): f32 x head_dim]
-size_t workspace_bytes_for(int batch, int hq, int head_dim, int max_ctx, int split_tokens) {
+int64_t counter_bytes(int batch, int hkv) { return ceil_div((int64_t)batch * hkv, 64) * 256; }
+
+size_t workspace_bytes_for(int batch, int hq, int hkv, int head_dim, int max_ctx, int split_tokens) {
   const int64_t max_splits = ceil_div(max_ctx, split_tokens);
   if (max_splits <= 1) return 0;
-  return (size_t)batch * hq * max_splits * (head_dim + 2) * sizeof(float);
+  return (size_t)counter_bytes(batch, hkv) +
+         (size_t)batch * hq * max_splits * (head_dim + 2) * sizeof(float);
 }
 
 struct DecodeLaunch {
   luc_decode_args a{};
   hipFunction_t fn = nullptr;
-  hipFunction_t combine = nullptr;
   dim3 grid;
-  int batch = 0;
-  bool need_combine = false;
 };
 
 // Shared argument checks and argument block of the two decode entry points.
@@ -229,26 +229,21 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
 
   const int st = split_tokens_for(batch, num_kv_heads, head_dim, max_ctx, split_tokens);
   const int max_splits = (int)ceil_div(max_ctx, st);
-  const size_t need = workspace_bytes_for(batch, num_q_heads, head_dim, max_ctx, st);
+  const size_t need =
+      workspace_bytes_for(batch, num_q_heads, num_kv_heads, head_dim, max_ctx, st);
   if (need && (!workspace || workspace_bytes < need))
     return fail(LUC_E_WORKSPACE, "workspace %zu bytes, %zu needed", workspace_bytes, need);
   if (need && !aligned(workspace, 256)) return fail(LUC_E_INVALID, "workspace must be 256-byte aligned");
+  const int64_t grid = (int64_t)max_splits * batch * num_kv_heads;
+  if (grid > INT32_MAX) return fail(LUC_E_INVALID, "batch x kv heads x splits too large");
 
   if (batch == 0) return LUC_OK;  // nothing to launch
   const int group = num_q_heads / num_kv_heads;
-  const std::string suffix = std::string(dt_name(dtype)) + "_d" + std::to_string(head_dim) + "_g" +
-                             std::to_string(group);
-  const std::string name = std::string(step ? "luc_decode_step_" : "luc_decode_") + suffix;
+  const std::string name = std::string(step ? "luc_decode_step_" : "luc_decode_") +
+                           dt_name(dtype) + "_d" + std::to_string(head_dim) + "_g" +
+                           std::to_string(group);
   if (int rc = get_fn(ctx, name, &L->fn)) return rc;
-  if (int rc = get_fn(ctx, std::string(step ? "luc_decode_step_combine_" : "luc_decode_combine_") +
-                               suffix, &L->combine))
-    return rc;
-  // persistent grid: no more workgroups than can be resident at once
-  const int64_t items = (int64_t)batch * num_kv_heads * max_splits;
-  const int64_t slots = (int64_t)ctx->num_cus * ctx->resident.at(name);
-  L->grid = dim3((unsigned)std::min(items, slots));
-  L->batch = batch;
-  L->need_combine = step || max_splits > 1;
+  L->grid = dim3((unsigned)grid);
   luc_decode_args& a = L->a;
   a.q = static_cast<uint16_t*>(const_cast<void*>(q));
   a.q_stride = q_row_stride;
@@ -257,6 +252,7 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
   a.tables = block_tables;
   a.table_stride = table_stride;
   a.positions = positions;
+  a.batch = batch;
   a.layer = layer;
   a.num_layers = num_layers;
   a.hkv = num_kv_heads;
@@ -265,7 +261,9 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
   a.split_tokens = st;
   a.max_splits = max_splits;
   if (need) {
-    a.ws_ml = static_cast<float*>(workspace);
+    char* ws = static_cast<char*>(workspace);
+    a.ws_cnt = reinterpret_cast<uint32_t*>(ws);
+    a.ws_ml = reinterpret_cast<float*>(ws + counter_bytes(batch, num_kv_heads));
     a.ws_o = a.ws_ml + (size_t)batch * num_q_heads * max_splits * 2;
   }
   a.out = static_cast<uint16_t*>(out);
@@ -274,11 +272,8 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
 }
 
 int launch_decode(DecodeLaunch& L, void* stream) {
-  void* args[] = {&L.a, &L.batch};
-  if (int rc = launch(L.fn, L.grid, dim3(kDecodeWaves * 64), stream, args)) return rc;
-  if (!L.need_combine) return LUC_OK;
-  void* cargs[] = {&L.a};
-  return launch(L.combine, dim3(L.a.hkv, L.batch), dim3(256), stream, cargs);
+  void* args[] = {&L.a};
+  return launch(L.fn, L.grid, dim3(kDecodeWaves * 64), stream, args);
 }
 
 }  // namespace
@@ -315,8 +310,7 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
     names.push_back(std::string("luc_rope_append_") + dt);
     for (int d : {64, 128})
       for (int g = 1; g <= 8; ++g)
-        for (const char* kind : {"luc_decode_", "luc_decode_step_", "luc_decode_combine_",
-                                 "luc_decode_step_combine_"})
+        for (const char* kind : {"luc_decode_", "luc_decode_step_"})
           names.push_back(std::string(kind) + dt + "_d" + std::to_string(d) + "_g" +
                           std::to_string(g));
   }
@@ -329,14 +323,6 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
       return fail(LUC_E_LOAD, "kernel %s not found in %s", n.c_str(), dir.c_str());
     }
     ctx->fns[n] = fn;
-    if (n.rfind("luc_decode_", 0) == 0 && n.find("combine") == std::string::npos) {
-      int per_cu = 0;
-      if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDecodeWaves * 64, 0) !=
-              hipSuccess ||
-          per_cu < 1)
-        per_cu = 1;
-      ctx->resident[n] = per_cu;
-    }
   }
   if (hipDeviceGetAttribute(&ctx->num_cus, hipDeviceAttributeMultiprocessorCount, device) !=
           hipSuccess ||
@@ -442,7 +428,7 @@ size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_he
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_ctx <= 0) return 0;
   if (head_dim != 64 && head_dim != 128) return 0;
   const int st = split_tokens_for(batch, num_kv_heads, head_dim, max_ctx, split_tokens);
-  return workspace_bytes_for(batch, num_q_heads, head_dim, max_ctx, st);
+  return workspace_bytes_for(batch, num_q_heads, num_kv_heads, head_dim, max_ctx, st);
 }
 
 int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t out_row_stride,

@@ -91,16 +91,25 @@ def test_decode_argument_checks(cdll):
 
 def test_workspace_size_policy(cdll):
     ws = cdll.luc_paged_decode_workspace_size
+
+    def expect(batch, hq, hkv, d, splits):
+        # arrival counters (u32 per sequence x kv head, padded to 256 B), then
+        # (max, sum) and o[d] in f32 per (sequence, q-head, split)
+        counters = -(-batch * hkv // 64) * 256
+        return counters + batch * hq * splits * (d + 2) * 4
+
     # one split per sequence -> no workspace
     assert ws(32, 14, 2, 64, 100, 0) == 0
-    # explicit split size: B*Hq*splits*(d+2)*4
-    assert ws(2, 14, 2, 64, 1000, 256) == 2 * 14 * 4 * 66 * 4
-    assert ws(100, 28, 4, 128, 1000, 128) == 100 * 28 * 8 * 130 * 4
+    assert ws(2, 14, 2, 64, 1000, 256) == expect(2, 14, 2, 64, 4)
+    assert ws(100, 28, 4, 128, 1000, 128) == expect(100, 28, 4, 128, 8)
     # at most 256 splits per sequence: the split grows with the context
-    assert ws(1, 4, 1, 64, 64 * 1024, 64) == 1 * 4 * 256 * 66 * 4
-    # rounding of the requested split to the tile (64 for d=64)
+    assert ws(1, 4, 1, 64, 64 * 1024, 64) == expect(1, 4, 1, 64, 256)
+    # rounding of the requested split to the tile (64 tokens at d=64, 32 at d=128)
     assert ws(2, 14, 2, 64, 1000, 250) == ws(2, 14, 2, 64, 1000, 256)
+    assert ws(2, 14, 2, 128, 1000, 90) == ws(2, 14, 2, 128, 1000, 96)
     assert ws(1, 4, 1, 96, 1000, 0) == 0
+    # the automatic split aims at ~2 workgroups per CU of 256 CUs
+    assert ws(32, 14, 2, 64, 4096, 0) == expect(32, 14, 2, 64, 16)
 
 
 def test_rope_table_entry_point_matches_oracle(orc, cdll):
