@@ -22,9 +22,8 @@ struct luc_decode_args {
   int32_t batch, layer, num_layers, hkv;
   float qk_scale_log2;      // sm_scale * log2(e)
   int32_t max_ctx, split_tokens, max_splits;
-  uint32_t* ws_cnt;         // [batch*Hkv] arrival counters (zero between launches)
-  float* ws_ml;             // [batch*Hq*max_splits][2]  (max, sum) per split
-  float* ws_o;              // [batch*Hq*max_splits][head_dim]
+  float* ws_ml;             // [batch*Hkv][max_splits][G][2]  (max, sum) per split
+  float* ws_o;              // [batch*Hkv][max_splits][G*head_dim]
   uint16_t* out;            // row b at out + b*out_stride, [Hq*head_dim]
   int64_t out_stride;
 };

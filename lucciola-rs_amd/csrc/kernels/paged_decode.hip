@@ -14,31 +14,41 @@
 // v + v_bias (src/kernels/kv_cache.cu).  Attention takes the new token's K/V
 // from LDS, so it does not depend on the order of the cache write.
 //
-// One launch per step.  Work decomposition:
-//   Workgroup = (split, sequence b, kv head h), split-major, so the splits
-//   every sequence has (split 0, 1, ...) are dispatched first and the
-//   workgroups of splits past a context exit at once.  A workgroup is 4
-//   waves; the G = Hq/Hkv q-heads of kv head h are processed together, so
-//   each KV page is read from HBM once per kv head (GQA).
-//   Prologue: positions[b], the wave's block-table entries and q are loaded
-//   together (one memory round trip before the KV stream).
-//   A wave walks 8 KB tiles of K (64 tokens at head_dim 64, 32 at 128):
+// Two launches per step: the split-K decode kernel, then the log-sum-exp
+// combine kernel.
+//
+// Decode kernel work decomposition:
+//   Workgroup = one wave = (split, sequence b, kv head h), split-major, so the
+//   splits every sequence has are dispatched first and the workgroups of
+//   splits past a context exit at once.  The G = Hq/Hkv q-heads of kv head h
+//   are processed together, so each KV page is read from HBM once per kv
+//   head (GQA).
+//   Prologue: positions[b], the split's block-table entries and q are loaded
+//   together (one memory round trip before the KV stream).  q stays in 2G
+//   registers, spread so that DPP row_newbcast hands every lane the q word it
+//   needs as an operand of v_dot2c (no LDS traffic for q).
+//   The wave walks its split in 8 KB tiles of K (64 tokens at head_dim 64, 32
+//   at 128), in pairs: both tiles of a pair are issued, tile i is computed
+//   while tile i+1 lands.  Per tile:
 //     1. K goes straight from HBM into LDS (global_load_lds_dwordx4; one
 //        wave-wide load = 1 KB of a page), each token row XOR-swizzled by
 //        16-byte chunk so the per-token LDS reads are conflict-free; V goes
 //        to registers in the same load layout (lane = token x 16-byte chunk).
+//        All K loads of a tile precede its V loads, so the scores start as
+//        soon as K has landed.
 //     2. Scores: lane = token (x2 lanes per token at head_dim 128), all G
-//        heads with v_dot2_f32_{f16,bf16}, q broadcast from LDS.
-//     3. Online softmax in the exp2 domain: wave max by DPP row reductions +
-//        readlane; o rescaled only when the running max moves.
+//        heads with v_dot2c_f32_{f16,bf16}, q by DPP broadcast.
+//     3. Online softmax in the exp2 domain, wave max by a DPP reduction; o is
+//        rescaled only when the running max moves.
 //     4. o += p * V with V in its load layout.  fp16: p of tokens t and
 //        t + TILE/2 packed as an fp16 pair, V of the same two tokens paired by
 //        v_perm, one v_dot2_f32_f16 per (head, dim).  bf16: f32 FMA.
-//   The wave's token groups are reduced with permlane swaps (reduce-scatter)
-//   and the 4 waves merge through LDS.  A sequence with one split writes its
-//   output; otherwise each split writes (m, l, o) to the workspace, and the
-//   last split to arrive (an agent-scope arrival counter per (b, h)) merges
-//   all splits with the log-sum-exp rule and resets the counter.
+//   The wave's token groups are reduced with permlane swaps (reduce-scatter).
+//   A sequence with one split writes its output; otherwise each split writes
+//   (m, l, o) to the workspace.
+// Combine kernel: one workgroup per (sequence, kv head) merges the splits
+// with the log-sum-exp rule.  The step variant also writes the roped q and k
+// of the new token back in place (after every split has read them).
 #include "decode_args.h"
 #include "luc_common.h"
 
@@ -50,31 +60,25 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 template <int D>
 struct DecodeGeo {
-  static constexpr int NW = 4;                 // waves per workgroup
   static constexpr int CH = D / 8;             // 16-byte chunks per token row
   static constexpr int TPL = 64 / CH;          // tokens per wave-wide 16-byte load
-  static constexpr int TILE = 512 / CH;        // tokens per wave tile (8 KB of K)
+  static constexpr int TILE = 512 / CH;        // tokens per tile (8 KB of K)
   static constexpr int LOADS = TILE / TPL;     // K (and V) loads per lane per tile
   static constexpr int HALF = TILE / 2;        // PV pairs tokens t and t + HALF
   static constexpr int QKL = 64 / TILE;        // lanes per token for the scores
   static constexpr int LPP = kPage / TPL;      // load instructions per page
   static constexpr int PAGES = TILE / kPage;   // pages per tile
   static constexpr int ROWB = D * 2;           // bytes per token row
-  static constexpr int KBYTES = TILE * ROWB;   // LDS bytes of one wave's K tile
+  static constexpr int KBYTES = TILE * ROWB;   // LDS bytes of one K tile
   static_assert(LOADS == 8 && TPL * ROWB == 1024, "one wave-wide load is 1 KB");
 };
 
 constexpr int kCpolNT = 2;  // non-temporal load: the KV stream is read once per step
 
-#ifndef LUC_SCHED_FENCE
-#define LUC_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
-#endif
-
-// Wait until this wave has no vector memory operation in flight (also covers
-// the LDS writes of global_load_lds, which the compiler does not track).
-__device__ inline void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-// ... until at most 8 (the V loads of a tile) are still in flight.
-__device__ inline void wait_vmcnt_loads() { asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); }
+// Wait until at most N vector memory operations of this wave are in flight.
+// They complete in issue order, so this also covers the LDS writes of
+// global_load_lds, which the compiler does not track.
+#define LUC_WAIT_VM(N) asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory")
 
 // 16 bytes per lane from global memory straight into LDS at l + 16*lane + rb;
 // rb (the instruction offset) also moves the global address.  rb must fold
@@ -88,17 +92,67 @@ __device__ inline void dma16(const char* g, lds_char* l, int rb) {
   }
 }
 
-// Agent-coherent (sc1) f32 store / load: visible across the XCDs' L2 caches
-// without a cache write-back.
-__device__ inline void st_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline float ld_agent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Four 16-byte LDS reads, complete on return.  Written as one asm block so
+// the compiler does not see them as reads of memory that global_load_lds may
+// still be writing (it would wait for every outstanding load first); the
+// caller orders them after the loads they need with LUC_WAIT_VM.
+__device__ inline void lds_read4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint4 (&x)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %5\n\t"
+      "ds_read_b128 %2, %6\n\t"
+      "ds_read_b128 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3])
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "memory");
 }
 
-__device__ inline uint4 lds_ld16(const char* base, int off) {
-  return *(const uint4*)(base + off);
+// 32-bit LDS address of a pointer into a __shared__ array.
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_char*)p;
+}
+
+// acc + sum over 16 dwords j of dot2(q word j, k[j]), where q word j is lane
+// j of this lane's 16-lane row of register qd (DPP row_newbcast).  The
+// compiler does not see the instructions inside the asm, so the block pads
+// both hazards itself: s_nop 1 before (a VALU write of qd just before a DPP
+// read of it needs 2 wait states) and s_nop 2 after (a v_dot result read by
+// any VALU instruction other than the same dot reading it as accumulator
+// needs 3 wait states; without them the next instruction can read a stale
+// accumulator).
+#define LUC_DOT16(OP)                                                                     \
+  "s_nop 1\n\t"                                                                           \
+  OP " %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"                        \
+  OP " %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"                        \
+  OP " %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"                        \
+  OP " %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"                        \
+  OP " %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"                        \
+  OP " %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"                        \
+  OP " %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"                        \
+  OP " %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"                        \
+  OP " %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"                       \
+  OP " %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"                       \
+  OP " %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"                      \
+  OP " %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"                      \
+  OP " %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"                      \
+  OP " %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"                      \
+  OP " %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"                      \
+  OP " %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"                      \
+  "s_nop 2"
+#define LUC_DOT16_ARGS(acc, qd, k)                                                        \
+  : "+v"(acc)                                                                            \
+  : "v"(qd), "v"(k[0].x), "v"(k[0].y), "v"(k[0].z), "v"(k[0].w), "v"(k[1].x), "v"(k[1].y), \
+    "v"(k[1].z), "v"(k[1].w), "v"(k[2].x), "v"(k[2].y), "v"(k[2].z), "v"(k[2].w),          \
+    "v"(k[3].x), "v"(k[3].y), "v"(k[3].z), "v"(k[3].w)
+template <int DT>
+__device__ inline float dot16_bcast(float acc, uint32_t qd, const uint4 (&k)[4]) {
+  if constexpr (DT == kF16) {
+    asm(LUC_DOT16("v_dot2c_f32_f16_dpp") LUC_DOT16_ARGS(acc, qd, k));
+  } else {
+    asm(LUC_DOT16("v_dot2c_f32_bf16_dpp") LUC_DOT16_ARGS(acc, qd, k));
+  }
+  return acc;
 }
 
 // Bias + RoPE of one pair (x1, x2) in f32, each product and the
@@ -133,67 +187,81 @@ __device__ inline uint32_t pack_f16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// x[i] for a wave-uniform runtime i < N, without indexing a register array.
+template <int N>
+__device__ __attribute__((always_inline)) inline float pick(const float (&x)[N], int i) {
+  float r = x[0];
+#pragma unroll
+  for (int k = 1; k < N; ++k) r = i == k ? x[k] : r;
+  return r;
+}
+
 template <int DT, int D, int G, bool APPEND>
 __device__ void decode_impl(const DecodeArgs& A) {
   using S = DecodeGeo<D>;
-  constexpr int NW = S::NW, NT = NW * 64;
   constexpr bool PV_DOT2 = (DT == kF16);
-  constexpr int PWORDS = (PV_DOT2 ? S::HALF : S::TILE) * 8;  // per-wave p exchange, 32-bit words
+  constexpr int PWORDS = (PV_DOT2 ? S::HALF : S::TILE) * 8;  // p exchange, 32-bit words
   constexpr int HD = D / 2;
-  __shared__ __attribute__((aligned(16))) char s_k[NW * S::KBYTES];
-  __shared__ __attribute__((aligned(16))) uint32_t s_p[NW * PWORDS];
-  __shared__ __attribute__((aligned(16))) uint16_t s_q[G * D];
+  constexpr int GD = G * D;
+  constexpr int NV = 8 * G;  // o values per lane: 8 dims x G heads
+  // K tiles, double-buffered.  Two arrays (not one of twice the size) so the
+  // compiler can tell which outstanding global_load_lds a read depends on.
+  __shared__ __attribute__((aligned(16))) char s_k0[S::KBYTES];
+  __shared__ __attribute__((aligned(16))) char s_k1[S::KBYTES];
+  __shared__ __attribute__((aligned(16))) uint32_t s_p[PWORDS];
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[GD];
   __shared__ __attribute__((aligned(16))) uint16_t s_knew[D];
   __shared__ __attribute__((aligned(16))) uint16_t s_vnew[D];
-  __shared__ float s_m[NW][8], s_l[NW][8], s_L[8];
-  __shared__ int s_last;
 
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x;
   const int pairs = A.batch * A.hkv;
   const int split = blockIdx.x / pairs;
   const int bh = blockIdx.x - split * pairs;
   const int b = bh / A.hkv, h = bh - b * A.hkv;
-  const int hq = A.hkv * G;
   const int ST = A.split_tokens;
   const int s_begin = split * ST;
   const int64_t page_stride = (int64_t)A.num_layers * A.hkv * kPage * D;
   const int64_t head_off = ((int64_t)A.layer * A.hkv + h) * kPage * D;
   const int* trow = A.tables + (int64_t)b * A.table_stride;
   const int tmax = (int)A.table_stride - 1;
-  uint16_t* out_row = A.out + (int64_t)b * A.out_stride + (int64_t)h * G * D;
-  const uint16_t* qrow = A.q + (int64_t)b * A.q_stride + (int64_t)h * G * D;
+  uint16_t* out_row = A.out + (int64_t)b * A.out_stride + (int64_t)h * GD;
+  const uint16_t* qrow = A.q + (int64_t)b * A.q_stride + (int64_t)h * GD;
 
-  // ---- prologue: position, this wave's first table entries and q together ----
-  const int t_first = s_begin + w * S::TILE;
-  int tab = 0;  // lane j < PAGES: physical page j of the wave's current tile
-  if (lane < S::PAGES) tab = trow[min(t_first / kPage + lane, tmax)];
-  uint32_t qv[(G * D / 2 + NT - 1) / NT];
+  // ---- prologue: position, the split's table entries and q together ----
+  const int p0 = s_begin / kPage;  // lane j of tab0 / tab1: page j / 64 + j of the split
+  const int tab0 = trow[min(p0 + lane, tmax)];
+  const int tab1 = ST > 64 * kPage ? trow[min(p0 + 64 + lane, tmax)] : 0;
+  // q registers: qd[2g + hc], lane (row-half qhalf, j = lane % 16) holds q
+  // word g * D/2 + qhalf * 32 + hc * 16 + j of the row (32-bit words), where
+  // qhalf = lane / 32 at head_dim 128 (the lane's 64 dims), else 0.
+  const int qhalf = D == 128 ? lane / 32 : 0;
+  auto q_word = [&](int m) { return (m / 2) * HD + qhalf * 32 + (m % 2) * 16 + (lane & 15); };
+  uint32_t qd[2 * G];
   if constexpr (!APPEND) {
 #pragma unroll
-    for (int i = 0; i < (G * D / 2 + NT - 1) / NT; ++i) {
-      const int idx = threadIdx.x + i * NT;
-      if (idx < G * D / 2) qv[i] = ((const uint32_t*)qrow)[idx];
-    }
+    for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)qrow)[q_word(m)];
   }
   const int pos = A.positions[b];
   const int ctx = pos + 1;
   if (ctx < 1 || ctx > A.max_ctx) {
     // empty context (0/0 in the reference) or beyond the host bound: NaN
     if (split == 0)
-      for (int i = threadIdx.x; i < G * D; i += NT) out_row[i] = St<DT>::store(__builtin_nanf(""));
+      for (int i = lane; i < GD; i += 64) out_row[i] = St<DT>::store(__builtin_nanf(""));
     return;
   }
   if (s_begin >= ctx) return;  // split past this context
   const int nsplit = (ctx + ST - 1) / ST;
   const int s_end = min(ctx, s_begin + ST);
   const bool owns = APPEND && pos < s_end;  // the split holding the new token
+  auto page_of = [&](int j) -> int64_t {     // physical page j of the split (uniform j)
+    return j < 64 ? __builtin_amdgcn_readlane(tab0, j) : __builtin_amdgcn_readlane(tab1, j - 64);
+  };
 
   // The step variant's prologue operands (q and k of the new token with their
   // biases, the cos/sin row, v + v_bias) are loaded before the KV stream is
   // issued, so using them does not wait for it.
-  constexpr int NPAIR = APPEND ? ((G + 1) * HD + NT - 1) / NT : 1;
-  uint16_t rx1[NPAIR], rx2[NPAIR], rb1[NPAIR], rb2[NPAIR], rv = 0, rvb = 0;
+  constexpr int NPAIR = APPEND ? ((G + 1) * HD + 63) / 64 : 1;
+  uint16_t rx1[NPAIR], rx2[NPAIR], rb1[NPAIR], rb2[NPAIR], rv[S::QKL], rvb[S::QKL];
   float rc[NPAIR], rs[NPAIR];
   if constexpr (APPEND) {
     const float* crow = A.cos_t + (int64_t)pos * HD;
@@ -201,7 +269,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
     const uint16_t* krow = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
 #pragma unroll
     for (int i = 0; i < NPAIR; ++i) {
-      const int idx = min(threadIdx.x + i * NT, (G + 1) * HD - 1);
+      const int idx = min(lane + i * 64, (G + 1) * HD - 1);
       const int g = idx / HD, j = idx % HD;
       const uint16_t* x = g < G ? qrow + g * D : krow;
       const uint16_t* bias = g < G ? (A.q_bias ? A.q_bias + ((int64_t)h * G + g) * D : nullptr)
@@ -213,9 +281,11 @@ __device__ void decode_impl(const DecodeArgs& A) {
       rc[i] = crow[j];
       rs[i] = srow[j];
     }
-    if (threadIdx.x < D) {
-      rv = A.v_new[(int64_t)b * A.q_stride + (int64_t)h * D + threadIdx.x];
-      if (A.v_bias) rvb = A.v_bias[(int64_t)h * D + threadIdx.x];
+#pragma unroll
+    for (int i = 0; i < S::QKL; ++i) {
+      const int d = lane + 64 * i;
+      rv[i] = A.v_new[(int64_t)b * A.q_stride + (int64_t)h * D + d];
+      rvb[i] = A.v_bias ? A.v_bias[(int64_t)h * D + d] : 0;
     }
   }
 
@@ -223,8 +293,6 @@ __device__ void decode_impl(const DecodeArgs& A) {
   const int qh = lane / S::TILE;     // scores: which 64 dims (head_dim 128)
   const int pv_tok = lane / S::CH;   // load layout: token within a load
   const int pv_ch = lane % S::CH;    // load layout: 16-byte chunk of the row
-  const int kbase = w * S::KBYTES;   // this wave's K tile in s_k
-  lds_char* const kdma = (lds_char*)s_k + kbase;
 
   // Per-lane byte offsets inside a (page, layer, kv head) slab.  Load r reads
   // page r / LPP at + (r % LPP) * 1KB; the K slot pv_ch of token tl holds
@@ -235,34 +303,48 @@ __device__ void decode_impl(const DecodeArgs& A) {
   };
   const uint32_t koff0 = k_lane_off(0), koff1 = k_lane_off(1);
   const uint32_t voff = (uint32_t)(pv_tok * S::ROWB + (pv_ch << 4));
-  uint4 vr[S::LOADS];
-  // All K loads of a tile go out before its V loads, so the scores can start
-  // as soon as K has landed (vmcnt <= LOADS) while V is still in flight.  Pages
-  // past the split re-read the tile's last valid page (a cache hit), which
-  // keeps the number of loads per tile fixed.
-  auto issue = [&](int t0) {
-    const int jlast = min(S::PAGES - 1, (s_end - 1 - t0) / kPage);
+
+  // Issue one tile: all its K loads (into the LDS buffer) before its V loads
+  // (into vr).  Pages past the split re-read the split's last page (a cache
+  // hit), which keeps the number of loads per tile fixed at 8 + 8; a tile
+  // that starts past the split (the odd tile of a pair) is all such pages.
+  const int jend = (s_end - 1 - s_begin) / kPage;  // last page of the split
+  auto issue = [&](int t0, int buf, uint4(&vr)[S::LOADS]) __attribute__((always_inline)) {
+    const int jbase = (t0 - s_begin) / kPage;
+    lds_char* kdma = (lds_char*)(buf ? s_k1 : s_k0);
 #pragma unroll
     for (int r = 0; r < S::LOADS; ++r) {
-      const int64_t phys = __builtin_amdgcn_readlane(tab, min(r / S::LPP, jlast));
+      const int64_t phys = page_of(min(jbase + r / S::LPP, jend));
       // wave-uniform slab base (scalar registers) + 32-bit lane offsets
       const char* kslab = (const char*)(A.k_pool + phys * page_stride + head_off);
-      dma16(kslab + ((r & 1) ? koff1 : koff0), kdma + (r - r % S::LPP) * 1024, (r % S::LPP) * 1024);
+      dma16(kslab + ((r & 1) ? koff1 : koff0), kdma + (r - r % S::LPP) * 1024,
+            (r % S::LPP) * 1024);
     }
 #pragma unroll
     for (int r = 0; r < S::LOADS; ++r) {
-      const int64_t phys = __builtin_amdgcn_readlane(tab, min(r / S::LPP, jlast));
+      const int64_t phys = page_of(min(jbase + r / S::LPP, jend));
       const char* vslab = (const char*)(A.v_pool + phys * page_stride + head_off);
       vr[r] = ld_nt16((const uint16_t*)(vslab + voff + (r % S::LPP) * 1024));
     }
   };
-  if (t_first < s_end) issue(t_first);
+
+  const int nt = (s_end - s_begin + S::TILE - 1) / S::TILE;
+  if constexpr (!APPEND) {
+    // q must have landed before the KV stream is issued (it came with the
+    // table and position loads): the compiler then needs no wait for it
+    // behind the stream.
+#pragma unroll
+    for (int m = 0; m < 2 * G; ++m) asm volatile("" ::"v"(qd[m]));
+  }
+  uint4 vr0[S::LOADS], vr1[S::LOADS];
+  issue(s_begin, 0, vr0);
+  issue(s_begin + S::TILE, 1, vr1);
 
   // ---- q of the G heads (roped in the step variant), new token's k, v ----
   if constexpr (APPEND) {
 #pragma unroll
     for (int i = 0; i < NPAIR; ++i) {
-      const int idx = threadIdx.x + i * NT;
+      const int idx = lane + i * 64;
       if (idx < (G + 1) * HD) {
         const int g = idx / HD, j = idx % HD;
         uint16_t o1, o2;
@@ -272,15 +354,13 @@ __device__ void decode_impl(const DecodeArgs& A) {
         dst[j + HD] = o2;
       }
     }
-    if (threadIdx.x < D) s_vnew[threadIdx.x] = St<DT>::store(St<DT>::load(rv) + St<DT>::load(rvb));
-  } else {
 #pragma unroll
-    for (int i = 0; i < (G * D / 2 + NT - 1) / NT; ++i) {
-      const int idx = threadIdx.x + i * NT;
-      if (idx < G * D / 2) ((uint32_t*)s_q)[idx] = qv[i];
-    }
+    for (int i = 0; i < S::QKL; ++i)
+      s_vnew[lane + 64 * i] = St<DT>::store(St<DT>::load(rv[i]) + St<DT>::load(rvb[i]));
+    wave_lds_sync();
+#pragma unroll
+    for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)s_q)[q_word(m)];
   }
-  __syncthreads();
 
   float m_run[G], l_lane[G], o[G][8];
 #pragma unroll
@@ -290,59 +370,30 @@ __device__ void decode_impl(const DecodeArgs& A) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
   }
-  uint32_t* const pw = s_p + w * PWORDS;
 
-  for (int t0 = t_first; t0 < s_end; t0 += NW * S::TILE) {
-    if (t0 != t_first) issue(t0);
-    wait_vmcnt_loads();  // K in LDS (V may still be in flight)
+  // ---- scores, online softmax and p exchange of the tile at t0 (K in buf) ----
+  auto tile_scores = [&](int t0, int buf) __attribute__((always_inline)) {
+    char* const kb = buf ? s_k1 : s_k0;
     if constexpr (APPEND) {
-      if (owns && pos >= t0 && pos < t0 + S::TILE) {  // this tile holds the new token
-        const int t = pos - t0;
-        if (lane < S::CH) {
-          // its K row in LDS, V in registers, and the cache write of both
-          *(uint4*)(s_k + kbase + t * S::ROWB + lane * 16) =
-              *(const uint4*)(s_knew + ((lane ^ (t & 7)) * 8));
-          const int64_t phys = __builtin_amdgcn_readlane(tab, t / kPage);
-          const int64_t slot = phys * page_stride + head_off + (int64_t)(t % kPage) * D + lane * 8;
-          *(uint4*)(A.k_pool + slot) = *(const uint4*)(s_knew + lane * 8);
-          *(uint4*)(A.v_pool + slot) = *(const uint4*)(s_vnew + lane * 8);
-        }
-#pragma unroll
-        for (int r = 0; r < S::LOADS; ++r)
-          if (r == t / S::TPL && pv_tok == t % S::TPL) vr[r] = *(const uint4*)(s_vnew + pv_ch * 8);
+      if (owns && pos >= t0 && pos < t0 + S::TILE && lane < S::CH) {
+        const int t = pos - t0;  // the new token's K row (swizzled slots)
+        *(uint4*)(kb + t * S::ROWB + lane * 16) =
+            *(const uint4*)(s_knew + ((lane ^ (t & 7)) * 8));
       }
+      wave_lds_sync();
     }
-    {  // the next tile's table entries, while this tile computes
-      const int t_next = t0 + NW * S::TILE;
-      if (t_next < s_end && lane < S::PAGES) tab = trow[min(t_next / kPage + lane, tmax)];
-    }
-    wave_lds_sync();
-
-    // ---- scores: lane = token (x2 lanes per token at head_dim 128) ----
     float acc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] = 0.0f;
-    const int krow = kbase + tq * S::ROWB;
+    const uint32_t krow = lds_addr(kb) + tq * S::ROWB;
     const int sw = tq & 7;
-    // q is re-read from LDS every tile: an opaque zero offset keeps the
-    // compiler from hoisting G*D/8 loop-invariant 16-byte values into registers.
-    int qz;
-    asm volatile("s_mov_b32 %0, 0" : "=s"(qz));
-    const uint16_t* qb = s_q + qz + qh * 64;
-#pragma unroll 2
-    for (int c = 0; c < 8; ++c) {
-      const uint4 kc = lds_ld16(s_k, krow + (((qh * 8 + c) ^ sw) << 4));
+    auto ka = [&](int c) { return krow + ((uint32_t)((qh * 8 + c) ^ sw) << 4); };
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const uint4 qc = *(const uint4*)(qb + g * D + c * 8);
-        float a = acc[g];
-        a = St<DT>::dot2(qc.x, kc.x, a);
-        a = St<DT>::dot2(qc.y, kc.y, a);
-        a = St<DT>::dot2(qc.z, kc.z, a);
-        a = St<DT>::dot2(qc.w, kc.w, a);
-        acc[g] = a;
-      }
-      LUC_SCHED_FENCE();
+    for (int hc = 0; hc < 2; ++hc) {  // chunks 4*hc .. 4*hc+3 of the lane's 64 dims
+      uint4 kc[4];
+      lds_read4(ka(4 * hc), ka(4 * hc + 1), ka(4 * hc + 2), ka(4 * hc + 3), kc);
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[g] = dot16_bcast<DT>(acc[g], qd[2 * g + hc], kc);
     }
     if constexpr (S::QKL == 2) {
 #pragma unroll
@@ -353,7 +404,6 @@ __device__ void decode_impl(const DecodeArgs& A) {
       }
     }
 
-    // ---- online softmax (exp2 domain) ----
     const bool valid = (t0 + tq) < s_end;
     float p[G];
 #pragma unroll
@@ -375,27 +425,37 @@ __device__ void decode_impl(const DecodeArgs& A) {
       l_lane[g] += qh == 0 ? p[g] : 0.0f;
     }
 
-    // ---- p to the load layout through LDS ----
+    // p to the load layout through LDS
     if constexpr (PV_DOT2) {
       uint32_t pk[8];
 #pragma unroll
       for (int g = 0; g < 8; ++g) pk[g] = g < G ? pack_f16(p[g], upper_half_value<D>(p[g])) : 0u;
       if (lane < S::HALF) {
-        *(uint4*)(pw + tq * 8) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        *(uint4*)(pw + tq * 8 + 4) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+        *(uint4*)(s_p + tq * 8) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        *(uint4*)(s_p + tq * 8 + 4) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
       }
     } else {
       float pf[8];
 #pragma unroll
       for (int g = 0; g < 8; ++g) pf[g] = g < G ? p[g] : 0.0f;
       if (qh == 0) {
-        *(float4*)(pw + tq * 8) = make_float4(pf[0], pf[1], pf[2], pf[3]);
-        *(float4*)(pw + tq * 8 + 4) = make_float4(pf[4], pf[5], pf[6], pf[7]);
+        *(float4*)(s_p + tq * 8) = make_float4(pf[0], pf[1], pf[2], pf[3]);
+        *(float4*)(s_p + tq * 8 + 4) = make_float4(pf[4], pf[5], pf[6], pf[7]);
       }
     }
     wave_lds_sync();
+  };
 
-    // ---- o += p * V, V in its load layout ----
+  // ---- o += p * V of the tile at t0, V in its load layout ----
+  auto tile_pv = [&](int t0, uint4(&vr)[S::LOADS]) __attribute__((always_inline)) {
+    if constexpr (APPEND) {
+      if (owns && pos >= t0 && pos < t0 + S::TILE) {  // the new token's V
+        const int t = pos - t0;
+#pragma unroll
+        for (int r = 0; r < S::LOADS; ++r)
+          if (r == t / S::TPL && pv_tok == t % S::TPL) vr[r] = *(const uint4*)(s_vnew + pv_ch * 8);
+      }
+    }
     // tokens past the split: V must contribute exactly zero (p is 0 there,
     // and 0 * stale data must not produce NaN)
     const bool partial = t0 + S::TILE > s_end;
@@ -408,8 +468,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
           if (t0 + t >= s_end) va = make_uint4(0, 0, 0, 0);
           if (t0 + t + S::HALF >= s_end) vb = make_uint4(0, 0, 0, 0);
         }
-        const uint4 p0 = *(const uint4*)(pw + t * 8);
-        const uint4 p1 = *(const uint4*)(pw + t * 8 + 4);
+        const uint4 p0 = *(const uint4*)(s_p + t * 8);
+        const uint4 p1 = *(const uint4*)(s_p + t * 8 + 4);
         const uint32_t pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
         const uint32_t aw[4] = {va.x, va.y, va.z, va.w};
         const uint32_t bw[4] = {vb.x, vb.y, vb.z, vb.w};
@@ -423,7 +483,6 @@ __device__ void decode_impl(const DecodeArgs& A) {
         for (int g = 0; g < G; ++g)
 #pragma unroll
           for (int e = 0; e < 8; ++e) o[g][e] = St<kF16>::dot2(pr[e], pp[g], o[g][e]);
-        LUC_SCHED_FENCE();
       }
     } else {
 #pragma unroll
@@ -431,8 +490,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
         const int t = r * S::TPL + pv_tok;
         uint4 v = vr[r];
         if (partial && t0 + t >= s_end) v = make_uint4(0, 0, 0, 0);
-        const float4 pa = *(const float4*)(pw + t * 8);
-        const float4 pb = *(const float4*)(pw + t * 8 + 4);
+        const float4 pa = *(const float4*)(s_p + t * 8);
+        const float4 pb = *(const float4*)(s_p + t * 8 + 4);
         const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
         const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
         float vv[8];
@@ -445,14 +504,49 @@ __device__ void decode_impl(const DecodeArgs& A) {
         for (int g = 0; g < G; ++g)
 #pragma unroll
           for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pv[g], vv[e], o[g][e]);
-        LUC_SCHED_FENCE();
       }
     }
     wave_lds_sync();
+  };
+
+  // ---- the split's tiles, in pairs: both tiles of a pair are issued
+  // (unconditionally, so that the loads keep their place ahead of the waits
+  // below), tile i is computed while tile i+1 lands.  In flight after issuing
+  // a pair: K_i V_i K_{i+1} V_{i+1}, 8 loads each, completing in issue order.
+  // The first pair was issued before the prologue; later pairs load into
+  // registers local to their iteration (no values carried around the loop).
+  auto pair_compute = [&](int t0, bool pair, uint4(&va)[S::LOADS], uint4(&vb)[S::LOADS])
+                          __attribute__((always_inline)) {
+    LUC_WAIT_VM(24);  // K_i
+    tile_scores(t0, 0);
+    LUC_WAIT_VM(16);  // V_i
+    tile_pv(t0, va);
+    if (pair) {
+      LUC_WAIT_VM(8);  // K_{i+1}
+      tile_scores(t0 + S::TILE, 1);
+      LUC_WAIT_VM(0);  // V_{i+1}
+      tile_pv(t0 + S::TILE, vb);
+    }
+  };
+  pair_compute(s_begin, nt > 1, vr0, vr1);
+  for (int i = 2; i < nt; i += 2) {
+    const int t0 = s_begin + i * S::TILE;
+    uint4 va[S::LOADS], vb[S::LOADS];
+    issue(t0, 0, va);
+    issue(t0 + S::TILE, 1, vb);
+    pair_compute(t0, i + 1 < nt, va, vb);
+  }
+
+  if constexpr (APPEND) {
+    if (owns && lane < S::CH) {  // the cache write of the new token
+      const int64_t phys = page_of((pos - s_begin) / kPage);
+      const int64_t slot = phys * page_stride + head_off + (int64_t)(pos % kPage) * D + lane * 8;
+      *(uint4*)(A.k_pool + slot) = *(const uint4*)(s_knew + lane * 8);
+      *(uint4*)(A.v_pool + slot) = *(const uint4*)(s_vnew + lane * 8);
+    }
   }
 
   // ---- reduce the wave's token groups (lanes sharing pv_ch): reduce-scatter ----
-  constexpr int NV = 8 * G;
   float u[NV / 2], y[NV / 4];
 #pragma unroll
   for (int k = 0; k < NV / 2; ++k) {
@@ -471,134 +565,166 @@ __device__ void decode_impl(const DecodeArgs& A) {
 #pragma unroll
     for (int k = 0; k < NV / 4; ++k) y[k] += dpp_mov<0x128>(y[k]);  // row_ror:8
   }
-  float* red = (float*)(s_k + kbase);  // this wave's [G][D] result (its K tile is done)
-  if (D == 128 || (lane & 8) == 0) {
-    const int base = ((lane >> 5) & 1) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);
+  // the lane holds o values base + k (value v: head v / 8, dim pv_ch * 8 + v % 8)
+  const int base = ((lane >> 5) & 1) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);
+  const bool writer = D == 128 || (lane & 8) == 0;
+  float lsum[G];
 #pragma unroll
-    for (int k = 0; k < NV / 4; ++k) {
-      const int kk = base + k;
-      red[(kk / 8) * D + pv_ch * 8 + (kk % 8)] = y[k];
+  for (int g = 0; g < G; ++g) lsum[g] = wave_sum(l_lane[g]);
+
+  if (nsplit == 1) {
+    if (writer) {
+#pragma unroll
+      for (int k = 0; k < NV / 4; ++k) {
+        const int kk = base + k, g = kk / 8;
+        out_row[g * D + pv_ch * 8 + (kk % 8)] = St<DT>::store(y[k] / pick(lsum, g));
+      }
+    }
+  } else {
+    // ---- this split's partial: o[G*D], (m, l)[G] ----
+    const int64_t rec = (int64_t)bh * A.max_splits + split;
+    float* wo = A.ws_o + rec * GD;
+    if (writer) {
+#pragma unroll
+      for (int k = 0; k < NV / 4; ++k) {
+        const int kk = base + k;
+        wo[(kk / 8) * D + pv_ch * 8 + (kk % 8)] = y[k];
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (lane == g) {
+        A.ws_ml[(rec * G + g) * 2] = m_run[g];
+        A.ws_ml[(rec * G + g) * 2 + 1] = lsum[g];
+      }
     }
   }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float l = wave_sum(l_lane[g]);
-    if (lane == 0) {
-      s_m[w][g] = m_run[g];
-      s_l[w][g] = l;
+}
+
+// Log-sum-exp merge of the splits of one (sequence, kv head) -- the
+// reference's partition merge (attention.cu:140-174) over splits:
+// M = max m_s, L = sum l_s 2^(m_s - M), O = sum o_s 2^(m_s - M) / L.  The step
+// variant also writes the roped q (G heads) and k of the new token back into
+// the qkv row, after every split of the decode launch has read them.
+template <int DT, int D, int G, bool APPEND>
+__device__ void combine_impl(const DecodeArgs& A) {
+  constexpr int NT = 256;
+  constexpr int HD = D / 2;
+  constexpr int GD = G * D;
+  constexpr int NE = (GD + NT - 1) / NT;  // output elements per thread
+  constexpr int SB = 16;                  // splits per batch of o loads
+  __shared__ float s_w[G][256];           // split weights
+  __shared__ float s_L[G];
+  const int bh = blockIdx.x;
+  const int b = bh / A.hkv, h = bh - b * A.hkv;
+  const int pos = A.positions[b];
+  const int ctx = pos + 1;
+  if (ctx < 1 || ctx > A.max_ctx) return;  // the decode kernel wrote NaN
+  const int nsplit = (ctx + A.split_tokens - 1) / A.split_tokens;
+  if constexpr (APPEND) {
+    const float* crow = A.cos_t + (int64_t)pos * HD;
+    const float* srow = A.sin_t + (int64_t)pos * HD;
+    uint16_t* qrow = A.q + (int64_t)b * A.q_stride + (int64_t)h * GD;
+    uint16_t* krow = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
+    for (int idx = threadIdx.x; idx < (G + 1) * HD; idx += NT) {
+      const int g = idx / HD, j = idx % HD;
+      uint16_t* x = g < G ? qrow + g * D : krow;
+      const uint16_t* bias = g < G ? (A.q_bias ? A.q_bias + ((int64_t)h * G + g) * D : nullptr)
+                                   : (A.k_bias ? A.k_bias + (int64_t)h * D : nullptr);
+      uint16_t o1, o2;
+      rot_pair<DT>(x[j], bias ? bias[j] : 0, x[j + HD], bias ? bias[j + HD] : 0, crow[j], srow[j],
+                   o1, o2);
+      x[j] = o1;
+      x[j + HD] = o2;
     }
+  }
+  if (nsplit <= 1) return;  // the decode kernel wrote the output
+  const float* ml = A.ws_ml + (int64_t)bh * A.max_splits * G * 2;
+  const float* po = A.ws_o + (int64_t)bh * A.max_splits * GD;
+  // o of the first batch of splits goes out before the weights are known
+  float ob[SB][NE];
+  auto load_batch = [&](int s0) {
+#pragma unroll
+    for (int j = 0; j < SB; ++j)
+#pragma unroll
+      for (int c = 0; c < NE; ++c) {
+        const int e = min((int)threadIdx.x + NT * c, GD - 1);
+        ob[j][c] = po[(int64_t)min(s0 + j, nsplit - 1) * GD + e];
+      }
+  };
+  load_batch(0);
+  // weights: wave w handles heads w, w + 4, ...
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int g = w; g < G; g += NT / 64) {
+    float mv[4], lv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int s = lane + 64 * k;
+      mv[k] = s < nsplit ? ml[((int64_t)s * G + g) * 2] : -INFINITY;
+      lv[k] = s < nsplit ? ml[((int64_t)s * G + g) * 2 + 1] : 0.0f;
+    }
+    const float M = wave_max(fmaxf(fmaxf(mv[0], mv[1]), fmaxf(mv[2], mv[3])));
+    float L = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float wgt = __builtin_amdgcn_exp2f(mv[k] - M);  // 0 past nsplit
+      s_w[g][lane + 64 * k] = wgt;
+      L = fmaf(wgt, lv[k], L);
+    }
+    L = wave_sum(L);
+    if (lane == 0) s_L[g] = L;
   }
   __syncthreads();
-
-  // ---- merge the waves ----
-  const int64_t ws_base = ((int64_t)b * hq + (int64_t)h * G) * A.max_splits;
-  for (int idx = threadIdx.x; idx < G * D; idx += NT) {
-    const int g = idx / D, d = idx % D;
-    float M = -INFINITY;
+  float acc[NE];
 #pragma unroll
-    for (int w2 = 0; w2 < NW; ++w2) M = fmaxf(M, s_m[w2][g]);
-    float L = 0.0f, acc = 0.0f;
+  for (int c = 0; c < NE; ++c) acc[c] = 0.0f;
+  for (int s0 = 0; s0 < nsplit; s0 += SB) {
+    if (s0 > 0) load_batch(s0);
 #pragma unroll
-    for (int w2 = 0; w2 < NW; ++w2) {
-      const float sc = __builtin_amdgcn_exp2f(s_m[w2][g] - M);  // 0 for waves without tiles
-      L = fmaf(sc, s_l[w2][g], L);
-      acc = fmaf(sc, ((const float*)(s_k + w2 * S::KBYTES))[g * D + d], acc);
-    }
-    if (nsplit == 1) {
-      out_row[idx] = St<DT>::store(acc / L);
-    } else {
-      const int64_t ws = ws_base + (int64_t)g * A.max_splits + split;
-      st_agent(A.ws_o + ws * D + d, acc);
-      if (d == 0) {
-        st_agent(A.ws_ml + ws * 2, M);
-        st_agent(A.ws_ml + ws * 2 + 1, L);
+    for (int j = 0; j < SB; ++j) {
+      if (s0 + j < nsplit) {
+#pragma unroll
+        for (int c = 0; c < NE; ++c) {
+          const int e = min((int)threadIdx.x + NT * c, GD - 1);
+          acc[c] = fmaf(s_w[e / D][s0 + j], ob[j][c], acc[c]);
+        }
       }
     }
   }
-
-  if (nsplit > 1) {
-    // ---- arrival: the last split of (b, h) merges them all ----
-    // Partials travel through agent-coherent (sc1) stores and loads, so no
-    // L2 write-back is needed: every store of this workgroup has completed
-    // before its arrival is counted, and the last arrival loads after the
-    // count has returned.
-    wait_vmem_all();
-    __syncthreads();
-    if (threadIdx.x == 0)
-      s_last = __hip_atomic_fetch_add(A.ws_cnt + bh, 1u, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(nsplit - 1);
-    __syncthreads();
-    if (!s_last) return;
-    float* s_wt = (float*)s_k;  // [G][256] split weights
-    for (int g = w; g < G; g += NW) {
-      const float* ml = A.ws_ml + (ws_base + (int64_t)g * A.max_splits) * 2;
-      float mv[4], lv[4];  // splits lane, lane+64, ... (at most 256)
+  uint16_t* out_row = A.out + (int64_t)b * A.out_stride + (int64_t)h * GD;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int s = lane + 64 * k;
-        mv[k] = s < nsplit ? ld_agent(ml + s * 2) : -INFINITY;
-        lv[k] = s < nsplit ? ld_agent(ml + s * 2 + 1) : 0.0f;
-      }
-      const float M = wave_max(fmaxf(fmaxf(mv[0], mv[1]), fmaxf(mv[2], mv[3])));
-      float L = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int s = lane + 64 * k;
-        const float wgt = __builtin_amdgcn_exp2f(mv[k] - M);  // 0 past nsplit
-        if (s < nsplit) s_wt[g * 256 + s] = wgt;
-        L = fmaf(wgt, lv[k], L);
-      }
-      L = wave_sum(L);
-      if (lane == 0) s_L[g] = L;
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < G * D; idx += NT) {
-      const int g = idx / D, d = idx % D;
-      const float* op = A.ws_o + (ws_base + (int64_t)g * A.max_splits) * D + d;
-      const float* wt = s_wt + g * 256;
-      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-      int s = 0;
-      for (; s + 4 <= nsplit; s += 4) {
-        a0 = fmaf(wt[s], ld_agent(op + (int64_t)s * D), a0);
-        a1 = fmaf(wt[s + 1], ld_agent(op + (int64_t)(s + 1) * D), a1);
-        a2 = fmaf(wt[s + 2], ld_agent(op + (int64_t)(s + 2) * D), a2);
-        a3 = fmaf(wt[s + 3], ld_agent(op + (int64_t)(s + 3) * D), a3);
-      }
-      for (; s < nsplit; ++s) a0 = fmaf(wt[s], ld_agent(op + (int64_t)s * D), a0);
-      out_row[idx] = St<DT>::store(((a0 + a1) + (a2 + a3)) / s_L[g]);
-    }
-    if (threadIdx.x == 0)  // ready for the next launch
-      __hip_atomic_store(A.ws_cnt + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-
-  if constexpr (APPEND) {
-    // every split has read q and k: write the roped values back in place
-    uint16_t* qw = A.q + (int64_t)b * A.q_stride + (int64_t)h * G * D;
-    uint16_t* kw = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
-    for (int i = threadIdx.x; i < G * D; i += NT) qw[i] = s_q[i];
-    for (int i = threadIdx.x; i < D; i += NT) kw[i] = s_knew[i];
+  for (int c = 0; c < NE; ++c) {
+    const int e = threadIdx.x + NT * c;
+    if (e < GD) out_row[e] = St<DT>::store(acc[c] / s_L[e / D]);
   }
 }
 
 }  // namespace luc
 
-// Resident-wave targets (waves per SIMD).  fp16 fits three 4-wave workgroups
-// per CU in registers; the bf16 FMA path needs more registers and runs two.
+// Resident-wave targets (waves per SIMD).
 #ifndef LUC_DECODE_OCC_f16
-#define LUC_DECODE_OCC_f16 __attribute__((amdgpu_waves_per_eu(3)))
+#define LUC_DECODE_OCC_f16 __attribute__((amdgpu_waves_per_eu(2)))
 #endif
 #ifndef LUC_DECODE_OCC_bf16
 #define LUC_DECODE_OCC_bf16 __attribute__((amdgpu_waves_per_eu(2)))
 #endif
 
 #define LUC_DECODE(DTN, DT, D, G)                                                                  \
-  extern "C" __global__ __launch_bounds__(256) LUC_DECODE_OCC_##DTN void luc_decode_##DTN##_d##D##_g##G( \
+  extern "C" __global__ __launch_bounds__(64) LUC_DECODE_OCC_##DTN void luc_decode_##DTN##_d##D##_g##G( \
       luc::DecodeArgs a) {                                                                         \
     luc::decode_impl<DT, D, G, false>(a);                                                          \
   }                                                                                                \
-  extern "C" __global__ __launch_bounds__(256) LUC_DECODE_OCC_##DTN void                          \
+  extern "C" __global__ __launch_bounds__(64) LUC_DECODE_OCC_##DTN void                           \
       luc_decode_step_##DTN##_d##D##_g##G(luc::DecodeArgs a) {                                     \
     luc::decode_impl<DT, D, G, true>(a);                                                           \
+  }                                                                                                \
+  extern "C" __global__ __launch_bounds__(256) void luc_decode_combine_##DTN##_d##D##_g##G(        \
+      luc::DecodeArgs a) {                                                                         \
+    luc::combine_impl<DT, D, G, false>(a);                                                         \
+  }                                                                                                \
+  extern "C" __global__ __launch_bounds__(256) void luc_decode_step_combine_##DTN##_d##D##_g##G(   \
+      luc::DecodeArgs a) {                                                                         \
+    luc::combine_impl<DT, D, G, true>(a);                                                          \
   }
 
 #define LUC_DECODE_GROUPS(DTN, DT, D)                                                              \

@@ -55,11 +55,14 @@ int fail(int code, const char* fmt, ...) {
 
 constexpr const char* kCodeObjects[] = {"rope_append.hsaco", "paged_decode.hsaco"};
 
-// Kernel-side constants (kept in step with csrc/kernels/paged_decode.hip).
-constexpr int kDecodeWaves = 4;
+// Kernel-side constants (kept in step with csrc/kernels/paged_decode.hip):
+// one wave per workgroup; tiles of 64 tokens (head_dim 64) or 32 (128); a
+// split's block-table entries are held in two registers (128 pages).
+constexpr int kDecodeWaves = 1;
 int decode_tile(int head_dim) { return head_dim == 64 ? 64 : 32; }
-// Number of compute units the automatic split choice plans for (MI355X).
-constexpr int kPlanCUs = 256;
+constexpr int kMaxSplitTokens = 128 * LUC_BLOCK_SIZE;
+// Waves the automatic split choice plans for: one per SIMD of an MI355X.
+constexpr int kPlanWaves = 256 * 4;
 
 const char* dt_name(int dtype) { return dtype == LUC_F16 ? "f16" : "bf16"; }
 
@@ -171,36 +174,48 @@ int check_cache(const void* k_pool, const void* v_pool, const int32_t* tables, i
 // Splits per sequence are capped at kMaxSplits (the merge's LDS weight table).
 constexpr int kMaxSplits = 256;
 
-// Split-K chunk length in tokens: a multiple of the wave tile.  The automatic
-// choice assumes the mean context is half of max_ctx and aims at about two
-// resident workgroups per CU on a kPlanCUs-CU device.  It depends only on the
-// arguments, so luc_paged_decode_workspace_size agrees with the launch.
+// Split-K chunk length in tokens: a multiple of the tile, at most
+// kMaxSplitTokens.  The automatic choice assumes the mean context is half of
+// max_ctx and aims at about one wave per SIMD, each with at least two tiles
+// (the kernel keeps two tiles in flight).  It depends only on the arguments,
+// so luc_paged_decode_workspace_size agrees with the launch.  Returns 0 when
+// max_ctx cannot be covered by kMaxSplits splits.
 int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requested) {
   const int tile = decode_tile(head_dim);
   const int64_t floor_tokens = ceil_div(ceil_div(max_ctx, kMaxSplits), tile) * tile;
-  if (requested > 0) return (int)std::max<int64_t>(ceil_div(requested, tile) * tile, floor_tokens);
-  const int64_t wg_tokens = (int64_t)kDecodeWaves * tile;
-  const int64_t est = (int64_t)batch * hkv * std::max<int64_t>(ceil_div(max_ctx, 2), 1);
-  const int64_t st = ceil_div(ceil_div(est, 2 * kPlanCUs), wg_tokens) * wg_tokens;
-  return (int)std::max<int64_t>(st, floor_tokens);
+  if (floor_tokens > kMaxSplitTokens) return 0;
+  int64_t st;
+  if (requested > 0) {
+    st = ceil_div(requested, tile) * tile;
+  } else {
+    const int64_t est = (int64_t)batch * hkv * std::max<int64_t>(ceil_div(max_ctx, 2), 1);
+    st = ceil_div(ceil_div(est, kPlanWaves), 2 * tile) * 2 * tile;
+  }
+  st = std::min<int64_t>(std::max<int64_t>(st, floor_tokens), kMaxSplitTokens);
+  return (int)st;
 }
 
-// Workspace layout: [arrival counter per (b, kv head): u32, padded to 256 B]
-//                   [(max, sum) per (b, q-head, split): f32 x2]
-//                   [o per (b, q-head, split): f32 x head_dim]
-int64_t counter_bytes(int batch, int hkv) { return ceil_div((int64_t)batch * hkv, 64) * 256; }
+// Workspace layout (each section 256-byte aligned):
+//   [(max, sum) per (b, kv head, split, head of the group): f32 x2]
+//   [o per (b, kv head, split): f32 x group x head_dim]
+int64_t align256(int64_t n) { return ceil_div(n, 256) * 256; }
+int64_t ml_bytes(int batch, int hq, int max_splits) {
+  return align256((int64_t)batch * hq * max_splits * 2 * 4);
+}
 
-size_t workspace_bytes_for(int batch, int hq, int hkv, int head_dim, int max_ctx, int split_tokens) {
+size_t workspace_bytes_for(int batch, int hq, int head_dim, int max_ctx, int split_tokens) {
   const int64_t max_splits = ceil_div(max_ctx, split_tokens);
   if (max_splits <= 1) return 0;
-  return (size_t)counter_bytes(batch, hkv) +
-         (size_t)batch * hq * max_splits * (head_dim + 2) * sizeof(float);
+  return (size_t)(ml_bytes(batch, hq, (int)max_splits) +
+                  (int64_t)batch * hq * max_splits * head_dim * 4);
 }
 
 struct DecodeLaunch {
   luc_decode_args a{};
-  hipFunction_t fn = nullptr;
+  hipFunction_t fn = nullptr;       // split-K decode
+  hipFunction_t combine = nullptr;  // log-sum-exp merge (+ q/k write-back for the step)
   dim3 grid;
+  bool need_combine = false;
 };
 
 // Shared argument checks and argument block of the two decode entry points.
@@ -228,9 +243,11 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
     return fail(LUC_E_INVALID, "table_stride %d pages cannot hold max_ctx %d", table_stride, max_ctx);
 
   const int st = split_tokens_for(batch, num_kv_heads, head_dim, max_ctx, split_tokens);
+  if (st == 0)
+    return fail(LUC_E_UNSUPPORTED, "max_ctx %d exceeds %d splits of %d tokens", max_ctx,
+                kMaxSplits, kMaxSplitTokens);
   const int max_splits = (int)ceil_div(max_ctx, st);
-  const size_t need =
-      workspace_bytes_for(batch, num_q_heads, num_kv_heads, head_dim, max_ctx, st);
+  const size_t need = workspace_bytes_for(batch, num_q_heads, head_dim, max_ctx, st);
   if (need && (!workspace || workspace_bytes < need))
     return fail(LUC_E_WORKSPACE, "workspace %zu bytes, %zu needed", workspace_bytes, need);
   if (need && !aligned(workspace, 256)) return fail(LUC_E_INVALID, "workspace must be 256-byte aligned");
@@ -239,11 +256,15 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
 
   if (batch == 0) return LUC_OK;  // nothing to launch
   const int group = num_q_heads / num_kv_heads;
-  const std::string name = std::string(step ? "luc_decode_step_" : "luc_decode_") +
-                           dt_name(dtype) + "_d" + std::to_string(head_dim) + "_g" +
-                           std::to_string(group);
-  if (int rc = get_fn(ctx, name, &L->fn)) return rc;
+  const std::string suffix = std::string(dt_name(dtype)) + "_d" + std::to_string(head_dim) + "_g" +
+                             std::to_string(group);
+  if (int rc = get_fn(ctx, std::string(step ? "luc_decode_step_" : "luc_decode_") + suffix, &L->fn))
+    return rc;
+  if (int rc = get_fn(ctx, std::string(step ? "luc_decode_step_combine_" : "luc_decode_combine_") +
+                               suffix, &L->combine))
+    return rc;
   L->grid = dim3((unsigned)grid);
+  L->need_combine = step || max_splits > 1;
   luc_decode_args& a = L->a;
   a.q = static_cast<uint16_t*>(const_cast<void*>(q));
   a.q_stride = q_row_stride;
@@ -262,9 +283,8 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
   a.max_splits = max_splits;
   if (need) {
     char* ws = static_cast<char*>(workspace);
-    a.ws_cnt = reinterpret_cast<uint32_t*>(ws);
-    a.ws_ml = reinterpret_cast<float*>(ws + counter_bytes(batch, num_kv_heads));
-    a.ws_o = a.ws_ml + (size_t)batch * num_q_heads * max_splits * 2;
+    a.ws_ml = reinterpret_cast<float*>(ws);
+    a.ws_o = reinterpret_cast<float*>(ws + ml_bytes(batch, num_q_heads, max_splits));
   }
   a.out = static_cast<uint16_t*>(out);
   a.out_stride = out_row_stride;
@@ -273,7 +293,9 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
 
 int launch_decode(DecodeLaunch& L, void* stream) {
   void* args[] = {&L.a};
-  return launch(L.fn, L.grid, dim3(kDecodeWaves * 64), stream, args);
+  if (int rc = launch(L.fn, L.grid, dim3(kDecodeWaves * 64), stream, args)) return rc;
+  if (!L.need_combine) return LUC_OK;
+  return launch(L.combine, dim3(L.a.batch * L.a.hkv), dim3(256), stream, args);
 }
 
 }  // namespace
@@ -310,7 +332,8 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
     names.push_back(std::string("luc_rope_append_") + dt);
     for (int d : {64, 128})
       for (int g = 1; g <= 8; ++g)
-        for (const char* kind : {"luc_decode_", "luc_decode_step_"})
+        for (const char* kind : {"luc_decode_", "luc_decode_step_", "luc_decode_combine_",
+                                 "luc_decode_step_combine_"})
           names.push_back(std::string(kind) + dt + "_d" + std::to_string(d) + "_g" +
                           std::to_string(g));
   }
@@ -327,7 +350,7 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
   if (hipDeviceGetAttribute(&ctx->num_cus, hipDeviceAttributeMultiprocessorCount, device) !=
           hipSuccess ||
       ctx->num_cus < 1)
-    ctx->num_cus = kPlanCUs;
+    ctx->num_cus = 256;
   (void)hipGetLastError();  // clear the misses from probing several modules
   *out_ctx = ctx;
   return LUC_OK;
@@ -428,7 +451,8 @@ size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_he
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_ctx <= 0) return 0;
   if (head_dim != 64 && head_dim != 128) return 0;
   const int st = split_tokens_for(batch, num_kv_heads, head_dim, max_ctx, split_tokens);
-  return workspace_bytes_for(batch, num_q_heads, num_kv_heads, head_dim, max_ctx, st);
+  if (st == 0) return 0;
+  return workspace_bytes_for(batch, num_q_heads, head_dim, max_ctx, st);
 }
 
 int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t out_row_stride,

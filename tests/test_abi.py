@@ -93,10 +93,10 @@ def test_workspace_size_policy(cdll):
     ws = cdll.luc_paged_decode_workspace_size
 
     def expect(batch, hq, hkv, d, splits):
-        # arrival counters (u32 per sequence x kv head, padded to 256 B), then
-        # (max, sum) and o[d] in f32 per (sequence, q-head, split)
-        counters = -(-batch * hkv // 64) * 256
-        return counters + batch * hq * splits * (d + 2) * 4
+        # 256-byte aligned sections: (max, sum) in f32 per (sequence, q-head,
+        # split), o[d] in f32 per (sequence, q-head, split)
+        a256 = lambda n: -(-n // 256) * 256  # noqa: E731
+        return a256(batch * hq * splits * 8) + batch * hq * splits * d * 4
 
     # one split per sequence -> no workspace
     assert ws(32, 14, 2, 64, 100, 0) == 0
@@ -108,8 +108,12 @@ def test_workspace_size_policy(cdll):
     assert ws(2, 14, 2, 64, 1000, 250) == ws(2, 14, 2, 64, 1000, 256)
     assert ws(2, 14, 2, 128, 1000, 90) == ws(2, 14, 2, 128, 1000, 96)
     assert ws(1, 4, 1, 96, 1000, 0) == 0
-    # the automatic split aims at ~2 workgroups per CU of 256 CUs
-    assert ws(32, 14, 2, 64, 4096, 0) == expect(32, 14, 2, 64, 16)
+    # the automatic split aims at about one wave per SIMD (1024), two tiles each
+    assert ws(32, 14, 2, 64, 4096, 0) == expect(32, 14, 2, 64, 32)
+    # a split holds at most 128 pages: longer contexts than 256 x 2048 tokens
+    # are not supported
+    assert ws(1, 4, 1, 64, 256 * 2048, 0) > 0
+    assert ws(1, 4, 1, 64, 256 * 2048 + 1, 0) == 0
 
 
 def test_rope_table_entry_point_matches_oracle(orc, cdll):

@@ -114,6 +114,19 @@ def test_split_count_independence(orc, luc):
         assert d <= 2 * 2.0 ** -8  # two bf16 ulps at |x| < 1
 
 
+@pytest.mark.parametrize("split", [64, 128, 192, 256, 512, 1024, 2048])
+def test_split_sizes_fp16_against_oracle(orc, luc, split):
+    """Every split size (one tile per split, tile pairs, and splits walking
+    several pairs) matches the oracle at the fp16 tolerance, at the
+    batch32_mixed shape with contexts up to 4096."""
+    cfg = wl.scaled(wl.CONFIGS["batch32_mixed"], batch=6, ctx_lo=200, ctx_hi=4096,
+                    pool_pages=6 * 256 + 1)
+    h = wl.host_decode_inputs(cfg, seed=29)
+    want = oracle_step(orc, luc, h)
+    got = gpu_step(luc, h, split_tokens=split)
+    assert_step_matches(orc, got, want, "f16")
+
+
 def test_page_permutation_is_bit_exact(orc, luc):
     """Moving pages in the pool and remapping the table changes nothing."""
     cfg = wl.scaled(wl.CONFIGS["batch32_mixed"], batch=4, ctx_lo=200, ctx_hi=1200,
