@@ -109,6 +109,46 @@ __device__ inline float wave_sum(float x) {
   return readlane(r, 63);
 }
 
+// Wave sums of H <= 4 independent values at once: the same DPP chain, issued
+// step-major so that between the write of a value and the next DPP read of it
+// lie H-1 other instructions; for H < 3 an s_nop pads the two wait states.
+// One such block costs about one chain's latency instead of H of them.
+#define LUC_RS1(CTRL) "v_add_f32_dpp %[r0], %[r0], %[r0] " CTRL "\n\t"
+#define LUC_RS2(CTRL) LUC_RS1(CTRL) "v_add_f32_dpp %[r1], %[r1], %[r1] " CTRL "\n\t"
+#define LUC_RS3(CTRL) LUC_RS2(CTRL) "v_add_f32_dpp %[r2], %[r2], %[r2] " CTRL "\n\t"
+#define LUC_RS4(CTRL) LUC_RS3(CTRL) "v_add_f32_dpp %[r3], %[r3], %[r3] " CTRL "\n\t"
+#define LUC_RSUM(H, PAD)                                                                     \
+  "s_nop 1\n\t" LUC_RS##H("quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf") PAD              \
+      LUC_RS##H("quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf") PAD                        \
+      LUC_RS##H("row_half_mirror row_mask:0xf bank_mask:0xf") PAD                            \
+      LUC_RS##H("row_mirror row_mask:0xf bank_mask:0xf") PAD                                 \
+      LUC_RS##H("row_bcast:15 row_mask:0xa bank_mask:0xf") PAD                               \
+      LUC_RS##H("row_bcast:31 row_mask:0xc bank_mask:0xf") "s_nop 1"
+template <int H>
+__device__ __attribute__((always_inline)) inline void wave_sum_group(float* x) {
+  static_assert(H >= 1 && H <= 4, "1 to 4 values per block");
+  if constexpr (H == 1) {
+    asm volatile(LUC_RSUM(1, "s_nop 1\n\t") : [r0] "+v"(x[0]));
+  } else if constexpr (H == 2) {
+    asm volatile(LUC_RSUM(2, "s_nop 0\n\t") : [r0] "+v"(x[0]), [r1] "+v"(x[1]));
+  } else if constexpr (H == 3) {
+    asm volatile(LUC_RSUM(3, "") : [r0] "+v"(x[0]), [r1] "+v"(x[1]), [r2] "+v"(x[2]));
+  } else {
+    asm volatile(LUC_RSUM(4, "")
+                 : [r0] "+v"(x[0]), [r1] "+v"(x[1]), [r2] "+v"(x[2]), [r3] "+v"(x[3]));
+  }
+#pragma unroll
+  for (int i = 0; i < H; ++i) x[i] = readlane(x[i], 63);
+}
+// x[i] = wave-uniform sum of x[i] over all 64 lanes, for i < N (N <= 8).
+template <int N>
+__device__ __attribute__((always_inline)) inline void wave_sum_n(float (&x)[N]) {
+  static_assert(N >= 1 && N <= 8, "at most 8 values");
+  constexpr int H1 = N <= 4 ? N : (N + 1) / 2;
+  wave_sum_group<H1>(x);
+  if constexpr (N > H1) wave_sum_group<N - H1>(x + H1);
+}
+
 // Orders this wave's LDS accesses at this point (DS operations of one wave
 // complete in issue order, so a code-motion barrier is all that is needed).
 __device__ inline void wave_lds_sync() {

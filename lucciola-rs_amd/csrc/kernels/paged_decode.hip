@@ -74,6 +74,9 @@ struct DecodeGeo {
 };
 
 constexpr int kCpolNT = 2;  // non-temporal load: the KV stream is read once per step
+// Online softmax: p = exp2(s - m) is kept <= 2^kLazyMax (exact in f16 range)
+// by moving the reference point m only when a score passes m + kLazyMax.
+constexpr float kLazyMax = 8.0f;
 
 // Wait until at most N vector memory operations of this wave are in flight.
 // They complete in issue order, so this also covers the LDS writes of
@@ -91,6 +94,40 @@ __device__ inline void dma16(const char* g, lds_char* l, int rb) {
     default: __builtin_amdgcn_global_load_lds(g, (lds_void*)l, 16, 3072, kCpolNT); break;
   }
 }
+
+// 4 bytes per lane from global memory straight into LDS at l + 4*lane.
+__device__ inline void dma4(const void* g, lds_char* l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)l, 4, 0, 0);
+}
+
+// x = LDS dword at byte address a + OFF; complete only after lds_wait.
+template <int OFF>
+__device__ inline void lds_read_u32_async(uint32_t a, uint32_t& x) {
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(x) : "v"(a), "i"(OFF));
+}
+// Waits for every outstanding LDS read of this wave; x and y come out of it,
+// so their uses stay behind the wait.
+__device__ inline void lds_wait(uint32_t& x, uint32_t& y) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x), "+v"(y));
+}
+
+// Issues the LDS reads of q words M..N-1 of the single-tile kernel: word m
+// of the lane (see q_word in decode_impl) is at byte (m/2 * HD + m%2 * 16) * 4
+// from the lane's base address.
+template <int M, int N, int HD>
+__device__ __attribute__((always_inline)) inline void read_q_words(uint32_t qa, uint32_t* qd) {
+  if constexpr (M < N) {
+    lds_read_u32_async<((M / 2) * HD + (M % 2) * 16) * 4>(qa, qd[M]);
+    read_q_words<M + 1, N, HD>(qa, qd);
+  }
+}
+
+typedef __attribute__((address_space(4))) const int const_i32;
+// N consecutive table entries in one scalar load (4-byte aligned).
+template <int N>
+struct I32Vec {
+  typedef int T __attribute__((ext_vector_type(N), aligned(4)));
+};
 
 // Four 16-byte LDS reads, complete on return.  Written as one asm block so
 // the compiler does not see them as reads of memory that global_load_lds may
@@ -113,46 +150,87 @@ __device__ inline uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const lds_char*)p;
 }
 
-// acc + sum over 16 dwords j of dot2(q word j, k[j]), where q word j is lane
-// j of this lane's 16-lane row of register qd (DPP row_newbcast).  The
-// compiler does not see the instructions inside the asm, so the block pads
-// both hazards itself: s_nop 1 before (a VALU write of qd just before a DPP
-// read of it needs 2 wait states) and s_nop 2 after (a v_dot result read by
-// any VALU instruction other than the same dot reading it as accumulator
-// needs 3 wait states; without them the next instruction can read a stale
-// accumulator).
-#define LUC_DOT16(OP)                                                                     \
-  "s_nop 1\n\t"                                                                           \
-  OP " %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"                        \
-  OP " %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"                        \
-  OP " %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"                        \
-  OP " %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"                        \
-  OP " %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"                        \
-  OP " %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"                        \
-  OP " %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"                        \
-  OP " %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"                        \
-  OP " %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"                       \
-  OP " %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"                       \
-  OP " %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"                      \
-  OP " %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"                      \
-  OP " %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"                      \
-  OP " %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"                      \
-  OP " %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"                      \
-  OP " %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"                      \
-  "s_nop 2"
-#define LUC_DOT16_ARGS(acc, qd, k)                                                        \
-  : "+v"(acc)                                                                            \
-  : "v"(qd), "v"(k[0].x), "v"(k[0].y), "v"(k[0].z), "v"(k[0].w), "v"(k[1].x), "v"(k[1].y), \
-    "v"(k[1].z), "v"(k[1].w), "v"(k[2].x), "v"(k[2].y), "v"(k[2].z), "v"(k[2].w),          \
-    "v"(k[3].x), "v"(k[3].y), "v"(k[3].z), "v"(k[3].w)
-template <int DT>
-__device__ inline float dot16_bcast(float acc, uint32_t qd, const uint4 (&k)[4]) {
+// Scores of H heads (H <= 4) against one lane's 16 K dwords:
+//   acc[i] += sum over j < 16 of dot2(q word j of head i, k[j]),
+// where q word j is lane j of this lane's 16-lane row of register q[i] (DPP
+// row_newbcast hands it to every lane of the row).  The dots are issued
+// j-major, head-minor, so consecutive instructions are independent and one
+// wave alone keeps the VALU busy.  The compiler does not see the
+// instructions inside the asm, so the block pads both hazards itself:
+// s_nop 1 before (a VALU write of q just before a DPP read of it needs 2 wait
+// states) and s_nop 2 after (a v_dot result read by any VALU instruction
+// other than the same dot reading it as accumulator needs 3 wait states;
+// without them the next instruction can read a stale accumulator).
+#define LUC_DQ1(OP, j) OP " %[a0], %[q0], %[k" #j "] row_newbcast:" #j "\n\t"
+#define LUC_DQ2(OP, j) LUC_DQ1(OP, j) OP " %[a1], %[q1], %[k" #j "] row_newbcast:" #j "\n\t"
+#define LUC_DQ3(OP, j) LUC_DQ2(OP, j) OP " %[a2], %[q2], %[k" #j "] row_newbcast:" #j "\n\t"
+#define LUC_DQ4(OP, j) LUC_DQ3(OP, j) OP " %[a3], %[q3], %[k" #j "] row_newbcast:" #j "\n\t"
+#define LUC_DQS(H, OP)                                                                      \
+  "s_nop 1\n\t" LUC_DQ##H(OP, 0) LUC_DQ##H(OP, 1) LUC_DQ##H(OP, 2) LUC_DQ##H(OP, 3)        \
+      LUC_DQ##H(OP, 4) LUC_DQ##H(OP, 5) LUC_DQ##H(OP, 6) LUC_DQ##H(OP, 7) LUC_DQ##H(OP, 8)  \
+          LUC_DQ##H(OP, 9) LUC_DQ##H(OP, 10) LUC_DQ##H(OP, 11) LUC_DQ##H(OP, 12)            \
+              LUC_DQ##H(OP, 13) LUC_DQ##H(OP, 14) LUC_DQ##H(OP, 15) "s_nop 2"
+#define LUC_DQ_OUT1 [a0] "+v"(acc[0])
+#define LUC_DQ_OUT2 LUC_DQ_OUT1, [a1] "+v"(acc[1])
+#define LUC_DQ_OUT3 LUC_DQ_OUT2, [a2] "+v"(acc[2])
+#define LUC_DQ_OUT4 LUC_DQ_OUT3, [a3] "+v"(acc[3])
+#define LUC_DQ_IN1 [q0] "v"(q[0])
+#define LUC_DQ_IN2 LUC_DQ_IN1, [q1] "v"(q[1])
+#define LUC_DQ_IN3 LUC_DQ_IN2, [q2] "v"(q[2])
+#define LUC_DQ_IN4 LUC_DQ_IN3, [q3] "v"(q[3])
+#define LUC_DQ_K                                                                             \
+  [k0] "v"(k[0].x), [k1] "v"(k[0].y), [k2] "v"(k[0].z), [k3] "v"(k[0].w), [k4] "v"(k[1].x), \
+      [k5] "v"(k[1].y), [k6] "v"(k[1].z), [k7] "v"(k[1].w), [k8] "v"(k[2].x),               \
+      [k9] "v"(k[2].y), [k10] "v"(k[2].z), [k11] "v"(k[2].w), [k12] "v"(k[3].x),            \
+      [k13] "v"(k[3].y), [k14] "v"(k[3].z), [k15] "v"(k[3].w)
+#define LUC_DQ_ASM(H, OP) asm(LUC_DQS(H, OP) : LUC_DQ_OUT##H : LUC_DQ_IN##H, LUC_DQ_K)
+
+template <int DT, int H>
+__device__ __attribute__((always_inline)) inline void dot_heads(float (&acc)[H], const uint32_t (&q)[H],
+                                                                const uint4 (&k)[4]) {
+  static_assert(H >= 1 && H <= 4, "one block holds 1 to 4 heads");
   if constexpr (DT == kF16) {
-    asm(LUC_DOT16("v_dot2c_f32_f16_dpp") LUC_DOT16_ARGS(acc, qd, k));
+    if constexpr (H == 1) LUC_DQ_ASM(1, "v_dot2c_f32_f16_dpp");
+    else if constexpr (H == 2) LUC_DQ_ASM(2, "v_dot2c_f32_f16_dpp");
+    else if constexpr (H == 3) LUC_DQ_ASM(3, "v_dot2c_f32_f16_dpp");
+    else LUC_DQ_ASM(4, "v_dot2c_f32_f16_dpp");
   } else {
-    asm(LUC_DOT16("v_dot2c_f32_bf16_dpp") LUC_DOT16_ARGS(acc, qd, k));
+    if constexpr (H == 1) LUC_DQ_ASM(1, "v_dot2c_f32_bf16_dpp");
+    else if constexpr (H == 2) LUC_DQ_ASM(2, "v_dot2c_f32_bf16_dpp");
+    else if constexpr (H == 3) LUC_DQ_ASM(3, "v_dot2c_f32_bf16_dpp");
+    else LUC_DQ_ASM(4, "v_dot2c_f32_bf16_dpp");
   }
-  return acc;
+}
+
+// Scores of all G heads for one 16-dword K chunk: the heads in (at most) two
+// blocks of up to 4; q word hc of head g is in qd[2g + hc].
+template <int DT, int G>
+__device__ __attribute__((always_inline)) inline void dot_all_heads(float (&acc)[G], const uint32_t* qd,
+                                                                    int hc, const uint4 (&k)[4]) {
+  constexpr int H1 = G <= 4 ? G : (G + 1) / 2;
+  constexpr int H2 = G - H1;
+  float a1[H1];
+  uint32_t q1[H1];
+#pragma unroll
+  for (int i = 0; i < H1; ++i) {
+    a1[i] = acc[i];
+    q1[i] = qd[2 * i + hc];
+  }
+  dot_heads<DT, H1>(a1, q1, k);
+#pragma unroll
+  for (int i = 0; i < H1; ++i) acc[i] = a1[i];
+  if constexpr (H2 > 0) {
+    float a2[H2];
+    uint32_t q2[H2];
+#pragma unroll
+    for (int i = 0; i < H2; ++i) {
+      a2[i] = acc[H1 + i];
+      q2[i] = qd[2 * (H1 + i) + hc];
+    }
+    dot_heads<DT, H2>(a2, q2, k);
+#pragma unroll
+    for (int i = 0; i < H2; ++i) acc[H1 + i] = a2[i];
+  }
 }
 
 // Bias + RoPE of one pair (x1, x2) in f32, each product and the
@@ -196,7 +274,7 @@ __device__ __attribute__((always_inline)) inline float pick(const float (&x)[N],
   return r;
 }
 
-template <int DT, int D, int G, bool APPEND>
+template <int DT, int D, int G, bool APPEND, int W, int NB>
 __device__ void decode_impl(const DecodeArgs& A) {
   using S = DecodeGeo<D>;
   constexpr bool PV_DOT2 = (DT == kF16);
@@ -204,16 +282,33 @@ __device__ void decode_impl(const DecodeArgs& A) {
   constexpr int HD = D / 2;
   constexpr int GD = G * D;
   constexpr int NV = 8 * G;  // o values per lane: 8 dims x G heads
-  // K tiles, double-buffered.  Two arrays (not one of twice the size) so the
-  // compiler can tell which outstanding global_load_lds a read depends on.
-  __shared__ __attribute__((aligned(16))) char s_k0[S::KBYTES];
-  __shared__ __attribute__((aligned(16))) char s_k1[S::KBYTES];
-  __shared__ __attribute__((aligned(16))) uint32_t s_p[PWORDS];
-  __shared__ __attribute__((aligned(16))) uint16_t s_q[GD];
-  __shared__ __attribute__((aligned(16))) uint16_t s_knew[D];
-  __shared__ __attribute__((aligned(16))) uint16_t s_vnew[D];
+  constexpr int WS = W * S::TILE;  // tokens between two tiles of one wave
+  // Single-tile kernel: no vector-memory round trip before the KV stream.
+  // The wave's page numbers come through the scalar cache, and q by 4-byte
+  // direct-to-LDS loads issued between the tile's K and V loads (behind the
+  // same K wait), instead of vector loads that would queue behind the KV
+  // streams other waves of the CU have already issued.
+  constexpr bool FASTQ = NB == 1 && !APPEND;
+  constexpr int NQ = (GD * 2 + 255) / 256;  // 4-byte direct-to-LDS loads for q
+  // Per wave: NB K tile buffers (the first one later holds the wave's merge
+  // record: o[G*D], m[G], l[G]), the p exchange, and for the step variant the
+  // roped q and the new token's k and v.
+  // merge record: after the reduce-scatter, writer lane (j = lane / 16,
+  // chunk pv_ch) holds the o values j * NV/4 + k, k < NV/4 (value v: head
+  // v / 8, dim pv_ch * 8 + v % 8); it stores them at slot j * CH + pv_ch,
+  // NVP floats per slot, followed by m[G] and l[G] of the wave.
+  constexpr int NVP = (NV / 4 + 3) / 4 * 4;
+  constexpr int REC_ML = 4 * S::CH * NVP;
+  static_assert(REC_ML + 2 * G <= S::KBYTES / 4, "merge record fits a K buffer");
+  __shared__ __attribute__((aligned(16))) char s_k[W][NB][S::KBYTES];
+  __shared__ __attribute__((aligned(16))) uint32_t s_p[W][PWORDS];
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[APPEND ? W : 1][APPEND ? GD : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t s_knew[APPEND ? W : 1][APPEND ? D : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t s_vnew[APPEND ? W : 1][APPEND ? D : 8];
+  __shared__ __attribute__((aligned(16))) char s_qr[FASTQ ? W : 1][FASTQ ? NQ * 256 : 16];
 
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave of the workgroup
   const int pairs = A.batch * A.hkv;
   const int split = blockIdx.x / pairs;
   const int bh = blockIdx.x - split * pairs;
@@ -229,33 +324,74 @@ __device__ void decode_impl(const DecodeArgs& A) {
 
   // ---- prologue: position, the split's table entries and q together ----
   const int p0 = s_begin / kPage;  // lane j of tab0 / tab1: page j / 64 + j of the split
-  const int tab0 = trow[min(p0 + lane, tmax)];
-  const int tab1 = ST > 64 * kPage ? trow[min(p0 + 64 + lane, tmax)] : 0;
+  const int tab0 = FASTQ ? 0 : trow[min(p0 + lane, tmax)];
+  const int tab1 = !FASTQ && ST > 64 * kPage ? trow[min(p0 + 64 + lane, tmax)] : 0;
   // q registers: qd[2g + hc], lane (row-half qhalf, j = lane % 16) holds q
   // word g * D/2 + qhalf * 32 + hc * 16 + j of the row (32-bit words), where
   // qhalf = lane / 32 at head_dim 128 (the lane's 64 dims), else 0.
   const int qhalf = D == 128 ? lane / 32 : 0;
   auto q_word = [&](int m) { return (m / 2) * HD + qhalf * 32 + (m % 2) * 16 + (lane & 15); };
+  // single-tile kernel: the page numbers of the wave's tile, through the
+  // scalar cache in the same round trip as the position (clamped to the
+  // split once the position is known)
+  // (PAGES entries from tstart: inside the row, which the host guarantees
+  // holds at least PAGES entries for this kernel)
+  const int j0 = w * S::PAGES;  // first page of the wave's tile within the split
+  const int tstart = min(p0 + j0, tmax - (S::PAGES - 1));
+  int traw[S::PAGES];
+  if constexpr (FASTQ) {
+    typedef __attribute__((address_space(4))) const typename I32Vec<S::PAGES>::T vec_t;
+    const auto v = *(vec_t*)(trow + tstart);
+#pragma unroll
+    for (int i = 0; i < S::PAGES; ++i) traw[i] = v[i];
+  }
   uint32_t qd[2 * G];
-  if constexpr (!APPEND) {
+  if constexpr (!APPEND && !FASTQ) {
 #pragma unroll
     for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)qrow)[q_word(m)];
   }
-  const int pos = A.positions[b];
+  int pos = A.positions[b];
+  if constexpr (FASTQ) {
+    // the table entries and the position share one scalar round trip
+    // (readfirstlane: both are wave-uniform, it only names the register class)
+    pos = __builtin_amdgcn_readfirstlane(pos);
+#pragma unroll
+    for (int i = 0; i < S::PAGES; ++i)
+      asm volatile("" : "+s"(pos) : "s"(__builtin_amdgcn_readfirstlane(traw[i])));
+  }
   const int ctx = pos + 1;
   if (ctx < 1 || ctx > A.max_ctx) {
     // empty context (0/0 in the reference) or beyond the host bound: NaN
     if (split == 0)
-      for (int i = lane; i < GD; i += 64) out_row[i] = St<DT>::store(__builtin_nanf(""));
+      for (int i = threadIdx.x; i < GD; i += 64 * W) out_row[i] = St<DT>::store(__builtin_nanf(""));
     return;
   }
-  if (s_begin >= ctx) return;  // split past this context
+  if (s_begin >= ctx) return;  // split past this context (the whole workgroup)
   const int nsplit = (ctx + ST - 1) / ST;
   const int s_end = min(ctx, s_begin + ST);
-  const bool owns = APPEND && pos < s_end;  // the split holding the new token
+  // this wave's tiles: s_begin + (w + i * W) * TILE, i < ntw
+  const int t_first = s_begin + w * S::TILE;
+  const int ntw = t_first < s_end ? (s_end - t_first + WS - 1) / WS : 0;
+  // the wave whose tiles hold the new token (in the last split)
+  const bool owns = APPEND && pos >= s_begin && pos < s_end && ((pos - s_begin) / S::TILE) % W == w;
   auto page_of = [&](int j) -> int64_t {     // physical page j of the split (uniform j)
     return j < 64 ? __builtin_amdgcn_readlane(tab0, j) : __builtin_amdgcn_readlane(tab1, j - 64);
   };
+  const int jend = (s_end - 1 - s_begin) / kPage;  // last page of the split
+  // single-tile kernel: the pages of this wave's tile (clamped to the split)
+  int tpage[S::PAGES];
+  if constexpr (FASTQ) {
+#pragma unroll
+    for (int i = 0; i < S::PAGES; ++i) {
+      // entry of page min(j0 + i, jend) of the split in traw (waves without
+      // a tile issue nothing, the index is only kept in range for them)
+      const int e = min(max(min(p0 + j0 + i, p0 + jend) - tstart, 0), S::PAGES - 1);
+      int t = traw[0];
+#pragma unroll
+      for (int k = 1; k < S::PAGES; ++k) t = e == k ? traw[k] : t;
+      tpage[i] = t;
+    }
+  }
 
   // The step variant's prologue operands (q and k of the new token with their
   // biases, the cos/sin row, v + v_bias) are loaded before the KV stream is
@@ -304,41 +440,71 @@ __device__ void decode_impl(const DecodeArgs& A) {
   const uint32_t koff0 = k_lane_off(0), koff1 = k_lane_off(1);
   const uint32_t voff = (uint32_t)(pv_tok * S::ROWB + (pv_ch << 4));
 
-  // Issue one tile: all its K loads (into the LDS buffer) before its V loads
+  // Issue one tile: all its K loads (into K buffer buf) before its V loads
   // (into vr).  Pages past the split re-read the split's last page (a cache
   // hit), which keeps the number of loads per tile fixed at 8 + 8; a tile
   // that starts past the split (the odd tile of a pair) is all such pages.
-  const int jend = (s_end - 1 - s_begin) / kPage;  // last page of the split
-  auto issue = [&](int t0, int buf, uint4(&vr)[S::LOADS]) __attribute__((always_inline)) {
-    const int jbase = (t0 - s_begin) / kPage;
-    lds_char* kdma = (lds_char*)(buf ? s_k1 : s_k0);
+  // In the single-tile kernel q follows the K loads (NQ more loads).
+  auto phys_of = [&](int t0, int r) __attribute__((always_inline)) -> int64_t {
+    if constexpr (FASTQ) return tpage[r / S::LPP];  // (t0 is the wave's only tile)
+    else return page_of(min((t0 - s_begin) / kPage + r / S::LPP, jend));
+  };
+  auto issue_k = [&](int t0, int buf) __attribute__((always_inline)) {
+    lds_char* kdma = (lds_char*)s_k[w][buf];
 #pragma unroll
     for (int r = 0; r < S::LOADS; ++r) {
-      const int64_t phys = page_of(min(jbase + r / S::LPP, jend));
+      const int64_t phys = phys_of(t0, r);
       // wave-uniform slab base (scalar registers) + 32-bit lane offsets
       const char* kslab = (const char*)(A.k_pool + phys * page_stride + head_off);
       dma16(kslab + ((r & 1) ? koff1 : koff0), kdma + (r - r % S::LPP) * 1024,
             (r % S::LPP) * 1024);
     }
+    if constexpr (FASTQ) {
+#pragma unroll
+      for (int i = 0; i < NQ; ++i)
+        dma4((const char*)qrow + min(i * 256 + lane * 4, GD * 2 - 4), (lds_char*)s_qr[w] + i * 256);
+    }
+  };
+  auto issue_v = [&](int t0, uint4(&vr)[S::LOADS]) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < S::LOADS; ++r) {
-      const int64_t phys = page_of(min(jbase + r / S::LPP, jend));
+      const int64_t phys = phys_of(t0, r);
       const char* vslab = (const char*)(A.v_pool + phys * page_stride + head_off);
       vr[r] = ld_nt16((const uint16_t*)(vslab + voff + (r % S::LPP) * 1024));
     }
   };
+  auto issue = [&](int t0, int buf, uint4(&vr)[S::LOADS]) __attribute__((always_inline)) {
+    issue_k(t0, buf);
+    issue_v(t0, vr);
+  };
 
-  const int nt = (s_end - s_begin + S::TILE - 1) / S::TILE;
-  if constexpr (!APPEND) {
-    // q must have landed before the KV stream is issued (it came with the
-    // table and position loads): the compiler then needs no wait for it
-    // behind the stream.
+  // Everything loaded so far (q, or the step variant's operands) must have
+  // landed before the KV stream is issued (it came with the table and
+  // position loads): the compiler then needs no wait for it behind the
+  // stream, where it could only wait for the whole stream.
+  if constexpr (FASTQ) {
+  } else if constexpr (!APPEND) {
 #pragma unroll
     for (int m = 0; m < 2 * G; ++m) asm volatile("" ::"v"(qd[m]));
+  } else {
+#pragma unroll
+    for (int i = 0; i < NPAIR; ++i)
+      asm volatile("" ::"v"(rx1[i]), "v"(rx2[i]), "v"(rb1[i]), "v"(rb2[i]), "v"(rc[i]), "v"(rs[i]));
+#pragma unroll
+    for (int i = 0; i < S::QKL; ++i) asm volatile("" ::"v"(rv[i]), "v"(rvb[i]));
   }
   uint4 vr0[S::LOADS], vr1[S::LOADS];
-  issue(s_begin, 0, vr0);
-  issue(s_begin + S::TILE, 1, vr1);
+  if constexpr (NB == 1) {
+    // every wave's K (and q) goes out before any wave's V: the CU's memory
+    // pipeline returns them roughly in that order, so the scores of all the
+    // waves overlap the V stream and only PV is left once the last V lands
+    if (ntw > 0) issue_k(t_first, 0);
+    __builtin_amdgcn_s_barrier();
+    if (ntw > 0) issue_v(t_first, vr0);
+  } else if (ntw > 0) {
+    issue(t_first, 0, vr0);
+    issue(t_first + WS, 1, vr1);
+  }
 
   // ---- q of the G heads (roped in the step variant), new token's k, v ----
   if constexpr (APPEND) {
@@ -349,17 +515,17 @@ __device__ void decode_impl(const DecodeArgs& A) {
         const int g = idx / HD, j = idx % HD;
         uint16_t o1, o2;
         rot_pair<DT>(rx1[i], rb1[i], rx2[i], rb2[i], rc[i], rs[i], o1, o2);
-        uint16_t* dst = g < G ? s_q + g * D : s_knew;
+        uint16_t* dst = g < G ? s_q[w] + g * D : s_knew[w];
         dst[j] = o1;
         dst[j + HD] = o2;
       }
     }
 #pragma unroll
     for (int i = 0; i < S::QKL; ++i)
-      s_vnew[lane + 64 * i] = St<DT>::store(St<DT>::load(rv[i]) + St<DT>::load(rvb[i]));
+      s_vnew[w][lane + 64 * i] = St<DT>::store(St<DT>::load(rv[i]) + St<DT>::load(rvb[i]));
     wave_lds_sync();
 #pragma unroll
-    for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)s_q)[q_word(m)];
+    for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)s_q[w])[q_word(m)];
   }
 
   float m_run[G], l_lane[G], o[G][8];
@@ -373,12 +539,12 @@ __device__ void decode_impl(const DecodeArgs& A) {
 
   // ---- scores, online softmax and p exchange of the tile at t0 (K in buf) ----
   auto tile_scores = [&](int t0, int buf) __attribute__((always_inline)) {
-    char* const kb = buf ? s_k1 : s_k0;
+    char* const kb = s_k[w][buf];
     if constexpr (APPEND) {
       if (owns && pos >= t0 && pos < t0 + S::TILE && lane < S::CH) {
         const int t = pos - t0;  // the new token's K row (swizzled slots)
         *(uint4*)(kb + t * S::ROWB + lane * 16) =
-            *(const uint4*)(s_knew + ((lane ^ (t & 7)) * 8));
+            *(const uint4*)(s_knew[w] + ((lane ^ (t & 7)) * 8));
       }
       wave_lds_sync();
     }
@@ -392,8 +558,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
     for (int hc = 0; hc < 2; ++hc) {  // chunks 4*hc .. 4*hc+3 of the lane's 64 dims
       uint4 kc[4];
       lds_read4(ka(4 * hc), ka(4 * hc + 1), ka(4 * hc + 2), ka(4 * hc + 3), kc);
-#pragma unroll
-      for (int g = 0; g < G; ++g) acc[g] = dot16_bcast<DT>(acc[g], qd[2 * g + hc], kc);
+      dot_all_heads<DT, G>(acc, qd, hc, kc);
     }
     if constexpr (S::QKL == 2) {
 #pragma unroll
@@ -409,11 +574,16 @@ __device__ void decode_impl(const DecodeArgs& A) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float s = valid ? acc[g] * A.qk_scale_log2 : -INFINITY;
-      // wave-uniform: kept in a scalar register
-      const float mn = __builtin_bit_cast(
-          float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fmaxf(m_run[g], wave_max(s)))));
-      p[g] = __builtin_amdgcn_exp2f(s - mn);
-      if (mn > m_run[g]) {  // wave-uniform: rescale only when the max moves
+      // The reference point m_run[g] only has to keep exp2(s - m_run) small:
+      // it starts at the score of lane 0 (the tile's first token, always
+      // valid in a wave's first tile) and moves (wave-wide max, rescale of o
+      // and l) only when a score exceeds it by more than kLazyMax, which one
+      // ballot detects; p stays <= 2^kLazyMax.
+      if (m_run[g] == -INFINITY)  // wave-uniform: the wave's first tile
+        m_run[g] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, s)));
+      if (__builtin_amdgcn_ballot_w64(s > m_run[g] + kLazyMax) != 0) {  // wave-uniform
+        const float mn = __builtin_bit_cast(
+            float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fmaxf(m_run[g], wave_max(s)))));
         if (m_run[g] > -INFINITY) {  // (nothing accumulated before the first tile)
           const float alpha = __builtin_amdgcn_exp2f(m_run[g] - mn);
           l_lane[g] *= alpha;
@@ -422,25 +592,27 @@ __device__ void decode_impl(const DecodeArgs& A) {
         }
         m_run[g] = mn;
       }
+      p[g] = __builtin_amdgcn_exp2f(s - m_run[g]);
       l_lane[g] += qh == 0 ? p[g] : 0.0f;
     }
 
     // p to the load layout through LDS
+    uint32_t* const sp = s_p[w];
     if constexpr (PV_DOT2) {
       uint32_t pk[8];
 #pragma unroll
       for (int g = 0; g < 8; ++g) pk[g] = g < G ? pack_f16(p[g], upper_half_value<D>(p[g])) : 0u;
       if (lane < S::HALF) {
-        *(uint4*)(s_p + tq * 8) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        *(uint4*)(s_p + tq * 8 + 4) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+        *(uint4*)(sp + tq * 8) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        *(uint4*)(sp + tq * 8 + 4) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
       }
     } else {
       float pf[8];
 #pragma unroll
       for (int g = 0; g < 8; ++g) pf[g] = g < G ? p[g] : 0.0f;
       if (qh == 0) {
-        *(float4*)(s_p + tq * 8) = make_float4(pf[0], pf[1], pf[2], pf[3]);
-        *(float4*)(s_p + tq * 8 + 4) = make_float4(pf[4], pf[5], pf[6], pf[7]);
+        *(float4*)(sp + tq * 8) = make_float4(pf[0], pf[1], pf[2], pf[3]);
+        *(float4*)(sp + tq * 8 + 4) = make_float4(pf[4], pf[5], pf[6], pf[7]);
       }
     }
     wave_lds_sync();
@@ -453,12 +625,13 @@ __device__ void decode_impl(const DecodeArgs& A) {
         const int t = pos - t0;
 #pragma unroll
         for (int r = 0; r < S::LOADS; ++r)
-          if (r == t / S::TPL && pv_tok == t % S::TPL) vr[r] = *(const uint4*)(s_vnew + pv_ch * 8);
+          if (r == t / S::TPL && pv_tok == t % S::TPL) vr[r] = *(const uint4*)(s_vnew[w] + pv_ch * 8);
       }
     }
     // tokens past the split: V must contribute exactly zero (p is 0 there,
     // and 0 * stale data must not produce NaN)
     const bool partial = t0 + S::TILE > s_end;
+    const uint32_t* const sp = s_p[w];
     if constexpr (PV_DOT2) {
 #pragma unroll
       for (int r = 0; r < S::LOADS / 2; ++r) {
@@ -468,8 +641,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
           if (t0 + t >= s_end) va = make_uint4(0, 0, 0, 0);
           if (t0 + t + S::HALF >= s_end) vb = make_uint4(0, 0, 0, 0);
         }
-        const uint4 p0 = *(const uint4*)(s_p + t * 8);
-        const uint4 p1 = *(const uint4*)(s_p + t * 8 + 4);
+        const uint4 p0 = *(const uint4*)(sp + t * 8);
+        const uint4 p1 = *(const uint4*)(sp + t * 8 + 4);
         const uint32_t pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
         const uint32_t aw[4] = {va.x, va.y, va.z, va.w};
         const uint32_t bw[4] = {vb.x, vb.y, vb.z, vb.w};
@@ -490,8 +663,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
         const int t = r * S::TPL + pv_tok;
         uint4 v = vr[r];
         if (partial && t0 + t >= s_end) v = make_uint4(0, 0, 0, 0);
-        const float4 pa = *(const float4*)(s_p + t * 8);
-        const float4 pb = *(const float4*)(s_p + t * 8 + 4);
+        const float4 pa = *(const float4*)(sp + t * 8);
+        const float4 pb = *(const float4*)(sp + t * 8 + 4);
         const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
         const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
         float vv[8];
@@ -509,44 +682,67 @@ __device__ void decode_impl(const DecodeArgs& A) {
     wave_lds_sync();
   };
 
-  // ---- the split's tiles, in pairs: both tiles of a pair are issued
-  // (unconditionally, so that the loads keep their place ahead of the waits
-  // below), tile i is computed while tile i+1 lands.  In flight after issuing
-  // a pair: K_i V_i K_{i+1} V_{i+1}, 8 loads each, completing in issue order.
-  // The first pair was issued before the prologue; later pairs load into
-  // registers local to their iteration (no values carried around the loop).
-  auto pair_compute = [&](int t0, bool pair, uint4(&va)[S::LOADS], uint4(&vb)[S::LOADS])
-                          __attribute__((always_inline)) {
-    LUC_WAIT_VM(24);  // K_i
-    tile_scores(t0, 0);
-    LUC_WAIT_VM(16);  // V_i
-    tile_pv(t0, va);
-    if (pair) {
-      LUC_WAIT_VM(8);  // K_{i+1}
-      tile_scores(t0 + S::TILE, 1);
-      LUC_WAIT_VM(0);  // V_{i+1}
-      tile_pv(t0 + S::TILE, vb);
+  if constexpr (NB == 1) {
+    // at most one tile per wave (the split is W tiles)
+    if (ntw > 0) {
+      LUC_WAIT_VM(8);  // K and q
+      if constexpr (FASTQ) {  // q words from LDS: qd[m] = word q_word(m)
+        const uint32_t qa = lds_addr(s_qr[w]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
+        read_q_words<0, 2 * G, HD>(qa, qd);
+#pragma unroll
+        for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
+      }
+      tile_scores(t_first, 0);
+      LUC_WAIT_VM(0);  // V
+      tile_pv(t_first, vr0);
     }
-  };
-  pair_compute(s_begin, nt > 1, vr0, vr1);
-  for (int i = 2; i < nt; i += 2) {
-    const int t0 = s_begin + i * S::TILE;
-    uint4 va[S::LOADS], vb[S::LOADS];
-    issue(t0, 0, va);
-    issue(t0 + S::TILE, 1, vb);
-    pair_compute(t0, i + 1 < nt, va, vb);
+  } else {
+    // The wave's tiles in pairs: both tiles of a pair are issued
+    // (unconditionally, so that the loads keep their place ahead of the
+    // waits below), tile i is computed while tile i+1 lands.  In flight after
+    // issuing a pair: K_i V_i K_{i+1} V_{i+1}, 8 loads each, completing in
+    // issue order.  The first pair was issued before the prologue; later
+    // pairs load into registers local to their iteration (no values carried
+    // around the loop).
+    auto pair_compute = [&](int t0, bool pair, uint4(&va)[S::LOADS], uint4(&vb)[S::LOADS])
+                            __attribute__((always_inline)) {
+      LUC_WAIT_VM(24);  // K_i
+      tile_scores(t0, 0);
+      LUC_WAIT_VM(16);  // V_i
+      tile_pv(t0, va);
+      if (pair) {
+        LUC_WAIT_VM(8);  // K_{i+1}
+        tile_scores(t0 + WS, 1);
+        LUC_WAIT_VM(0);  // V_{i+1}
+        tile_pv(t0 + WS, vb);
+      }
+    };
+    if (ntw > 0) {
+      pair_compute(t_first, ntw > 1, vr0, vr1);
+      for (int i = 2; i < ntw; i += 2) {
+        const int t0 = t_first + i * WS;
+        uint4 va[S::LOADS], vb[S::LOADS];
+        issue(t0, 0, va);
+        issue(t0 + WS, 1, vb);
+        pair_compute(t0, i + 1 < ntw, va, vb);
+      }
+    }
   }
 
   if constexpr (APPEND) {
     if (owns && lane < S::CH) {  // the cache write of the new token
       const int64_t phys = page_of((pos - s_begin) / kPage);
       const int64_t slot = phys * page_stride + head_off + (int64_t)(pos % kPage) * D + lane * 8;
-      *(uint4*)(A.k_pool + slot) = *(const uint4*)(s_knew + lane * 8);
-      *(uint4*)(A.v_pool + slot) = *(const uint4*)(s_vnew + lane * 8);
+      *(uint4*)(A.k_pool + slot) = *(const uint4*)(s_knew[w] + lane * 8);
+      *(uint4*)(A.v_pool + slot) = *(const uint4*)(s_vnew[w] + lane * 8);
     }
   }
 
   // ---- reduce the wave's token groups (lanes sharing pv_ch): reduce-scatter ----
+  float lsum[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) lsum[g] = l_lane[g];
+  wave_sum_n<G>(lsum);
   float u[NV / 2], y[NV / 4];
 #pragma unroll
   for (int k = 0; k < NV / 2; ++k) {
@@ -565,37 +761,55 @@ __device__ void decode_impl(const DecodeArgs& A) {
 #pragma unroll
     for (int k = 0; k < NV / 4; ++k) y[k] += dpp_mov<0x128>(y[k]);  // row_ror:8
   }
+
+  // ---- merge the W waves through LDS: each wave's record (o, m, l) in its
+  // first K buffer (no loads into it are outstanding any more) ----
   // the lane holds o values base + k (value v: head v / 8, dim pv_ch * 8 + v % 8)
   const int base = ((lane >> 5) & 1) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);
   const bool writer = D == 128 || (lane & 8) == 0;
-  float lsum[G];
+  float* const recw = (float*)s_k[w][0];
+  if (writer) {
+    float* const slot = recw + ((lane >> 4) * S::CH + pv_ch) * NVP;
 #pragma unroll
-  for (int g = 0; g < G; ++g) lsum[g] = wave_sum(l_lane[g]);
-
-  if (nsplit == 1) {
-    if (writer) {
-#pragma unroll
-      for (int k = 0; k < NV / 4; ++k) {
-        const int kk = base + k, g = kk / 8;
-        out_row[g * D + pv_ch * 8 + (kk % 8)] = St<DT>::store(y[k] / pick(lsum, g));
-      }
-    }
-  } else {
-    // ---- this split's partial: o[G*D], (m, l)[G] ----
-    const int64_t rec = (int64_t)bh * A.max_splits + split;
-    float* wo = A.ws_o + rec * GD;
-    if (writer) {
-#pragma unroll
-      for (int k = 0; k < NV / 4; ++k) {
-        const int kk = base + k;
-        wo[(kk / 8) * D + pv_ch * 8 + (kk % 8)] = y[k];
-      }
-    }
+    for (int k = 0; k < NVP; k += 4)
+      *(float4*)(slot + k) = make_float4(y[k], k + 1 < NV / 4 ? y[k + 1] : 0.0f,
+                                         k + 2 < NV / 4 ? y[k + 2] : 0.0f,
+                                         k + 3 < NV / 4 ? y[k + 3] : 0.0f);
+  }
+  if (lane == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      if (lane == g) {
-        A.ws_ml[(rec * G + g) * 2] = m_run[g];
-        A.ws_ml[(rec * G + g) * 2 + 1] = lsum[g];
+      recw[REC_ML + g] = m_run[g];
+      recw[REC_ML + G + g] = lsum[g];
+    }
+  }
+  __syncthreads();
+  const int64_t rec = (int64_t)bh * A.max_splits + split;
+  for (int e = threadIdx.x; e < GD; e += 64 * W) {
+    const int g = e / D, d = e % D;
+    const int val = g * 8 + d % 8;  // the value's index in the reduce-scatter
+    const int idx = ((val / (NV / 4)) * S::CH + d / 8) * NVP + val % (NV / 4);
+    float mw[W], M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < W; ++v) {
+      mw[v] = ((const float*)s_k[v][0])[REC_ML + g];
+      M = fmaxf(M, mw[v]);
+    }
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int v = 0; v < W; ++v) {  // waves without tiles: m = -inf, weight 0
+      const float* rv2 = (const float*)s_k[v][0];
+      const float wt = __builtin_amdgcn_exp2f(mw[v] - M);
+      O = fmaf(wt, rv2[idx], O);
+      L = fmaf(wt, rv2[REC_ML + G + g], L);
+    }
+    if (nsplit == 1) {
+      out_row[e] = St<DT>::store(O / L);
+    } else {
+      A.ws_o[rec * GD + e] = O;
+      if (e % D == 0) {
+        A.ws_ml[(rec * G + g) * 2] = M;
+        A.ws_ml[(rec * G + g) * 2 + 1] = L;
       }
     }
   }
@@ -701,23 +915,23 @@ __device__ void combine_impl(const DecodeArgs& A) {
 
 }  // namespace luc
 
-// Resident-wave targets (waves per SIMD).
-#ifndef LUC_DECODE_OCC_f16
-#define LUC_DECODE_OCC_f16 __attribute__((amdgpu_waves_per_eu(2)))
-#endif
-#ifndef LUC_DECODE_OCC_bf16
-#define LUC_DECODE_OCC_bf16 __attribute__((amdgpu_waves_per_eu(2)))
-#endif
+// Decode kernels: kDecodeWaves = 4 waves per workgroup; _t1 keeps one tile
+// per wave (splits of 4 tiles), _t2 two tiles in flight per wave (longer
+// splits).  Resident-wave targets are per SIMD.
+#define LUC_DECODE_W 4
+#define LUC_DECODE_KERNELS(DTN, DT, D, G, NB, OCC)                                                  \
+  extern "C" __global__ __launch_bounds__(64 * LUC_DECODE_W) __attribute__((amdgpu_waves_per_eu(OCC))) \
+  void luc_decode_##DTN##_d##D##_g##G##_t##NB(luc::DecodeArgs a) {                                  \
+    luc::decode_impl<DT, D, G, false, LUC_DECODE_W, NB>(a);                                         \
+  }                                                                                                 \
+  extern "C" __global__ __launch_bounds__(64 * LUC_DECODE_W) __attribute__((amdgpu_waves_per_eu(OCC))) \
+  void luc_decode_step_##DTN##_d##D##_g##G##_t##NB(luc::DecodeArgs a) {                             \
+    luc::decode_impl<DT, D, G, true, LUC_DECODE_W, NB>(a);                                          \
+  }
 
 #define LUC_DECODE(DTN, DT, D, G)                                                                  \
-  extern "C" __global__ __launch_bounds__(64) LUC_DECODE_OCC_##DTN void luc_decode_##DTN##_d##D##_g##G( \
-      luc::DecodeArgs a) {                                                                         \
-    luc::decode_impl<DT, D, G, false>(a);                                                          \
-  }                                                                                                \
-  extern "C" __global__ __launch_bounds__(64) LUC_DECODE_OCC_##DTN void                           \
-      luc_decode_step_##DTN##_d##D##_g##G(luc::DecodeArgs a) {                                     \
-    luc::decode_impl<DT, D, G, true>(a);                                                           \
-  }                                                                                                \
+  LUC_DECODE_KERNELS(DTN, DT, D, G, 1, 2)                                                          \
+  LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2)                                                          \
   extern "C" __global__ __launch_bounds__(256) void luc_decode_combine_##DTN##_d##D##_g##G(        \
       luc::DecodeArgs a) {                                                                         \
     luc::combine_impl<DT, D, G, false>(a);                                                         \

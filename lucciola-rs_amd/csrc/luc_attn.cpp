@@ -56,13 +56,15 @@ int fail(int code, const char* fmt, ...) {
 constexpr const char* kCodeObjects[] = {"rope_append.hsaco", "paged_decode.hsaco"};
 
 // Kernel-side constants (kept in step with csrc/kernels/paged_decode.hip):
-// one wave per workgroup; tiles of 64 tokens (head_dim 64) or 32 (128); a
-// split's block-table entries are held in two registers (128 pages).
-constexpr int kDecodeWaves = 1;
+// four waves per workgroup, which share one split; tiles of 64 tokens
+// (head_dim 64) or 32 (128); a split's block-table entries are held in two
+// registers (128 pages).
+constexpr int kDecodeWaves = 4;
 int decode_tile(int head_dim) { return head_dim == 64 ? 64 : 32; }
 constexpr int kMaxSplitTokens = 128 * LUC_BLOCK_SIZE;
-// Waves the automatic split choice plans for: one per SIMD of an MI355X.
-constexpr int kPlanWaves = 256 * 4;
+// Tiles the automatic split choice plans to have in flight at once: about two
+// single-tile waves per SIMD of an MI355X (256 CUs x 4 SIMDs).
+constexpr int kPlanTiles = 256 * 4 * 2;
 
 const char* dt_name(int dtype) { return dtype == LUC_F16 ? "f16" : "bf16"; }
 
@@ -174,22 +176,25 @@ int check_cache(const void* k_pool, const void* v_pool, const int32_t* tables, i
 // Splits per sequence are capped at kMaxSplits (the merge's LDS weight table).
 constexpr int kMaxSplits = 256;
 
-// Split-K chunk length in tokens: a multiple of the tile, at most
-// kMaxSplitTokens.  The automatic choice assumes the mean context is half of
-// max_ctx and aims at about one wave per SIMD, each with at least two tiles
-// (the kernel keeps two tiles in flight).  It depends only on the arguments,
-// so luc_paged_decode_workspace_size agrees with the launch.  Returns 0 when
+// Split-K chunk length in tokens: a multiple of one tile per wave of a
+// workgroup (the unit), at most kMaxSplitTokens.  A split of one unit gives
+// each wave at most one tile (the _t1 kernels); longer splits walk two tiles
+// at a time per wave (_t2).  The automatic choice assumes the mean context is
+// half of max_ctx and takes the shortest split that keeps about kPlanTiles
+// tiles per round.  It depends only on the arguments, so
+// luc_paged_decode_workspace_size agrees with the launch.  Returns 0 when
 // max_ctx cannot be covered by kMaxSplits splits.
 int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requested) {
-  const int tile = decode_tile(head_dim);
-  const int64_t floor_tokens = ceil_div(ceil_div(max_ctx, kMaxSplits), tile) * tile;
+  const int unit = kDecodeWaves * decode_tile(head_dim);
+  const int64_t floor_tokens = ceil_div(ceil_div(max_ctx, kMaxSplits), unit) * unit;
   if (floor_tokens > kMaxSplitTokens) return 0;
   int64_t st;
   if (requested > 0) {
-    st = ceil_div(requested, tile) * tile;
+    st = ceil_div(requested, unit) * unit;
   } else {
-    const int64_t est = (int64_t)batch * hkv * std::max<int64_t>(ceil_div(max_ctx, 2), 1);
-    st = ceil_div(ceil_div(est, kPlanWaves), 2 * tile) * 2 * tile;
+    const int64_t tiles = (int64_t)batch * hkv *
+                          std::max<int64_t>(ceil_div(ceil_div(max_ctx, 2), decode_tile(head_dim)), 1);
+    st = ceil_div(tiles, kPlanTiles) * unit;
   }
   st = std::min<int64_t>(std::max<int64_t>(st, floor_tokens), kMaxSplitTokens);
   return (int)st;
@@ -258,7 +263,13 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
   const int group = num_q_heads / num_kv_heads;
   const std::string suffix = std::string(dt_name(dtype)) + "_d" + std::to_string(head_dim) + "_g" +
                              std::to_string(group);
-  if (int rc = get_fn(ctx, std::string(step ? "luc_decode_step_" : "luc_decode_") + suffix, &L->fn))
+  // the single-tile kernel reads a tile's table entries as one vector, which
+  // must fit the table row
+  const bool one_tile = st == kDecodeWaves * decode_tile(head_dim) &&
+                        table_stride >= decode_tile(head_dim) / LUC_BLOCK_SIZE;
+  if (int rc = get_fn(ctx, std::string(step ? "luc_decode_step_" : "luc_decode_") + suffix +
+                               (one_tile ? "_t1" : "_t2"),
+                      &L->fn))
     return rc;
   if (int rc = get_fn(ctx, std::string(step ? "luc_decode_step_combine_" : "luc_decode_combine_") +
                                suffix, &L->combine))
@@ -333,9 +344,16 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
     for (int d : {64, 128})
       for (int g = 1; g <= 8; ++g)
         for (const char* kind : {"luc_decode_", "luc_decode_step_", "luc_decode_combine_",
-                                 "luc_decode_step_combine_"})
-          names.push_back(std::string(kind) + dt + "_d" + std::to_string(d) + "_g" +
-                          std::to_string(g));
+                                 "luc_decode_step_combine_"}) {
+          const std::string n = std::string(kind) + dt + "_d" + std::to_string(d) + "_g" +
+                                std::to_string(g);
+          if (std::string(kind).find("combine") != std::string::npos) {
+            names.push_back(n);
+          } else {
+            names.push_back(n + "_t1");
+            names.push_back(n + "_t2");
+          }
+        }
   }
   for (const auto& n : names) {
     hipFunction_t fn = nullptr;

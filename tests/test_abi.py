@@ -104,12 +104,17 @@ def test_workspace_size_policy(cdll):
     assert ws(100, 28, 4, 128, 1000, 128) == expect(100, 28, 4, 128, 8)
     # at most 256 splits per sequence: the split grows with the context
     assert ws(1, 4, 1, 64, 64 * 1024, 64) == expect(1, 4, 1, 64, 256)
-    # rounding of the requested split to the tile (64 tokens at d=64, 32 at d=128)
-    assert ws(2, 14, 2, 64, 1000, 250) == ws(2, 14, 2, 64, 1000, 256)
-    assert ws(2, 14, 2, 128, 1000, 90) == ws(2, 14, 2, 128, 1000, 96)
+    # rounding of the requested split to one tile per wave of a workgroup
+    # (4 x 64 tokens at d=64, 4 x 32 at d=128)
+    assert ws(2, 14, 2, 64, 1000, 100) == ws(2, 14, 2, 64, 1000, 256)
+    assert ws(2, 14, 2, 64, 1000, 257) == expect(2, 14, 2, 64, 2)
+    assert ws(2, 14, 2, 128, 1000, 90) == ws(2, 14, 2, 128, 1000, 128)
     assert ws(1, 4, 1, 96, 1000, 0) == 0
-    # the automatic split aims at about one wave per SIMD (1024), two tiles each
-    assert ws(32, 14, 2, 64, 4096, 0) == expect(32, 14, 2, 64, 32)
+    # the automatic split keeps about 2048 tiles per round: the batch32_mixed
+    # shape (mean context about half of 4096) gets one tile per wave
+    assert ws(32, 14, 2, 64, 4096, 0) == expect(32, 14, 2, 64, 16)
+    # ... and longer batches get longer splits
+    assert ws(64, 28, 4, 128, 16384, 0) == expect(64, 28, 4, 128, 16384 // 2048)
     # a split holds at most 128 pages: longer contexts than 256 x 2048 tokens
     # are not supported
     assert ws(1, 4, 1, 64, 256 * 2048, 0) > 0
