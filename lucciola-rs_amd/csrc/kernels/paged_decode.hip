@@ -122,6 +122,29 @@ __device__ __attribute__((always_inline)) inline void read_q_words(uint32_t qa, 
   }
 }
 
+// The operands of one RoPE dword pair from LDS (byte addresses): x and bias
+// words at dims j and j + D/2, the cos and sin of dims j, j + 1; complete on
+// return.  asm for the reason given at lds_read4.
+__device__ inline void lds_read_rope(uint32_t ax1, uint32_t ax2, uint32_t ab1, uint32_t ab2, uint32_t ac,
+                                     uint32_t as, uint32_t& x1, uint32_t& x2, uint32_t& b1,
+                                     uint32_t& b2, uint2& c, uint2& sn) {
+  asm volatile(
+      "ds_read_b32 %0, %6\n\t"
+      "ds_read_b32 %1, %7\n\t"
+      "ds_read_b32 %2, %8\n\t"
+      "ds_read_b32 %3, %9\n\t"
+      "ds_read_b64 %4, %10\n\t"
+      "ds_read_b64 %5, %11\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x1), "=&v"(x2), "=&v"(b1), "=&v"(b2), "=&v"(c), "=&v"(sn)
+      : "v"(ax1), "v"(ax2), "v"(ab1), "v"(ab2), "v"(ac), "v"(as)
+      : "memory");
+}
+__device__ inline void lds_read2(uint32_t a0, uint32_t a1, uint32_t& x0, uint32_t& x1) {
+  asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(x0), "=&v"(x1) : "v"(a0), "v"(a1) : "memory");
+}
+
 typedef __attribute__((address_space(4))) const int const_i32;
 // N consecutive table entries in one scalar load (4-byte aligned).
 template <int N>
@@ -283,13 +306,25 @@ __device__ void decode_impl(const DecodeArgs& A) {
   constexpr int GD = G * D;
   constexpr int NV = 8 * G;  // o values per lane: 8 dims x G heads
   constexpr int WS = W * S::TILE;  // tokens between two tiles of one wave
-  // Single-tile kernel: no vector-memory round trip before the KV stream.
-  // The wave's page numbers come through the scalar cache, and q by 4-byte
-  // direct-to-LDS loads issued between the tile's K and V loads (behind the
-  // same K wait), instead of vector loads that would queue behind the KV
-  // streams other waves of the CU have already issued.
-  constexpr bool FASTQ = NB == 1 && !APPEND;
+  // Single-tile kernels (T1): no vector-memory round trip before the KV
+  // stream.  The wave's page numbers come through the scalar cache, and q
+  // (FASTQ), or the step variant's operands (FASTA: q, k, v, their biases,
+  // the cos/sin rows), by 4-byte direct-to-LDS loads issued between the
+  // tile's K and V loads (behind the same K wait), instead of vector loads
+  // that would queue behind the KV streams other waves of the CU have
+  // already issued.
+  constexpr bool T1 = NB == 1;
+  constexpr bool FASTQ = T1 && !APPEND;
+  constexpr bool FASTA = T1 && APPEND;
   constexpr int NQ = (GD * 2 + 255) / 256;  // 4-byte direct-to-LDS loads for q
+  // FASTA operand block: q of the G heads, then their biases (256-byte
+  // padded), then six regions of 2*D bytes: k, k bias, cos, sin, v, v bias.
+  constexpr int SR = 2 * D;
+  constexpr int PA_XQ = 0, PA_BQ = NQ * 256, PA_SM = 2 * NQ * 256;
+  constexpr int PA_K = PA_SM, PA_KB = PA_SM + SR, PA_C = PA_SM + 2 * SR, PA_S = PA_SM + 3 * SR;
+  constexpr int PA_V = PA_SM + 4 * SR, PA_VB = PA_SM + 5 * SR;
+  constexpr int NSM = 6 * SR / 256;  // loads for the six small regions
+  constexpr int PBYTES = PA_SM + 6 * SR;
   // Per wave: NB K tile buffers (the first one later holds the wave's merge
   // record: o[G*D], m[G], l[G]), the p exchange, and for the step variant the
   // roped q and the new token's k and v.
@@ -306,6 +341,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   __shared__ __attribute__((aligned(16))) uint16_t s_knew[APPEND ? W : 1][APPEND ? D : 8];
   __shared__ __attribute__((aligned(16))) uint16_t s_vnew[APPEND ? W : 1][APPEND ? D : 8];
   __shared__ __attribute__((aligned(16))) char s_qr[FASTQ ? W : 1][FASTQ ? NQ * 256 : 16];
+  __shared__ __attribute__((aligned(16))) char s_pa[FASTA ? W : 1][FASTA ? PBYTES : 16];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave of the workgroup
@@ -324,8 +360,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
 
   // ---- prologue: position, the split's table entries and q together ----
   const int p0 = s_begin / kPage;  // lane j of tab0 / tab1: page j / 64 + j of the split
-  const int tab0 = FASTQ ? 0 : trow[min(p0 + lane, tmax)];
-  const int tab1 = !FASTQ && ST > 64 * kPage ? trow[min(p0 + 64 + lane, tmax)] : 0;
+  const int tab0 = T1 ? 0 : trow[min(p0 + lane, tmax)];
+  const int tab1 = !T1 && ST > 64 * kPage ? trow[min(p0 + 64 + lane, tmax)] : 0;
   // q registers: qd[2g + hc], lane (row-half qhalf, j = lane % 16) holds q
   // word g * D/2 + qhalf * 32 + hc * 16 + j of the row (32-bit words), where
   // qhalf = lane / 32 at head_dim 128 (the lane's 64 dims), else 0.
@@ -339,7 +375,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   const int j0 = w * S::PAGES;  // first page of the wave's tile within the split
   const int tstart = min(p0 + j0, tmax - (S::PAGES - 1));
   int traw[S::PAGES];
-  if constexpr (FASTQ) {
+  if constexpr (T1) {
     typedef __attribute__((address_space(4))) const typename I32Vec<S::PAGES>::T vec_t;
     const auto v = *(vec_t*)(trow + tstart);
 #pragma unroll
@@ -351,7 +387,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
     for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)qrow)[q_word(m)];
   }
   int pos = A.positions[b];
-  if constexpr (FASTQ) {
+  if constexpr (T1) {
     // the table entries and the position share one scalar round trip
     // (readfirstlane: both are wave-uniform, it only names the register class)
     pos = __builtin_amdgcn_readfirstlane(pos);
@@ -380,7 +416,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   const int jend = (s_end - 1 - s_begin) / kPage;  // last page of the split
   // single-tile kernel: the pages of this wave's tile (clamped to the split)
   int tpage[S::PAGES];
-  if constexpr (FASTQ) {
+  if constexpr (T1) {
 #pragma unroll
     for (int i = 0; i < S::PAGES; ++i) {
       // entry of page min(j0 + i, jend) of the split in traw (waves without
@@ -399,7 +435,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   constexpr int NPAIR = APPEND ? ((G + 1) * HD + 63) / 64 : 1;
   uint16_t rx1[NPAIR], rx2[NPAIR], rb1[NPAIR], rb2[NPAIR], rv[S::QKL], rvb[S::QKL];
   float rc[NPAIR], rs[NPAIR];
-  if constexpr (APPEND) {
+  if constexpr (APPEND && !T1) {
     const float* crow = A.cos_t + (int64_t)pos * HD;
     const float* srow = A.sin_t + (int64_t)pos * HD;
     const uint16_t* krow = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
@@ -446,7 +482,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   // that starts past the split (the odd tile of a pair) is all such pages.
   // In the single-tile kernel q follows the K loads (NQ more loads).
   auto phys_of = [&](int t0, int r) __attribute__((always_inline)) -> int64_t {
-    if constexpr (FASTQ) return tpage[r / S::LPP];  // (t0 is the wave's only tile)
+    if constexpr (T1) return tpage[r / S::LPP];  // (t0 is the wave's only tile)
     else return page_of(min((t0 - s_begin) / kPage + r / S::LPP, jend));
   };
   auto issue_k = [&](int t0, int buf) __attribute__((always_inline)) {
@@ -463,6 +499,33 @@ __device__ void decode_impl(const DecodeArgs& A) {
 #pragma unroll
       for (int i = 0; i < NQ; ++i)
         dma4((const char*)qrow + min(i * 256 + lane * 4, GD * 2 - 4), (lds_char*)s_qr[w] + i * 256);
+    }
+    if constexpr (FASTA) {
+      // the operand block; a missing bias reads the operand itself (ignored)
+      const char* krow = (const char*)(A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D);
+      const char* vrow = (const char*)(A.v_new + (int64_t)b * A.q_stride + (int64_t)h * D);
+      const char* qb = A.q_bias ? (const char*)(A.q_bias + (int64_t)h * GD) : (const char*)qrow;
+      const char* kb = A.k_bias ? (const char*)(A.k_bias + (int64_t)h * D) : krow;
+      const char* vb = A.v_bias ? (const char*)(A.v_bias + (int64_t)h * D) : vrow;
+      const char* cr = (const char*)(A.cos_t + (int64_t)pos * HD);
+      const char* sr = (const char*)(A.sin_t + (int64_t)pos * HD);
+      lds_char* pa = (lds_char*)s_pa[w];
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) {
+        const int off = min(i * 256 + lane * 4, GD * 2 - 4);
+        dma4((const char*)qrow + off, pa + PA_XQ + i * 256);
+        dma4(qb + off, pa + PA_BQ + i * 256);
+      }
+      const char* small[6] = {krow, kb, cr, sr, vrow, vb};
+#pragma unroll
+      for (int i = 0; i < NSM; ++i) {
+        const int o = i * 256 + lane * 4;  // byte of the six regions
+        const int reg = o / SR;
+        const char* src = small[0];
+#pragma unroll
+        for (int k = 1; k < 6; ++k) src = reg == k ? small[k] : src;
+        dma4(src + (o - reg * SR), pa + PA_SM + i * 256);
+      }
     }
   };
   auto issue_v = [&](int t0, uint4(&vr)[S::LOADS]) __attribute__((always_inline)) {
@@ -482,7 +545,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   // landed before the KV stream is issued (it came with the table and
   // position loads): the compiler then needs no wait for it behind the
   // stream, where it could only wait for the whole stream.
-  if constexpr (FASTQ) {
+  if constexpr (T1) {
   } else if constexpr (!APPEND) {
 #pragma unroll
     for (int m = 0; m < 2 * G; ++m) asm volatile("" ::"v"(qd[m]));
@@ -507,7 +570,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   }
 
   // ---- q of the G heads (roped in the step variant), new token's k, v ----
-  if constexpr (APPEND) {
+  if constexpr (APPEND && !T1) {
 #pragma unroll
     for (int i = 0; i < NPAIR; ++i) {
       const int idx = lane + i * 64;
@@ -692,6 +755,57 @@ __device__ void decode_impl(const DecodeArgs& A) {
 #pragma unroll
         for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
       }
+      if constexpr (FASTA) {
+        // bias + RoPE of q (G heads) and k of the new token, in dword pairs
+        // (dims j, j + 1 and j + D/2, j + D/2 + 1) from the operand block;
+        // v + v_bias
+        const uint32_t pa = lds_addr(s_pa[w]);
+        constexpr int NP2 = (G + 1) * HD / 2;
+        const bool hqb = A.q_bias != nullptr, hkb = A.k_bias != nullptr, hvb = A.v_bias != nullptr;
+#pragma unroll
+        for (int i = 0; i < (NP2 + 63) / 64; ++i) {
+          const int idx = lane + 64 * i;
+          if (idx < NP2) {
+            const int g = idx / (HD / 2), j = (idx % (HD / 2)) * 2;
+            const uint32_t xb = pa + (g < G ? PA_XQ + g * D * 2 : PA_K);
+            const uint32_t bb = pa + (g < G ? PA_BQ + g * D * 2 : PA_KB);
+            uint32_t x1, x2, b1, b2;
+            uint2 c, sn;
+            lds_read_rope(xb + j * 2, xb + (j + HD) * 2, bb + j * 2, bb + (j + HD) * 2,
+                          pa + PA_C + j * 4, pa + PA_S + j * 4, x1, x2, b1, b2, c, sn);
+            if (!(g < G ? hqb : hkb)) b1 = b2 = 0u;
+            uint16_t o1a, o2a, o1b, o2b;
+            rot_pair<DT>(x1 & 0xffff, b1 & 0xffff, x2 & 0xffff, b2 & 0xffff, __uint_as_float(c.x),
+                         __uint_as_float(sn.x), o1a, o2a);
+            rot_pair<DT>(x1 >> 16, b1 >> 16, x2 >> 16, b2 >> 16, __uint_as_float(c.y),
+                         __uint_as_float(sn.y), o1b, o2b);
+            const uint32_t lo = (uint32_t)o1a | ((uint32_t)o1b << 16);
+            const uint32_t hi = (uint32_t)o2a | ((uint32_t)o2b << 16);
+            if (g < G) {  // (two stores with known targets: no alias with the loads into LDS)
+              *(uint32_t*)(s_q[w] + g * D + j) = lo;
+              *(uint32_t*)(s_q[w] + g * D + j + HD) = hi;
+            } else {
+              *(uint32_t*)(s_knew[w] + j) = lo;
+              *(uint32_t*)(s_knew[w] + j + HD) = hi;
+            }
+          }
+        }
+        if (lane < D / 2) {
+          uint32_t vv, vbv;
+          lds_read2(pa + PA_V + lane * 4, pa + PA_VB + lane * 4, vv, vbv);
+          if (!hvb) vbv = 0u;
+          const uint16_t lo = St<DT>::store(St<DT>::load(vv & 0xffff) + St<DT>::load(vbv & 0xffff));
+          const uint16_t hi = St<DT>::store(St<DT>::load(vv >> 16) + St<DT>::load(vbv >> 16));
+          *(uint32_t*)(s_vnew[w] + 2 * lane) = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        wave_lds_sync();
+        // q words (as in the plain kernel; compiler-visible reads of LDS would
+        // wait for every outstanding load)
+        const uint32_t qa = lds_addr(s_q[w]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
+        read_q_words<0, 2 * G, HD>(qa, qd);
+#pragma unroll
+        for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
+      }
       tile_scores(t_first, 0);
       LUC_WAIT_VM(0);  // V
       tile_pv(t_first, vr0);
@@ -731,7 +845,16 @@ __device__ void decode_impl(const DecodeArgs& A) {
 
   if constexpr (APPEND) {
     if (owns && lane < S::CH) {  // the cache write of the new token
-      const int64_t phys = page_of((pos - s_begin) / kPage);
+      int64_t phys;
+      if constexpr (T1) {  // in the owner's only tile: one of its pages
+        const int jt = (pos - t_first) / kPage;
+        int t = tpage[0];
+#pragma unroll
+        for (int k = 1; k < S::PAGES; ++k) t = jt == k ? tpage[k] : t;
+        phys = t;
+      } else {
+        phys = page_of((pos - s_begin) / kPage);
+      }
       const int64_t slot = phys * page_stride + head_off + (int64_t)(pos % kPage) * D + lane * 8;
       *(uint4*)(A.k_pool + slot) = *(const uint4*)(s_knew[w] + lane * 8);
       *(uint4*)(A.v_pool + slot) = *(const uint4*)(s_vnew[w] + lane * 8);
@@ -835,6 +958,37 @@ __device__ void combine_impl(const DecodeArgs& A) {
   const int ctx = pos + 1;
   if (ctx < 1 || ctx > A.max_ctx) return;  // the decode kernel wrote NaN
   const int nsplit = (ctx + A.split_tokens - 1) / A.split_tokens;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // The partials go out first: o of the first SB splits and (m, l) of every
+  // split (wave w reads heads w, w + 4, ...), so that their round trip
+  // overlaps the step variant's q/k write-back below.
+  constexpr int GW = (G + NT / 64 - 1) / (NT / 64);  // heads per wave
+  const float* ml = A.ws_ml + (int64_t)bh * A.max_splits * G * 2;
+  const float* po = A.ws_o + (int64_t)bh * A.max_splits * GD;
+  float ob[SB][NE];
+  auto load_batch = [&](int s0) {
+#pragma unroll
+    for (int j = 0; j < SB; ++j)
+#pragma unroll
+      for (int c = 0; c < NE; ++c) {
+        const int e = min((int)threadIdx.x + NT * c, GD - 1);
+        ob[j][c] = po[(int64_t)min(s0 + j, nsplit - 1) * GD + e];
+      }
+  };
+  float mv[GW][4], lv[GW][4];
+  if (nsplit > 1) {
+    load_batch(0);
+#pragma unroll
+    for (int gi = 0; gi < GW; ++gi) {
+      const int g = min(w + (NT / 64) * gi, G - 1);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int s = lane + 64 * k;
+        mv[gi][k] = s < nsplit ? ml[((int64_t)s * G + g) * 2] : -INFINITY;
+        lv[gi][k] = s < nsplit ? ml[((int64_t)s * G + g) * 2 + 1] : 0.0f;
+      }
+    }
+  }
   if constexpr (APPEND) {
     const float* crow = A.cos_t + (int64_t)pos * HD;
     const float* srow = A.sin_t + (int64_t)pos * HD;
@@ -853,40 +1007,23 @@ __device__ void combine_impl(const DecodeArgs& A) {
     }
   }
   if (nsplit <= 1) return;  // the decode kernel wrote the output
-  const float* ml = A.ws_ml + (int64_t)bh * A.max_splits * G * 2;
-  const float* po = A.ws_o + (int64_t)bh * A.max_splits * GD;
-  // o of the first batch of splits goes out before the weights are known
-  float ob[SB][NE];
-  auto load_batch = [&](int s0) {
+  // weights of the splits: 2^(m_s - M), and L = sum l_s 2^(m_s - M)
 #pragma unroll
-    for (int j = 0; j < SB; ++j)
+  for (int gi = 0; gi < GW; ++gi) {
+    const int g = w + (NT / 64) * gi;
+    if (g < G) {
+      const float M =
+          wave_max(fmaxf(fmaxf(mv[gi][0], mv[gi][1]), fmaxf(mv[gi][2], mv[gi][3])));
+      float L = 0.0f;
 #pragma unroll
-      for (int c = 0; c < NE; ++c) {
-        const int e = min((int)threadIdx.x + NT * c, GD - 1);
-        ob[j][c] = po[(int64_t)min(s0 + j, nsplit - 1) * GD + e];
+      for (int k = 0; k < 4; ++k) {
+        const float wgt = __builtin_amdgcn_exp2f(mv[gi][k] - M);  // 0 past nsplit
+        s_w[g][lane + 64 * k] = wgt;
+        L = fmaf(wgt, lv[gi][k], L);
       }
-  };
-  load_batch(0);
-  // weights: wave w handles heads w, w + 4, ...
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int g = w; g < G; g += NT / 64) {
-    float mv[4], lv[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int s = lane + 64 * k;
-      mv[k] = s < nsplit ? ml[((int64_t)s * G + g) * 2] : -INFINITY;
-      lv[k] = s < nsplit ? ml[((int64_t)s * G + g) * 2 + 1] : 0.0f;
+      L = wave_sum(L);
+      if (lane == 0) s_L[g] = L;
     }
-    const float M = wave_max(fmaxf(fmaxf(mv[0], mv[1]), fmaxf(mv[2], mv[3])));
-    float L = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float wgt = __builtin_amdgcn_exp2f(mv[k] - M);  // 0 past nsplit
-      s_w[g][lane + 64 * k] = wgt;
-      L = fmaf(wgt, lv[k], L);
-    }
-    L = wave_sum(L);
-    if (lane == 0) s_L[g] = L;
   }
   __syncthreads();
   float acc[NE];
