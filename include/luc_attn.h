@@ -152,6 +152,31 @@ int luc_decode_step(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qk
                     int split_tokens, void* out, int64_t out_row_stride, void* workspace,
                     size_t workspace_bytes);
 
+/* Causal prefill of packed prompts: the engine's per-token prefill loop
+ * (Qwen2Model::forward_layer, src/models.rs:485-550 -- rope
+ * (src/kernels/rope.cu), the cache write (src/kernels/kv_cache.cu) and
+ * flash_decoding (src/kernels/attention.cu:4-176) for each prompt token in
+ * turn) for whole prompts at once.  Rows cu_seqlens[b] .. cu_seqlens[b+1]-1 of
+ * qkv ([q (Hq*d) | k (Hkv*d) | v (Hkv*d)] at qkv + r*qkv_row_stride) are the
+ * prompt of sequence b, at positions start_pos[b] + (r - cu_seqlens[b]) of
+ * table row b (cu_seqlens and start_pos are device int32 arrays of batch+1
+ * and batch entries; total_rows = cu_seqlens[batch]).  Every row's q and k
+ * get bias + RoPE in place, its roped k and v + v_bias go to the cache, and
+ * every row attends to positions 0..its own of its sequence (the cached
+ * prefix and the prompt rows up to itself); out row r = out + r*out_row_stride,
+ * [Hq][head_dim].  max_ctx is a host-side upper bound of start_pos[b] plus the
+ * rows of b; a sequence beyond it gets NaN outputs.  qkv must be 16-byte
+ * aligned with a row stride that is a multiple of 8 elements; out 8-byte
+ * aligned with a row stride that is a multiple of 4.  Biases may be NULL.
+ * Attention runs on bf16/fp16 MFMA (v_mfma_f32_32x32x16). */
+int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qkv_row_stride,
+                      const void* q_bias, const void* k_bias, const void* v_bias,
+                      const float* cos_table, const float* sin_table, void* k_pool, void* v_pool,
+                      const int32_t* block_tables, int table_stride, const int32_t* cu_seqlens,
+                      const int32_t* start_pos, int batch, int total_rows, int max_ctx, int layer,
+                      int num_layers, int num_q_heads, int num_kv_heads, int head_dim,
+                      int block_size, float sm_scale, void* out, int64_t out_row_stride);
+
 #ifdef __cplusplus
 }
 #endif

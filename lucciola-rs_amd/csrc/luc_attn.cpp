@@ -53,7 +53,8 @@ int fail(int code, const char* fmt, ...) {
     if (e_ != hipSuccess) return fail(LUC_E_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
   } while (0)
 
-constexpr const char* kCodeObjects[] = {"rope_append.hsaco", "paged_decode.hsaco"};
+constexpr const char* kCodeObjects[] = {"rope_append.hsaco", "paged_decode.hsaco",
+                                         "paged_prefill.hsaco"};
 
 // Kernel-side constants (kept in step with csrc/kernels/paged_decode.hip):
 // four waves per workgroup, which share one split; tiles of 64 tokens
@@ -302,6 +303,23 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
   return LUC_OK;
 }
 
+// Argument block of the prefill attention kernel (paged_prefill.hip,
+// luc::PrefillArgs): the same fixed-size fields in the same order.
+struct PrefillArgs {
+  const void* qkv;
+  int64_t qkv_stride;
+  const void* k_pool;
+  const void* v_pool;
+  const int32_t* tables;
+  int64_t table_stride;
+  const int32_t* cu_seqlens;
+  const int32_t* start_pos;
+  void* out;
+  int64_t out_stride;
+  int32_t batch, layer, num_layers, hkv, max_ctx, row_tiles;
+  float qk_scale_log2;
+};
+
 int launch_decode(DecodeLaunch& L, void* stream) {
   void* args[] = {&L.a};
   if (int rc = launch(L.fn, L.grid, dim3(kDecodeWaves * 64), stream, args)) return rc;
@@ -341,6 +359,10 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
   std::vector<std::string> names;
   for (const char* dt : {"bf16", "f16"}) {
     names.push_back(std::string("luc_rope_append_") + dt);
+    for (int d : {64, 128})
+      for (int g = 1; g <= 8; ++g)
+        names.push_back(std::string("luc_prefill_") + dt + "_d" + std::to_string(d) + "_g" +
+                        std::to_string(g));
     for (int d : {64, 128})
       for (int g = 1; g <= 8; ++g)
         for (const char* kind : {"luc_decode_", "luc_decode_step_", "luc_decode_combine_",
@@ -516,6 +538,67 @@ int luc_decode_step(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qk
   L.a.cos_t = cos_table;
   L.a.sin_t = sin_table;
   return launch_decode(L, stream);
+}
+
+int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qkv_row_stride,
+                      const void* q_bias, const void* k_bias, const void* v_bias,
+                      const float* cos_table, const float* sin_table, void* k_pool, void* v_pool,
+                      const int32_t* block_tables, int table_stride, const int32_t* cu_seqlens,
+                      const int32_t* start_pos, int batch, int total_rows, int max_ctx, int layer,
+                      int num_layers, int num_q_heads, int num_kv_heads, int head_dim,
+                      int block_size, float sm_scale, void* out, int64_t out_row_stride) {
+  if (int rc = check_common(ctx, dtype, head_dim)) return rc;
+  if (int rc = check_heads(num_q_heads, num_kv_heads)) return rc;
+  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers, block_size))
+    return rc;
+  if (batch < 0 || total_rows < 0) return fail(LUC_E_INVALID, "batch %d / total_rows %d < 0", batch, total_rows);
+  if (max_ctx <= 0) return fail(LUC_E_INVALID, "max_ctx %d <= 0", max_ctx);
+  if (!qkv || !cos_table || !sin_table || !cu_seqlens || !start_pos || !out)
+    return fail(LUC_E_INVALID, "null qkv, rope table, cu_seqlens, start_pos or out");
+  const int row = num_q_heads * head_dim;
+  if (qkv_row_stride < (int64_t)(num_q_heads + 2 * num_kv_heads) * head_dim || out_row_stride < row)
+    return fail(LUC_E_INVALID, "qkv/out row stride smaller than a row");
+  // q rows are read as 16-byte vectors and outputs written as 8-byte vectors
+  if (!aligned(qkv, 16) || qkv_row_stride % 8)
+    return fail(LUC_E_INVALID, "qkv must be 16-byte aligned with a row stride that is a multiple of 8");
+  if (!aligned(out, 8) || out_row_stride % 4)
+    return fail(LUC_E_INVALID, "out must be 8-byte aligned with a row stride that is a multiple of 4");
+  if ((int64_t)table_stride * LUC_BLOCK_SIZE < max_ctx)
+    return fail(LUC_E_INVALID, "table_stride %d pages cannot hold max_ctx %d", table_stride, max_ctx);
+  if (batch == 0 || total_rows == 0) return LUC_OK;
+  if (int rc = check_device(ctx)) return rc;
+  const int group = num_q_heads / num_kv_heads;
+  hipFunction_t fn;
+  if (int rc = get_fn(ctx, std::string("luc_prefill_") + dt_name(dtype) + "_d" +
+                               std::to_string(head_dim) + "_g" + std::to_string(group),
+                      &fn))
+    return rc;
+  const int row_tiles = (int)ceil_div(total_rows, 32);
+  const int64_t grid = (int64_t)batch * num_kv_heads * row_tiles;
+  if (grid > INT32_MAX) return fail(LUC_E_INVALID, "batch x kv heads x row tiles too large");
+
+  // 1) bias + RoPE of every prompt row's q and k in place, cache write of the
+  //    roped k and v + v_bias (models.rs:505-534 for each row)
+  uint16_t* base = static_cast<uint16_t*>(qkv);
+  AppendArgs a;
+  a.q = base; a.q_bias = q_bias; a.k = base + (int64_t)num_q_heads * head_dim; a.k_bias = k_bias;
+  a.v = base + (int64_t)(num_q_heads + num_kv_heads) * head_dim; a.v_bias = v_bias;
+  a.row_stride = qkv_row_stride; a.cos_t = cos_table; a.sin_t = sin_table;
+  a.cu_seqlens = cu_seqlens; a.start_pos = start_pos; a.batch = batch;
+  a.tables = block_tables; a.table_stride = table_stride; a.k_pool = k_pool; a.v_pool = v_pool;
+  a.layer = layer; a.num_layers = num_layers; a.hq = num_q_heads; a.hkv = num_kv_heads;
+  a.head_dim = head_dim; a.flags = kRopeQ | kRopeK | kWriteKV;
+  if (int rc = launch_append(ctx, stream, dtype, total_rows, a)) return rc;
+
+  // 2) causal attention of every row over the cache (models.rs:536-549 per row)
+  PrefillArgs p{};
+  p.qkv = qkv; p.qkv_stride = qkv_row_stride; p.k_pool = k_pool; p.v_pool = v_pool;
+  p.tables = block_tables; p.table_stride = table_stride; p.cu_seqlens = cu_seqlens;
+  p.start_pos = start_pos; p.out = out; p.out_stride = out_row_stride; p.batch = batch;
+  p.layer = layer; p.num_layers = num_layers; p.hkv = num_kv_heads; p.max_ctx = max_ctx;
+  p.row_tiles = row_tiles; p.qk_scale_log2 = sm_scale * 1.4426950408889634f;
+  void* args[] = {&p};
+  return launch(fn, dim3((unsigned)grid), dim3(64 * group), stream, args);
 }
 
 }  // extern "C"

@@ -44,6 +44,9 @@ SIGNATURES = {
     "luc_decode_step": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                _i32, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                _i32, _vp, _i64, _vp, _sz]),
+    "luc_paged_prefill": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                 _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                 _i32, _i32, _f32, _vp, _i64]),
 }
 
 
@@ -185,6 +188,20 @@ class LucAttn:
             head_dim, block_size, sm_scale, split_tokens, _p(out),
             out_row_stride if out_row_stride is not None else hq * head_dim, _p(workspace),
             ws_bytes))
+
+    def paged_prefill(self, qkv, q_bias, k_bias, v_bias, cos, sin, k_pool, v_pool, tables,
+                      cu_seqlens, start_pos, total_rows, max_ctx, layer, num_layers, hq, hkv,
+                      head_dim, sm_scale, out, qkv_row_stride=None, out_row_stride=None,
+                      block_size=16, stream=None):
+        """luc_paged_prefill: rope + cache write + causal attention of packed
+        prompts (cu_seqlens [B+1], start_pos [B] device int32)."""
+        self._check(self.lib.luc_paged_prefill(
+            self.ctx, _stream(stream), dtype_code(k_pool), _p(qkv),
+            qkv_row_stride if qkv_row_stride is not None else (hq + 2 * hkv) * head_dim,
+            _p(q_bias), _p(k_bias), _p(v_bias), _p(cos), _p(sin), _p(k_pool), _p(v_pool),
+            _p(tables), tables.shape[-1], _p(cu_seqlens), _p(start_pos), start_pos.shape[0],
+            total_rows, max_ctx, layer, num_layers, hq, hkv, head_dim, block_size, sm_scale,
+            _p(out), out_row_stride if out_row_stride is not None else hq * head_dim))
 
     def workspace(self, batch, hq, hkv, head_dim, max_ctx, split_tokens=0, device=None):
         """A zero-filled decode workspace (None when no split-K is needed)."""

@@ -178,3 +178,102 @@ def decode_bytes(cfg: DecodeConfig, ctx: np.ndarray) -> int:
     table = int((((c + PAGE - 1) // PAGE) * 4).sum())
     append = cfg.batch * cfg.hkv * cfg.head_dim * 2 * eb
     return kv + q + o + table + append
+
+
+# ---------------------------------------------------------------------------
+# Prefill (causal attention of packed prompts over the paged cache)
+
+@dataclass(frozen=True)
+class PrefillConfig:
+    name: str
+    batch: int
+    rows: int           # prompt rows per sequence
+    hq: int
+    hkv: int
+    head_dim: int
+    dtype: str
+    start_lo: int       # cached prefix length before the prompt, U{start_lo..start_hi}
+    start_hi: int
+    sigma: float
+    rope_theta: float = 1e6
+
+    @property
+    def torch_dtype(self):
+        return torch.float16 if self.dtype == "f16" else torch.bfloat16
+
+    @property
+    def row(self):
+        return (self.hq + 2 * self.hkv) * self.head_dim
+
+
+PREFILL_CONFIGS = {
+    # 4 prompts of 2048 tokens from an empty cache, Qwen2.5-0.5B heads, bf16
+    # (128 pages per sequence)
+    "prefill_4x2048": PrefillConfig("prefill_4x2048", 4, 2048, 14, 2, 64, "bf16", 0, 0, 0.5),
+}
+
+
+@dataclass
+class HostPrefill:
+    """Host copy of one prefill launch's inputs (bit patterns)."""
+    cfg: PrefillConfig
+    num_layers: int
+    cu_seqlens: np.ndarray  # [B+1] int32
+    start_pos: np.ndarray   # [B] int32
+    tables: np.ndarray      # [B, max_pages] int32
+    qkv: np.ndarray         # [T, row] uint16
+    k_pool: np.ndarray      # [pool+1, L, Hkv, 16, d] uint16
+    v_pool: np.ndarray
+
+    @property
+    def max_ctx(self) -> int:
+        return int((self.start_pos + np.diff(self.cu_seqlens)).max())
+
+
+def host_prefill_inputs(cfg: PrefillConfig, seed: int, num_layers: int = 1, rows=None,
+                        starts=None, poison: bool = True) -> HostPrefill:
+    """Seeded inputs for a prefill launch: prompts of `rows` (default cfg.rows
+    each) after cached prefixes of `starts` tokens (default U{start_lo..start_hi}).
+    Pages are a seeded shuffle of the pool dealt to the sequences in order.  The
+    prefix slots hold N(0,1)*sigma values (as written by earlier steps); with
+    `poison`, every other slot, the reserved last page and the unused table
+    entries are NaN, so a read outside a row's causal range shows up."""
+    rng = np.random.default_rng(seed)
+    rows = np.full(cfg.batch, cfg.rows, np.int64) if rows is None else np.asarray(rows, np.int64)
+    if starts is None:
+        starts = rng.integers(cfg.start_lo, cfg.start_hi + 1, cfg.batch)
+    starts = np.asarray(starts, np.int64)
+    ctx = starts + rows
+    need = (ctx + PAGE - 1) // PAGE
+    pool_pages = int(need.sum())
+    max_pages = int(need.max()) + 1
+    perm = rng.permutation(pool_pages).astype(np.int32)
+    tables = np.full((cfg.batch, max_pages), pool_pages, np.int32)
+    off = 0
+    for b in range(cfg.batch):
+        tables[b, : need[b]] = perm[off: off + need[b]]
+        off += need[b]
+    shape = (pool_pages + 1, num_layers, cfg.hkv, PAGE, cfg.head_dim)
+    k = normal(rng, shape, cfg.sigma)
+    v = normal(rng, shape, cfg.sigma)
+    if poison:
+        valid = np.zeros((pool_pages + 1, PAGE), bool)
+        for b in range(cfg.batch):
+            for p in range(int(starts[b])):
+                valid[tables[b, p // PAGE], p % PAGE] = True
+        keep = valid[:, None, None, :, None]
+        k = np.where(keep, k, np.float32(np.nan))
+        v = np.where(keep, v, np.float32(np.nan))
+    cu = np.concatenate([[0], np.cumsum(rows)]).astype(np.int32)
+    qkv = normal(rng, (int(cu[-1]), cfg.row), cfg.sigma)
+    return HostPrefill(cfg, num_layers, cu, starts.astype(np.int32), tables,
+                       to_bits(qkv, cfg.dtype), to_bits(k, cfg.dtype), to_bits(v, cfg.dtype))
+
+
+def prefill_flops(cfg: PrefillConfig, rows: np.ndarray, starts: np.ndarray) -> int:
+    """Algorithmic FLOPs of the attention: every prompt row i (position
+    start + i) against start + i + 1 keys, QK^T and PV, 2 flops per MAC."""
+    n = rows.astype(np.int64)
+    s = starts.astype(np.int64)
+    keys = (n * s + n * (n + 1) // 2).sum()  # sum over rows of (start + i + 1)
+    return int(2 * 2 * cfg.head_dim * cfg.hq * keys)

@@ -159,3 +159,32 @@ def test_decode_step_argument_checks(cdll):
     assert need > 0
     assert call(ws=ctypes.c_void_p(4096 + 8), ws_bytes=need) == -1   # alignment
     assert call(ws=ctypes.c_void_p(4096), ws_bytes=need - 4) == -5   # too small
+
+
+def test_prefill_argument_checks(cdll):
+    """luc_paged_prefill rejects bad arguments on the host (no GPU call): the
+    alignment its vector loads need, row strides, head sizes, missing arrays
+    and a table too short for max_ctx; an empty batch is a no-op."""
+    def call(**kw):
+        args = dict(ctx=ctypes.c_void_p(1), stream=None, dtype=0, qkv=ctypes.c_void_p(256),
+                    qkv_stride=18 * 64, qb=None, kb=None, vb=None, cos=ctypes.c_void_p(16),
+                    sin=ctypes.c_void_p(16), k_pool=ctypes.c_void_p(256),
+                    v_pool=ctypes.c_void_p(512), tables=ctypes.c_void_p(16), table_stride=129,
+                    cu=ctypes.c_void_p(16), start=ctypes.c_void_p(16), batch=4, total=8192,
+                    max_ctx=2048, layer=0, num_layers=24, hq=14, hkv=2, head_dim=64,
+                    block_size=16, scale=0.125, out=ctypes.c_void_p(256), out_stride=14 * 64)
+        args.update(kw)
+        return cdll.luc_paged_prefill(*args.values())
+    assert call(qkv_stride=14 * 64) == -1                 # a qkv row holds q, k and v
+    assert call(qkv=ctypes.c_void_p(264)) == -1           # q rows are read as 16-byte vectors
+    assert call(qkv_stride=18 * 64 + 4) == -1
+    assert call(out=ctypes.c_void_p(260)) == -1           # outputs written as 8-byte vectors
+    assert call(out_stride=14 * 64 + 2) == -1
+    assert call(cu=None) == -1 and call(start=None) == -1 and call(cos=None) == -1
+    assert call(table_stride=127) == -1                   # 127 pages < 2048 tokens
+    assert call(head_dim=80) == -2
+    assert call(hq=18) == -2                              # group 9 > 8
+    assert call(hq=15) == -1                              # not a multiple of hkv
+    assert call(block_size=32) == -2
+    assert call(max_ctx=0) == -1
+    assert call(batch=0) == 0 and call(total=0) == 0
