@@ -11,22 +11,24 @@
 // flash_decoding call for that token computes (src/kernels/attention.cu:4-176),
 // since by then the cache holds those positions and nothing later.
 //
-// Work decomposition: workgroup = (sequence b, kv head h, tile of 32 prompt
-// rows), G = Hq/Hkv waves, wave w = q-head h*G + w over the same 32 rows, so
-// the K and V tiles staged in LDS serve all G heads (GQA).  The workgroup
-// walks the tokens 0..(last position of its rows) in blocks of 64:
-//   - K block [64 tokens][D] straight into LDS (global_load_lds_dwordx4, one
-//     wave-wide load = 1 KB of a page), each token row XOR-swizzled by 16-byte
-//     chunk; V block into LDS transposed, V^T[dim][token], rows padded so the
-//     MFMA operand reads do not collide; tokens past the context are written
-//     as zeros so that 0-weight tokens contribute exactly zero.
+// Work decomposition: workgroup = (sequence b, kv head h, group of up to 4 of
+// its G = Hq/Hkv q-heads, tile of 32 prompt rows), one wave per q-head over the
+// same 32 rows, so the K and V tiles staged in LDS serve 4 heads (GQA).  The
+// workgroup walks the tokens 0..(last position of its rows) in blocks of 64,
+// in a two-stage LDS ring: block i+1 loads while block i is computed.
+//   - K and V blocks [64 tokens][D] straight into LDS (global_load_lds_dwordx4,
+//     one wave-wide load = 1 KB of a page), each token row XOR-swizzled by
+//     16-byte chunk so the operand reads below do not collide.  Tokens past
+//     the context re-read the last valid token (finite), so their zero
+//     weights contribute exactly zero.
 //   - per wave, per 32-token half: S^T = K Q^T with v_mfma_f32_32x32x16 (A = K
 //     from LDS, B = Q^T held in registers for the whole kernel).  In the MFMA
 //     accumulator layout lane l holds q row l % 32 and 16 of the tile's
 //     tokens; the other 16 are in lane l ^ 32.  So the causal mask, the row
 //     max and the running sum are per lane plus one permlane32 exchange.
 //   - online softmax in the exp2 domain, then O^T += V^T P^T
-//     (v_mfma_f32_32x32x16, A = V^T from LDS, B = P^T): P^T in the layout the
+//     (v_mfma_f32_32x32x16, A = V^T read from the row-major V block with the
+//     transposing ds_read_b64_tr_b16, B = P^T): P^T in the layout the
 //     MFMA wants is exactly what the lane already holds, packed to 16 bits,
 //     once the 16-token k-slots are ordered as the accumulator orders tokens
 //     (slot e of lane group g = token 4g + e, then 8 + 4g + e - 4).
@@ -36,6 +38,12 @@
 namespace luc {
 
 typedef __attribute__((address_space(3))) void lds_void_p;
+typedef __attribute__((address_space(3))) char lds_char_p;
+
+// 32-bit LDS address of a pointer into a __shared__ array.
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_char_p*)p;
+}
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -73,57 +81,111 @@ __device__ inline uint32_t pack2(float lo, float hi, int dt) {
   return (uint32_t)St<kBF16>::store(lo) | ((uint32_t)St<kBF16>::store(hi) << 16);
 }
 
+// LDS reads in asm (the compiler would otherwise wait for every outstanding
+// global_load_lds before them, including the next block's), each block with
+// its own wait, so the results cannot be used before they arrive.
+// Four 16-byte reads:
+__device__ inline void lds_b128x4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3,
+                                  uint4* x) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %5\n\t"
+      "ds_read_b128 %2, %6\n\t"
+      "ds_read_b128 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3])
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "memory");
+}
+// Two ds_read_b64_tr_b16: within each 16-lane group, output lane 4a + c
+// receives element c of the 8-byte chunks read by input lanes 4e + a,
+// e = 0..3.
+__device__ inline void lds_tr16x2(uint32_t a0, uint32_t a1, uint2* x) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %2\n\t"
+      "ds_read_b64_tr_b16 %1, %3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x[0]), "=&v"(x[1])
+      : "v"(a0), "v"(a1)
+      : "memory");
+}
+
 template <int DT, int D, int G>
 __device__ void prefill_impl(const PrefillArgs& A) {
+  constexpr int W = 4;            // waves per workgroup: up to 4 heads of the group
+  constexpr int NHG = (G + W - 1) / W;
   constexpr int BT = 64;          // tokens per block
   constexpr int CH = D / 8;       // 16-byte chunks per token row
-  constexpr int KB = BT * D * 2;  // bytes of a K block
-  constexpr int VROW = BT + 4;    // V^T row length in elements (padded)
+  constexpr int ROWB = 2 * D;     // bytes per token row
+  constexpr int KB = BT * ROWB;   // bytes of a K (or V) block
+  constexpr int LOADS = KB / 1024;       // 1 KB wave-wide loads per K (or V) block
+  constexpr int TPL = 1024 / ROWB;       // tokens per 1 KB load
   constexpr int ND = D / 32;      // 32-dim output tiles
   constexpr int NK = D / 16;      // 16-dim k-steps of QK
-  constexpr int NT = 64 * G;
-  __shared__ __attribute__((aligned(16))) char s_kb[KB];
-  __shared__ __attribute__((aligned(16))) uint16_t s_vt[D * VROW];
+  // two stages of K and V blocks, row-major, 16-byte chunk c of token t at
+  // slot c ^ (t & 7)
+  __shared__ __attribute__((aligned(16))) char s_kv[2][2][KB];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // tiles in reverse order of rows: the longest causal ranges start first
   const int tiles = A.row_tiles;
-  const int per_seq = A.hkv * tiles;
+  const int per_seq = A.hkv * NHG * tiles;
   const int b = blockIdx.x / per_seq;
-  const int rem = blockIdx.x - b * per_seq;
-  const int h = rem / tiles;
-  const int rt = tiles - 1 - (rem - h * tiles);
+  int rem = blockIdx.x - b * per_seq;
+  const int h = rem / (NHG * tiles);
+  rem -= h * NHG * tiles;
+  const int hg = rem / tiles;
+  const int rt = tiles - 1 - (rem - hg * tiles);
   const int row0 = A.cu_seqlens[b];
   const int nrows = A.cu_seqlens[b + 1] - row0;
   if (rt * 32 >= nrows) return;
   const int sp = A.start_pos[b];
-  const int qh = h * G + w;
+  const bool active = hg * W + w < G;  // wave-uniform: a q-head of the group
+  const int qh = h * G + min(hg * W + w, G - 1);
   const int my_i = rt * 32 + (lane & 31);  // the lane's prompt row (q row of the tile)
-  const bool row_ok = my_i < nrows;
+  const bool row_ok = active && my_i < nrows;
   const int my_pos = sp + my_i;
   uint16_t* const orow = A.out + (int64_t)(row0 + min(my_i, nrows - 1)) * A.out_stride + (int64_t)qh * D;
   const int last = sp + min(rt * 32 + 32, nrows) - 1;  // last position of the tile's rows
+  const int g = lane >> 5;
   if (sp < 0 || sp + nrows > A.max_ctx) {
     // positions outside the host bound: flagged with NaN, never truncated
-    if (row_ok) {
-      const int g = lane >> 5;
+    if (row_ok)
       for (int d = 0; d < D; d += 8)
         for (int j = 0; j < 4; ++j) orow[d + 4 * g + j] = St<DT>::store(__builtin_nanf(""));
-    }
     return;
   }
   const int nkv = last + 1;  // tokens the tile reads
   const int* trow = A.tables + (int64_t)b * A.table_stride;
   const int64_t page_stride = (int64_t)A.num_layers * A.hkv * kPage * D;
   const int64_t head_off = ((int64_t)A.layer * A.hkv + h) * kPage * D;
+  const int nblk = (nkv + BT - 1) / BT;
+
+  // Issue the K and V loads of block blk into stage st: 2*LOADS wave-wide
+  // loads shared round-robin by the waves.  Tokens past the context re-read
+  // token nkv - 1 (finite), so their zero weights contribute exactly zero.
+  auto issue = [&](int blk, int st) __attribute__((always_inline)) {
+    for (int j = w; j < 2 * LOADS; j += W) {
+      const int kv = j / LOADS, jj = j % LOADS;
+      const int tl = jj * TPL + lane / CH;  // token within the block
+      const int c = lane % CH;
+      const int t = min(blk * BT + tl, nkv - 1);
+      const int page = trow[t / kPage];
+      const uint16_t* pool = kv ? A.v_pool : A.k_pool;
+      const char* src = (const char*)(pool + (int64_t)page * page_stride + head_off +
+                                      (int64_t)(t % kPage) * D) + ((c ^ (tl & 7)) << 4);
+      __builtin_amdgcn_global_load_lds(src, (lds_void_p*)(s_kv[st][kv] + jj * 1024), 16, 0, 0);
+    }
+  };
+  issue(0, 0);
 
   // Q^T fragments (B operand): lane l holds q row my_i, dims (l/32)*8 + 16k .. +8
   uint4 qf[NK];
   {
     const uint16_t* qrow = A.qkv + (int64_t)(row0 + min(my_i, nrows - 1)) * A.qkv_stride + (int64_t)qh * D;
 #pragma unroll
-    for (int k = 0; k < NK; ++k) qf[k] = *(const uint4*)(qrow + (lane >> 5) * 8 + 16 * k);
+    for (int k = 0; k < NK; ++k) qf[k] = *(const uint4*)(qrow + g * 8 + 16 * k);
   }
 
   f32x16 o[ND];
@@ -132,60 +194,39 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[i][e] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
-  const int g = lane >> 5;
+  // V^T operand reads (ds_read_b64_tr_b16): input lane j = lane % 16 of
+  // 16-lane group k16 = lane / 16 reads token tb + j / 4, dims
+  // 16 * (k16 % 2) + 4 * (j % 4) .. + 3; the group's output lane i then holds
+  // dim 16 * (k16 % 2) + i of tokens tb .. tb + 3.
+  const int tr_e = (lane & 15) >> 2;
+  const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  const int nblk = (nkv + BT - 1) / BT;
   for (int blk = 0; blk < nblk; ++blk) {
-    const int t0 = blk * BT;
-    const int last_page = (nkv - 1) / kPage;
-    // ---- stage K (direct to LDS) and V^T ----
-    // K: BT*D*2 bytes = KB/1024 wave-wide loads of 1 KB; load j covers tokens
-    // j*(1024/(2D)) .. and is issued by wave j % G.  LDS chunk position
-    // (token t, slot c) holds chunk c ^ (t & 7) of the token row.
-    constexpr int KLOADS = KB / 1024;
-    constexpr int TPL = 1024 / (2 * D);  // tokens per 1 KB load
-    for (int j = w; j < KLOADS; j += G) {
-      const int tl = j * TPL + lane / CH;  // token within the block
-      const int c = lane % CH;
-      const int t = min(t0 + tl, nkv - 1);  // past the context: re-read a valid token
-      const int page = trow[min(t / kPage, last_page)];
-      const char* src = (const char*)(A.k_pool + (int64_t)page * page_stride + head_off +
-                                      (int64_t)(t % kPage) * D) + ((c ^ (tl & 7)) << 4);
-      __builtin_amdgcn_global_load_lds(src, (lds_void_p*)(s_kb + j * 1024), 16, 0, 0);
-    }
-    // V: 16-byte chunks (token, 8 dims) -> V^T[dim][token], zero past nkv
-    for (int idx = threadIdx.x; idx < BT * CH; idx += NT) {
-      const int tl = idx / CH, c = idx % CH;
-      const int t = t0 + tl;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (t < nkv) {
-        const int page = trow[t / kPage];
-        v = *(const uint4*)(A.v_pool + (int64_t)page * page_stride + head_off +
-                            (int64_t)(t % kPage) * D + c * 8);
-      }
-      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s_vt[(c * 8 + 2 * e) * VROW + tl] = (uint16_t)(vw[e] & 0xffff);
-        s_vt[(c * 8 + 2 * e + 1) * VROW + tl] = (uint16_t)(vw[e] >> 16);
-      }
-    }
+    const int st = blk & 1;
+    // this block's loads (this wave's share) have landed; after the barrier
+    // every wave's have, and every wave is done with the other stage
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    __builtin_amdgcn_s_barrier();
+    if (blk + 1 < nblk) issue(blk + 1, st ^ 1);
+    if (!active) continue;
+    const int t0 = blk * BT;
+    const uint32_t kbase = lds_addr(s_kv[st][0]);
+    const uint32_t vbase = lds_addr(s_kv[st][1]);
 
     // ---- S^T = K Q^T for the two 32-token halves ----
     f32x16 s[2];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
+      const int tl = hf * 32 + (lane & 31);  // A row: token
+      // chunk of dims (l/32)*8 + 16k: 2k + g, at slot (2k + g) ^ (tl & 7)
+      auto ka_addr = [&](int k) { return kbase + tl * ROWB + (((2 * k + g) ^ (tl & 7)) << 4); };
+      uint4 ka[NK];
+#pragma unroll
+      for (int k = 0; k < NK; k += 4) lds_b128x4(ka_addr(k), ka_addr(k + 1), ka_addr(k + 2), ka_addr(k + 3), ka + k);
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[hf][e] = 0.0f;
-      const int tl = hf * 32 + (lane & 31);  // A row: token
 #pragma unroll
-      for (int k = 0; k < NK; ++k) {
-        const int c = 2 * k + g;  // chunk of dims (l/32)*8 + 16k
-        const uint4 ka = *(const uint4*)(s_kb + tl * D * 2 + ((c ^ (tl & 7)) << 4));
-        s[hf] = mfma32<DT>(ka, qf[k], s[hf]);
-      }
+      for (int k = 0; k < NK; ++k) s[hf] = mfma32<DT>(ka[k], qf[k], s[hf]);
     }
     // ---- mask, online softmax (exp2 domain) ----
     // s[hf][4i + j]: token t0 + 32hf + 8i + 4g + j, q row my_i
@@ -234,18 +275,24 @@ __device__ void prefill_impl(const PrefillArgs& A) {
                                     pack2(s[hf][4 * i1], s[hf][4 * i1 + 1], DT),
                                     pack2(s[hf][4 * i1 + 2], s[hf][4 * i1 + 3], DT));
         const int tb = 32 * hf + 16 * mm + 4 * g;  // first token of the lane's slots
+        uint2 va[ND][2];
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
-          const uint16_t* vr = s_vt + (db * 32 + (lane & 31)) * VROW + tb;
-          const uint2 lo = *(const uint2*)vr;        // tokens tb .. tb+3
-          const uint2 hi = *(const uint2*)(vr + 8);  // tokens tb+8 .. tb+11
-          o[db] = mfma32<DT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[db]);
+          auto va_addr = [&](int half) {
+            const int t = tb + 8 * half + tr_e;  // the token this lane reads
+            const int dim = 32 * db + tr_d;
+            return vbase + t * ROWB + (((dim / 8) ^ (t & 7)) << 4) + (dim % 8) * 2;
+          };
+          lds_tr16x2(va_addr(0), va_addr(1), va[db]);
         }
+#pragma unroll
+        for (int db = 0; db < ND; ++db)
+          o[db] = mfma32<DT>(make_uint4(va[db][0].x, va[db][0].y, va[db][1].x, va[db][1].y), pb, o[db]);
       }
-    __syncthreads();  // the next block overwrites the LDS tiles
   }
 
   // ---- normalise and store: lane holds dims 32db + 8i + 4g + j of row my_i ----
+  if (!active) return;
   {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
     l_run = __uint_as_float(r[0]) + __uint_as_float(r[1]);
@@ -266,7 +313,7 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 }  // namespace luc
 
 #define LUC_PREFILL(DTN, DT, D, G)                                                              \
-  extern "C" __global__ __launch_bounds__(64 * G) void luc_prefill_##DTN##_d##D##_g##G(          \
+  extern "C" __global__ __launch_bounds__(256) void luc_prefill_##DTN##_d##D##_g##G(             \
       luc::PrefillArgs a) {                                                                     \
     luc::prefill_impl<DT, D, G>(a);                                                             \
   }

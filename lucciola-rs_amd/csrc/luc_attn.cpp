@@ -573,8 +573,9 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
                                std::to_string(head_dim) + "_g" + std::to_string(group),
                       &fn))
     return rc;
+  // workgroups: (sequence, kv head, group of up to 4 q-heads, 32 rows), 4 waves
   const int row_tiles = (int)ceil_div(total_rows, 32);
-  const int64_t grid = (int64_t)batch * num_kv_heads * row_tiles;
+  const int64_t grid = (int64_t)batch * num_kv_heads * ceil_div(group, 4) * row_tiles;
   if (grid > INT32_MAX) return fail(LUC_E_INVALID, "batch x kv heads x row tiles too large");
 
   // 1) bias + RoPE of every prompt row's q and k in place, cache write of the
@@ -598,7 +599,7 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
   p.layer = layer; p.num_layers = num_layers; p.hkv = num_kv_heads; p.max_ctx = max_ctx;
   p.row_tiles = row_tiles; p.qk_scale_log2 = sm_scale * 1.4426950408889634f;
   void* args[] = {&p};
-  return launch(fn, dim3((unsigned)grid), dim3(64 * group), stream, args);
+  return launch(fn, dim3((unsigned)grid), dim3(256), stream, args);
 }
 
 }  // extern "C"
