@@ -73,12 +73,17 @@ __device__ inline f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// Two values rounded (nearest even) to 16-bit storage, packed: one
+// v_cvt_pk_{f16,bf16}_f32 (these values are compared within tolerance; the
+// bit-exact RoPE path keeps its own rounding).
 __device__ inline uint32_t pack2(float lo, float hi, int dt) {
   if (dt == kF16) {
     const half2_t v = {(_Float16)lo, (_Float16)hi};
     return __builtin_bit_cast(uint32_t, v);
   }
-  return (uint32_t)St<kBF16>::store(lo) | ((uint32_t)St<kBF16>::store(hi) << 16);
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // LDS reads in asm (the compiler would otherwise wait for every outstanding
@@ -231,17 +236,27 @@ __device__ void prefill_impl(const PrefillArgs& A) {
     // ---- mask, online softmax (exp2 domain) ----
     // s[hf][4i + j]: token t0 + 32hf + 8i + 4g + j, q row my_i
     float mb = -INFINITY;
+    if (t0 + BT - 1 <= sp + rt * 32) {  // wave-uniform: below the diagonal, no mask
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
+      for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int t = t0 + 32 * hf + 8 * i + 4 * g + j;
-          const float x = t <= my_pos ? s[hf][4 * i + j] * A.qk_scale_log2 : -INFINITY;
-          s[hf][4 * i + j] = x;
-          mb = fmaxf(mb, x);
+        for (int e = 0; e < 16; ++e) {
+          s[hf][e] *= A.qk_scale_log2;
+          mb = fmaxf(mb, s[hf][e]);
         }
+    } else {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int t = t0 + 32 * hf + 8 * i + 4 * g + j;
+            const float x = t <= my_pos ? s[hf][4 * i + j] * A.qk_scale_log2 : -INFINITY;
+            s[hf][4 * i + j] = x;
+            mb = fmaxf(mb, x);
+          }
+    }
     {
       const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
       mb = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -258,10 +273,12 @@ __device__ void prefill_impl(const PrefillArgs& A) {
         ps += s[hf][e];
       }
     l_run = l_run * alpha + ps;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {  // wave-uniform: some row's max moved
 #pragma unroll
-    for (int i = 0; i < ND; ++i)
+      for (int i = 0; i < ND; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+        for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+    }
 
     // ---- O^T += V^T P^T, 16 tokens per MFMA ----
 #pragma unroll
