@@ -15,7 +15,7 @@
 // its G = Hq/Hkv q-heads, tile of 32 prompt rows), one wave per q-head over the
 // same 32 rows, so the K and V tiles staged in LDS serve 4 heads (GQA).  The
 // workgroup walks the tokens 0..(last position of its rows) in blocks of 64,
-// in a two-stage LDS ring: block i+1 loads while block i is computed.
+// in a three-stage LDS ring: blocks i+1 and i+2 load while block i is computed.
 //   - K and V blocks [64 tokens][D] straight into LDS (global_load_lds_dwordx4,
 //     one wave-wide load = 1 KB of a page), each token row XOR-swizzled by
 //     16-byte chunk so the operand reads below do not collide.  Tokens past
@@ -39,6 +39,7 @@ namespace luc {
 
 typedef __attribute__((address_space(3))) void lds_void_p;
 typedef __attribute__((address_space(3))) char lds_char_p;
+typedef __attribute__((address_space(4))) const int const_i32_p;  // scalar loads
 
 // 32-bit LDS address of a pointer into a __shared__ array.
 __device__ inline uint32_t lds_addr(const void* p) {
@@ -127,9 +128,12 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   constexpr int TPL = 1024 / ROWB;       // tokens per 1 KB load
   constexpr int ND = D / 32;      // 32-dim output tiles
   constexpr int NK = D / 16;      // 16-dim k-steps of QK
-  // two stages of K and V blocks, row-major, 16-byte chunk c of token t at
+  // NS stages of K and V blocks, row-major, 16-byte chunk c of token t at
   // slot c ^ (t & 7)
-  __shared__ __attribute__((aligned(16))) char s_kv[2][2][KB];
+  constexpr int NS = 3;
+  constexpr int LPW = 2 * LOADS / W;  // loads per wave per block
+  static_assert(2 * LOADS % W == 0, "every wave issues the same number of loads");
+  __shared__ __attribute__((aligned(16))) char s_kv[NS][2][KB];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -173,25 +177,33 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   auto issue = [&](int blk, int st) __attribute__((always_inline)) {
     for (int j = w; j < 2 * LOADS; j += W) {
       const int kv = j / LOADS, jj = j % LOADS;
+      // the load's TPL tokens lie in one page (TPL divides the page); its page
+      // number is wave-uniform and comes through the scalar cache, so no
+      // vector-memory wait precedes the load
+      const int tb = blk * BT + jj * TPL;
+      const int page = ((const const_i32_p*)trow)[min(tb, nkv - 1) / kPage];
       const int tl = jj * TPL + lane / CH;  // token within the block
       const int c = lane % CH;
-      const int t = min(blk * BT + tl, nkv - 1);
-      const int page = trow[t / kPage];
+      const int t = min(tb + lane / CH, nkv - 1);
       const uint16_t* pool = kv ? A.v_pool : A.k_pool;
       const char* src = (const char*)(pool + (int64_t)page * page_stride + head_off +
                                       (int64_t)(t % kPage) * D) + ((c ^ (tl & 7)) << 4);
       __builtin_amdgcn_global_load_lds(src, (lds_void_p*)(s_kv[st][kv] + jj * 1024), 16, 0, 0);
     }
   };
-  issue(0, 0);
-
   // Q^T fragments (B operand): lane l holds q row my_i, dims (l/32)*8 + 16k .. +8
+  // (loaded before the first blocks, so the block waits below can count
+  // only block loads)
   uint4 qf[NK];
   {
     const uint16_t* qrow = A.qkv + (int64_t)(row0 + min(my_i, nrows - 1)) * A.qkv_stride + (int64_t)qh * D;
 #pragma unroll
     for (int k = 0; k < NK; ++k) qf[k] = *(const uint4*)(qrow + g * 8 + 16 * k);
+#pragma unroll
+    for (int k = 0; k < NK; ++k) asm volatile("" ::"v"(qf[k].x), "v"(qf[k].y), "v"(qf[k].z), "v"(qf[k].w));
   }
+  issue(0, 0);
+  if (nblk > 1) issue(1, 1);
 
   f32x16 o[ND];
 #pragma unroll
@@ -207,12 +219,17 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   for (int blk = 0; blk < nblk; ++blk) {
-    const int st = blk & 1;
-    // this block's loads (this wave's share) have landed; after the barrier
-    // every wave's have, and every wave is done with the other stage
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const int st = blk % NS;
+    // this block's loads (this wave's share) have landed -- the next block's
+    // LPW loads may still be in flight, they complete in order -- and after
+    // the barrier every wave's have, and every wave is done with the stage
+    // that block blk + 2 loads into (it held block blk - 1)
+    if (blk + 1 < nblk)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    if (blk + 1 < nblk) issue(blk + 1, st ^ 1);
+    if (blk + 2 < nblk) issue(blk + 2, (blk + 2) % NS);
     if (!active) continue;
     const int t0 = blk * BT;
     const uint32_t kbase = lds_addr(s_kv[st][0]);
