@@ -32,6 +32,9 @@ HIPCC_FLAGS = [
     # no packed-FP32 instructions (v_pk_{add,mul,fma}_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+# per code object: the prefill kernel keeps its MFMA accumulators in ordinary
+# VGPRs (no accvgpr copies of the scores, three waves per SIMD)
+KERNEL_FLAGS = {"paged_prefill": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _run(cmd, verbose):
@@ -48,7 +51,8 @@ def build_kernel(name, verbose=False):
     src = os.path.join(KDIR, name + ".hip")
     out = os.path.join(LIB, name + ".hsaco")
     tmp = out + ".tmp"
-    _run([os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, "-I", KDIR, src, "-o", tmp], verbose)
+    _run([os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, *KERNEL_FLAGS.get(name, []), "-I", KDIR, src,
+          "-o", tmp], verbose)
     os.replace(tmp, out)
     return out
 

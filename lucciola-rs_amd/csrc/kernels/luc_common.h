@@ -157,4 +157,8 @@ __device__ inline void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Online softmax: p = exp2(s - m) is kept <= 2^kLazyMax (exact in f16 range)
+// by moving the reference point m only when a score passes m + kLazyMax.
+constexpr float kLazyMax = 8.0f;
+
 }  // namespace luc

@@ -74,9 +74,6 @@ struct DecodeGeo {
 };
 
 constexpr int kCpolNT = 2;  // non-temporal load: the KV stream is read once per step
-// Online softmax: p = exp2(s - m) is kept <= 2^kLazyMax (exact in f16 range)
-// by moving the reference point m only when a score passes m + kLazyMax.
-constexpr float kLazyMax = 8.0f;
 
 // Wait until at most N vector memory operations of this wave are in flight.
 // They complete in issue order, so this also covers the LDS writes of

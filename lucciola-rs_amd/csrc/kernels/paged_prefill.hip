@@ -12,10 +12,14 @@
 // since by then the cache holds those positions and nothing later.
 //
 // Work decomposition: workgroup = (sequence b, kv head h, group of up to 4 of
-// its G = Hq/Hkv q-heads, tile of 32 prompt rows), one wave per q-head over the
-// same 32 rows, so the K and V tiles staged in LDS serve 4 heads (GQA).  The
-// workgroup walks the tokens 0..(last position of its rows) in blocks of 64,
-// in a three-stage LDS ring: blocks i+1 and i+2 load while block i is computed.
+// its G = Hq/Hkv q-heads, pair p of tiles of 32 prompt rows), one wave per
+// q-head over the same 32 rows, so the K and V tiles staged in LDS serve 4
+// heads (GQA).  Of a sequence's nt row tiles the workgroup takes tile nt-1-p
+// and then tile p: causal tile t reads about t+1 token blocks, so every pair
+// carries the same work, the grid is one wave of equal workgroups and none
+// waits on a long tail.  For each tile the workgroup walks the tokens
+// 0..(last position of its rows) in blocks of 64, in a three-stage LDS ring:
+// blocks i+1 and i+2 load while block i is computed.
 //   - K and V blocks [64 tokens][D] straight into LDS (global_load_lds_dwordx4,
 //     one wave-wide load = 1 KB of a page), each token row XOR-swizzled by
 //     16-byte chunk so the operand reads below do not collide.  Tokens past
@@ -40,6 +44,10 @@ namespace luc {
 typedef __attribute__((address_space(3))) void lds_void_p;
 typedef __attribute__((address_space(3))) char lds_char_p;
 typedef __attribute__((address_space(4))) const int const_i32_p;  // scalar loads
+template <int N>
+struct IC {  // a compile-time index passed to a generic lambda
+  static constexpr int value = N;
+};
 
 // 32-bit LDS address of a pointer into a __shared__ array.
 __device__ inline uint32_t lds_addr(const void* p) {
@@ -60,7 +68,7 @@ struct PrefillArgs {
   const int32_t* start_pos;   // [batch]
   uint16_t* out;              // row r at out + r*out_stride, [Hq*D]
   int64_t out_stride;
-  int32_t batch, layer, num_layers, hkv, max_ctx, row_tiles;
+  int32_t batch, layer, num_layers, hkv, max_ctx, pairs;  // pairs: tile pairs per sequence
   float qk_scale_log2;  // sm_scale * log2(e)
 };
 
@@ -91,28 +99,30 @@ __device__ inline uint32_t pack2(float lo, float hi, int dt) {
 // global_load_lds before them, including the next block's), each block with
 // its own wait, so the results cannot be used before they arrive.
 // Four 16-byte reads:
+template <int OFF>
 __device__ inline void lds_b128x4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3,
                                   uint4* x) {
   asm volatile(
-      "ds_read_b128 %0, %4\n\t"
-      "ds_read_b128 %1, %5\n\t"
-      "ds_read_b128 %2, %6\n\t"
-      "ds_read_b128 %3, %7\n\t"
+      "ds_read_b128 %0, %4 offset:%8\n\t"
+      "ds_read_b128 %1, %5 offset:%8\n\t"
+      "ds_read_b128 %2, %6 offset:%8\n\t"
+      "ds_read_b128 %3, %7 offset:%8\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3])
-      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "n"(OFF)
       : "memory");
 }
 // Two ds_read_b64_tr_b16: within each 16-lane group, output lane 4a + c
 // receives element c of the 8-byte chunks read by input lanes 4e + a,
 // e = 0..3.
-__device__ inline void lds_tr16x2(uint32_t a0, uint32_t a1, uint2* x) {
+template <int OFF0, int OFF1>
+__device__ inline void lds_tr16x2(uint32_t a, uint2* x) {
   asm volatile(
-      "ds_read_b64_tr_b16 %0, %2\n\t"
-      "ds_read_b64_tr_b16 %1, %3\n\t"
+      "ds_read_b64_tr_b16 %0, %2 offset:%3\n\t"
+      "ds_read_b64_tr_b16 %1, %2 offset:%4\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(x[0]), "=&v"(x[1])
-      : "v"(a0), "v"(a1)
+      : "v"(a), "n"(OFF0), "n"(OFF1)
       : "memory");
 }
 
@@ -132,51 +142,83 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   // slot c ^ (t & 7)
   constexpr int NS = 3;
   constexpr int LPW = 2 * LOADS / W;  // loads per wave per block
-  static_assert(2 * LOADS % W == 0, "every wave issues the same number of loads");
+  static_assert(LOADS % W == 0, "every wave issues the same number of K (and V) loads");
   __shared__ __attribute__((aligned(16))) char s_kv[NS][2][KB];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // tiles in reverse order of rows: the longest causal ranges start first
-  const int tiles = A.row_tiles;
-  const int per_seq = A.hkv * NHG * tiles;
-  const int b = blockIdx.x / per_seq;
-  int rem = blockIdx.x - b * per_seq;
-  const int h = rem / (NHG * tiles);
-  rem -= h * NHG * tiles;
-  const int hg = rem / tiles;
-  const int rt = tiles - 1 - (rem - hg * tiles);
+  // pair-major order: every group's first pair is dispatched before any
+  // second pair, and consecutive workgroups (which the hardware spreads over
+  // the XCDs) belong to different groups
+  const int groups = A.batch * A.hkv * NHG;
+  const int pair = blockIdx.x / groups;
+  int rem = blockIdx.x - pair * groups;
+  const int b = rem / (A.hkv * NHG);
+  rem -= b * A.hkv * NHG;
+  const int h = rem / NHG;
+  const int hg = rem - h * NHG;
   const int row0 = A.cu_seqlens[b];
   const int nrows = A.cu_seqlens[b + 1] - row0;
-  if (rt * 32 >= nrows) return;
   const int sp = A.start_pos[b];
   const bool active = hg * W + w < G;  // wave-uniform: a q-head of the group
   const int qh = h * G + min(hg * W + w, G - 1);
+  const int g = lane >> 5;
+  if (sp < 0 || sp + nrows > A.max_ctx) {
+    // positions outside the host bound: flagged with NaN, never truncated
+    // (such a sequence may have more tiles than the grid has pairs: the
+    // workgroups of its group stride over all its rows)
+    if (active)
+      for (int r = pair * 32 + (lane & 31); r < nrows; r += A.pairs * 32) {
+        uint16_t* const orow = A.out + (int64_t)(row0 + r) * A.out_stride + (int64_t)qh * D;
+        for (int d = 0; d < D; d += 8)
+          for (int j = 0; j < 4; ++j) orow[d + 4 * g + j] = St<DT>::store(__builtin_nanf(""));
+      }
+    return;
+  }
+  const int nt = (nrows + 31) / 32;  // row tiles of the sequence (nt <= 2 * pairs)
+  if (pair >= (nt + 1) / 2) return;
+  const int* trow = A.tables + (int64_t)b * A.table_stride;
+  const int64_t page_stride = (int64_t)A.num_layers * A.hkv * kPage * D;
+  const int64_t head_off = ((int64_t)A.layer * A.hkv + h) * kPage * D;
+  const int ntiles = pair < nt - 1 - pair ? 2 : 1;
+  // exponents are exp2(s * scale - max): with q negated for a negative scale
+  // the scale is positive, so the row max of s * scale is (max s) * scale
+  const bool neg_scale = A.qk_scale_log2 < 0.0f;
+  const float scale = fabsf(A.qk_scale_log2);
+  // lane-relative LDS offsets of the operand reads within a stage:
+  //   K (A operand of S^T): token lane % 32 (+32 for the second half, an
+  //   immediate offset), chunk of dims 16k + 8g at slot (2k + g) ^ (token & 7);
+  //   V^T (ds_read_b64_tr_b16): input lane j = lane % 16 of 16-lane group
+  //   k16 = lane / 16 reads token 4g + j / 4 (+ 8, 16, 32 by immediates),
+  //   dims 32 db + 16 (k16 % 2) + 4 (j % 4) .. + 3; the group's output lane i
+  //   then holds dim 32 db + 16 (k16 % 2) + i of four consecutive tokens.
+  uint32_t krel[NK], vrel[ND];
+#pragma unroll
+  for (int k = 0; k < NK; ++k) krel[k] = (lane & 31) * ROWB + (((2 * k + g) ^ (lane & 7)) << 4);
+  {
+    const int tr = 4 * g + ((lane & 15) >> 2);  // token (mod 8) the lane reads
+    const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+      vrel[db] = tr * ROWB + ((((32 * db + tr_d) / 8) ^ tr) << 4) + (tr_d % 8) * 2;
+  }
+  for (int k = 0; k < ntiles; ++k) {
+  const int rt = k == 0 ? nt - 1 - pair : pair;
   const int my_i = rt * 32 + (lane & 31);  // the lane's prompt row (q row of the tile)
   const bool row_ok = active && my_i < nrows;
   const int my_pos = sp + my_i;
   uint16_t* const orow = A.out + (int64_t)(row0 + min(my_i, nrows - 1)) * A.out_stride + (int64_t)qh * D;
   const int last = sp + min(rt * 32 + 32, nrows) - 1;  // last position of the tile's rows
-  const int g = lane >> 5;
-  if (sp < 0 || sp + nrows > A.max_ctx) {
-    // positions outside the host bound: flagged with NaN, never truncated
-    if (row_ok)
-      for (int d = 0; d < D; d += 8)
-        for (int j = 0; j < 4; ++j) orow[d + 4 * g + j] = St<DT>::store(__builtin_nanf(""));
-    return;
-  }
   const int nkv = last + 1;  // tokens the tile reads
-  const int* trow = A.tables + (int64_t)b * A.table_stride;
-  const int64_t page_stride = (int64_t)A.num_layers * A.hkv * kPage * D;
-  const int64_t head_off = ((int64_t)A.layer * A.hkv + h) * kPage * D;
   const int nblk = (nkv + BT - 1) / BT;
 
   // Issue the K and V loads of block blk into stage st: 2*LOADS wave-wide
   // loads shared round-robin by the waves.  Tokens past the context re-read
   // token nkv - 1 (finite), so their zero weights contribute exactly zero.
   auto issue = [&](int blk, int st) __attribute__((always_inline)) {
-    for (int j = w; j < 2 * LOADS; j += W) {
-      const int kv = j / LOADS, jj = j % LOADS;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int kv = i * W / LOADS, jj = i * W % LOADS + w;
       // the load's TPL tokens lie in one page (TPL divides the page); its page
       // number is wave-uniform and comes through the scalar cache, so no
       // vector-memory wait precedes the load
@@ -199,9 +241,18 @@ __device__ void prefill_impl(const PrefillArgs& A) {
     const uint16_t* qrow = A.qkv + (int64_t)(row0 + min(my_i, nrows - 1)) * A.qkv_stride + (int64_t)qh * D;
 #pragma unroll
     for (int k = 0; k < NK; ++k) qf[k] = *(const uint4*)(qrow + g * 8 + 16 * k);
+    if (neg_scale) {  // S = -(K Q^T) exactly: sign flips commute with rounding
+#pragma unroll
+      for (int k = 0; k < NK; ++k) {
+        qf[k].x ^= 0x80008000u; qf[k].y ^= 0x80008000u;
+        qf[k].z ^= 0x80008000u; qf[k].w ^= 0x80008000u;
+      }
+    }
 #pragma unroll
     for (int k = 0; k < NK; ++k) asm volatile("" ::"v"(qf[k].x), "v"(qf[k].y), "v"(qf[k].z), "v"(qf[k].w));
   }
+  // every wave is done with the previous tile's last stage before it is refilled
+  if (k) __builtin_amdgcn_s_barrier();
   issue(0, 0);
   if (nblk > 1) issue(1, 1);
 
@@ -211,12 +262,6 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[i][e] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
-  // V^T operand reads (ds_read_b64_tr_b16): input lane j = lane % 16 of
-  // 16-lane group k16 = lane / 16 reads token tb + j / 4, dims
-  // 16 * (k16 % 2) + 4 * (j % 4) .. + 3; the group's output lane i then holds
-  // dim 16 * (k16 % 2) + i of tokens tb .. tb + 3.
-  const int tr_e = (lane & 15) >> 2;
-  const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   for (int blk = 0; blk < nblk; ++blk) {
     const int st = blk % NS;
@@ -236,20 +281,23 @@ __device__ void prefill_impl(const PrefillArgs& A) {
     const uint32_t vbase = lds_addr(s_kv[st][1]);
 
     // ---- S^T = K Q^T for the two 32-token halves ----
-    f32x16 s[2];
+    uint32_t ka_addr[NK];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int tl = hf * 32 + (lane & 31);  // A row: token
-      // chunk of dims (l/32)*8 + 16k: 2k + g, at slot (2k + g) ^ (tl & 7)
-      auto ka_addr = [&](int k) { return kbase + tl * ROWB + (((2 * k + g) ^ (tl & 7)) << 4); };
+    for (int k = 0; k < NK; ++k) ka_addr[k] = kbase + krel[k];
+    f32x16 s[2];
+    auto qk_half = [&](auto hfc) __attribute__((always_inline)) {
+      constexpr int hf = decltype(hfc)::value;
       uint4 ka[NK];
 #pragma unroll
-      for (int k = 0; k < NK; k += 4) lds_b128x4(ka_addr(k), ka_addr(k + 1), ka_addr(k + 2), ka_addr(k + 3), ka + k);
+      for (int k = 0; k < NK; k += 4)
+        lds_b128x4<hf * 32 * ROWB>(ka_addr[k], ka_addr[k + 1], ka_addr[k + 2], ka_addr[k + 3], ka + k);
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[hf][e] = 0.0f;
 #pragma unroll
       for (int k = 0; k < NK; ++k) s[hf] = mfma32<DT>(ka[k], qf[k], s[hf]);
-    }
+    };
+    qk_half(IC<0>{});
+    qk_half(IC<1>{});
     // ---- mask, online softmax (exp2 domain) ----
     // s[hf][4i + j]: token t0 + 32hf + 8i + 4g + j, q row my_i
     float mb = -INFINITY;
@@ -257,10 +305,7 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          s[hf][e] *= A.qk_scale_log2;
-          mb = fmaxf(mb, s[hf][e]);
-        }
+        for (int e = 0; e < 16; ++e) mb = fmaxf(mb, s[hf][e]);
     } else {
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
@@ -269,7 +314,7 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int t = t0 + 32 * hf + 8 * i + 4 * g + j;
-            const float x = t <= my_pos ? s[hf][4 * i + j] * A.qk_scale_log2 : -INFINITY;
+            const float x = t <= my_pos ? s[hf][4 * i + j] : -INFINITY;
             s[hf][4 * i + j] = x;
             mb = fmaxf(mb, x);
           }
@@ -278,55 +323,56 @@ __device__ void prefill_impl(const PrefillArgs& A) {
       const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
       mb = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
     }
-    const float m_new = fmaxf(m_run, mb);  // finite: token 0 is in every row's range
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-    float ps = 0.0f;
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        s[hf][e] = __builtin_amdgcn_exp2f(s[hf][e] - m_new);
-        ps += s[hf][e];
-      }
-    l_run = l_run * alpha + ps;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {  // wave-uniform: some row's max moved
+    // lazy running max: it moves only when some row's block max passes it by
+    // more than kLazyMax (then every row takes its new max), so exponents
+    // stay below 2^kLazyMax and the rescale of o is rare
+    const float m_blk = mb * scale;  // finite: token 0 is in every row's range
+    if (__builtin_amdgcn_ballot_w64(m_blk > m_run + kLazyMax) != 0) {  // wave-uniform
+      const float m_new = fmaxf(m_run, m_blk);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
 #pragma unroll
       for (int i = 0; i < ND; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
     }
-
-    // ---- O^T += V^T P^T, 16 tokens per MFMA ----
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        // B = P^T: slots 0..3 = tokens 16mm + 4g + j, slots 4..7 = 16mm + 8 + 4g + j
-        const int i0 = 2 * mm, i1 = 2 * mm + 1;
-        const uint4 pb = make_uint4(pack2(s[hf][4 * i0], s[hf][4 * i0 + 1], DT),
-                                    pack2(s[hf][4 * i0 + 2], s[hf][4 * i0 + 3], DT),
-                                    pack2(s[hf][4 * i1], s[hf][4 * i1 + 1], DT),
-                                    pack2(s[hf][4 * i1 + 2], s[hf][4 * i1 + 3], DT));
-        const int tb = 32 * hf + 16 * mm + 4 * g;  // first token of the lane's slots
-        uint2 va[ND][2];
-#pragma unroll
-        for (int db = 0; db < ND; ++db) {
-          auto va_addr = [&](int half) {
-            const int t = tb + 8 * half + tr_e;  // the token this lane reads
-            const int dim = 32 * db + tr_d;
-            return vbase + t * ROWB + (((dim / 8) ^ (t & 7)) << 4) + (dim % 8) * 2;
-          };
-          lds_tr16x2(va_addr(0), va_addr(1), va[db]);
-        }
-#pragma unroll
-        for (int db = 0; db < ND; ++db)
-          o[db] = mfma32<DT>(make_uint4(va[db][0].x, va[db][0].y, va[db][1].x, va[db][1].y), pb, o[db]);
+      for (int e = 0; e < 16; ++e) {
+        s[hf][e] = __builtin_amdgcn_exp2f(fmaf(s[hf][e], scale, -m_run));
+        l_run += s[hf][e];
       }
+
+    // ---- O^T += V^T P^T, 16 tokens per MFMA ----
+    uint32_t va_addr[ND];
+#pragma unroll
+    for (int db = 0; db < ND; ++db) va_addr[db] = vbase + vrel[db];
+    auto pv_step = [&](auto hfc, auto mmc) __attribute__((always_inline)) {
+      constexpr int hf = decltype(hfc)::value, mm = decltype(mmc)::value;
+      // B = P^T: slots 0..3 = tokens 16mm + 4g + j, slots 4..7 = 16mm + 8 + 4g + j
+      constexpr int i0 = 2 * mm, i1 = 2 * mm + 1;
+      const uint4 pb = make_uint4(pack2(s[hf][4 * i0], s[hf][4 * i0 + 1], DT),
+                                  pack2(s[hf][4 * i0 + 2], s[hf][4 * i0 + 3], DT),
+                                  pack2(s[hf][4 * i1], s[hf][4 * i1 + 1], DT),
+                                  pack2(s[hf][4 * i1 + 2], s[hf][4 * i1 + 3], DT));
+      constexpr int off = (32 * hf + 16 * mm) * ROWB;  // first token of the lane's slots, less 4g
+      uint2 va[ND][2];
+#pragma unroll
+      for (int db = 0; db < ND; ++db) lds_tr16x2<off, off + 8 * ROWB>(va_addr[db], va[db]);
+#pragma unroll
+      for (int db = 0; db < ND; ++db)
+        o[db] = mfma32<DT>(make_uint4(va[db][0].x, va[db][0].y, va[db][1].x, va[db][1].y), pb, o[db]);
+    };
+    pv_step(IC<0>{}, IC<0>{});
+    pv_step(IC<0>{}, IC<1>{});
+    pv_step(IC<1>{}, IC<0>{});
+    pv_step(IC<1>{}, IC<1>{});
   }
 
   // ---- normalise and store: lane holds dims 32db + 8i + 4g + j of row my_i ----
-  if (!active) return;
+  if (!active) continue;
   {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
     l_run = __uint_as_float(r[0]) + __uint_as_float(r[1]);
@@ -342,6 +388,7 @@ __device__ void prefill_impl(const PrefillArgs& A) {
         *(uint2*)(orow + db * 32 + 8 * i + 4 * g) = v;
       }
   }
+  }  // tiles
 }
 
 }  // namespace luc

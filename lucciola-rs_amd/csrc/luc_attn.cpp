@@ -316,7 +316,7 @@ struct PrefillArgs {
   const int32_t* start_pos;
   void* out;
   int64_t out_stride;
-  int32_t batch, layer, num_layers, hkv, max_ctx, row_tiles;
+  int32_t batch, layer, num_layers, hkv, max_ctx, pairs;
   float qk_scale_log2;
 };
 
@@ -573,9 +573,12 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
                                std::to_string(head_dim) + "_g" + std::to_string(group),
                       &fn))
     return rc;
-  // workgroups: (sequence, kv head, group of up to 4 q-heads, 32 rows), 4 waves
-  const int row_tiles = (int)ceil_div(total_rows, 32);
-  const int64_t grid = (int64_t)batch * num_kv_heads * ceil_div(group, 4) * row_tiles;
+  // workgroups: (sequence, kv head, group of up to 4 q-heads, pair of 32-row
+  // tiles), 4 waves.  A sequence within the bound has at most
+  // min(total_rows, max_ctx) rows, so row_tiles tiles of 32 rows
+  const int row_tiles = (int)ceil_div(std::min(total_rows, max_ctx), 32);
+  const int pairs = (int)ceil_div(row_tiles, 2);
+  const int64_t grid = (int64_t)batch * num_kv_heads * ceil_div(group, 4) * pairs;
   if (grid > INT32_MAX) return fail(LUC_E_INVALID, "batch x kv heads x row tiles too large");
 
   // 1) bias + RoPE of every prompt row's q and k in place, cache write of the
@@ -597,7 +600,7 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
   p.tables = block_tables; p.table_stride = table_stride; p.cu_seqlens = cu_seqlens;
   p.start_pos = start_pos; p.out = out; p.out_stride = out_row_stride; p.batch = batch;
   p.layer = layer; p.num_layers = num_layers; p.hkv = num_kv_heads; p.max_ctx = max_ctx;
-  p.row_tiles = row_tiles; p.qk_scale_log2 = sm_scale * 1.4426950408889634f;
+  p.pairs = pairs; p.qk_scale_log2 = sm_scale * 1.4426950408889634f;
   void* args[] = {&p};
   return launch(fn, dim3((unsigned)grid), dim3(256), stream, args);
 }

@@ -144,3 +144,17 @@ def test_prefill_beyond_max_ctx_gives_nan(orc, luc):
     got = gpu_prefill(luc, h, max_ctx=60)  # sequence 1 reaches position 119
     o = orc.to_f32(got["out"], "bf16")
     assert np.all(np.isfinite(o[:50])) and np.all(np.isnan(o[50:]))
+
+
+def test_prefill_long_prompt_beyond_max_ctx_all_flagged(orc, luc):
+    """A flagged prompt longer than the grid's tiles (130 rows against a bound
+    of 40) has every one of its rows flagged; the other sequence matches the
+    oracle."""
+    cfg = wl.PrefillConfig("over_long", 2, 0, 14, 2, 64, "bf16", 0, 0, 0.5)
+    h = wl.host_prefill_inputs(cfg, seed=6, rows=[30, 130], starts=[4, 0])
+    got = gpu_prefill(luc, h, max_ctx=40)
+    o = orc.to_f32(got["out"], "bf16")
+    assert np.all(np.isnan(o[30:]))
+    want = oracle_prefill(orc, luc, h)
+    err = float(np.max(np.abs(o[:30] - orc.to_f32(want["out"], "bf16")[:30])))
+    assert err <= TOL["bf16"]
