@@ -139,8 +139,8 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   constexpr int ND = D / 32;      // 32-dim output tiles
   constexpr int NK = D / 16;      // 16-dim k-steps of QK
   // NS stages of K and V blocks, row-major, 16-byte chunk c of token t at
-  // slot c ^ (t & 7)
-  constexpr int NS = 3;
+  // slot c ^ (t & 7): block i is loaded NS - 2 iterations before its scores
+  constexpr int NS = D == 64 ? 4 : 3;
   constexpr int LPW = 2 * LOADS / W;  // loads per wave per block
   static_assert(LOADS % W == 0, "every wave issues the same number of K (and V) loads");
   __shared__ __attribute__((aligned(16))) char s_kv[NS][2][KB];
@@ -212,18 +212,29 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   const int nkv = last + 1;  // tokens the tile reads
   const int nblk = (nkv + BT - 1) / BT;
 
+  // Page numbers of block blk that this wave's loads need: load jj covers
+  // TPL tokens of one page (TPL divides the page), jj = i * W + w for the K
+  // and the V block alike.  Wave-uniform, through the scalar cache, and read
+  // one iteration before the loads they address, so no wait on them
+  // precedes a load.
+  constexpr int NPG = LOADS / W;
+  auto load_pages = [&](int blk, int* pg) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NPG; ++i) {
+      const int tb = blk * BT + (i * W + w) * TPL;
+      pg[i] = ((const const_i32_p*)trow)[min(tb, nkv - 1) / kPage];
+    }
+  };
+  int pgn[NPG];  // pages of the next block to issue
   // Issue the K and V loads of block blk into stage st: 2*LOADS wave-wide
   // loads shared round-robin by the waves.  Tokens past the context re-read
   // token nkv - 1 (finite), so their zero weights contribute exactly zero.
-  auto issue = [&](int blk, int st) __attribute__((always_inline)) {
+  auto issue = [&](int blk, int st, const int* pg) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int kv = i * W / LOADS, jj = i * W % LOADS + w;
-      // the load's TPL tokens lie in one page (TPL divides the page); its page
-      // number is wave-uniform and comes through the scalar cache, so no
-      // vector-memory wait precedes the load
       const int tb = blk * BT + jj * TPL;
-      const int page = ((const const_i32_p*)trow)[min(tb, nkv - 1) / kPage];
+      const int page = pg[i % NPG];
       const int tl = jj * TPL + lane / CH;  // token within the block
       const int c = lane % CH;
       const int t = min(tb + lane / CH, nkv - 1);
@@ -251,61 +262,58 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 #pragma unroll
     for (int k = 0; k < NK; ++k) asm volatile("" ::"v"(qf[k].x), "v"(qf[k].y), "v"(qf[k].z), "v"(qf[k].w));
   }
-  // every wave is done with the previous tile's last stage before it is refilled
-  if (k) __builtin_amdgcn_s_barrier();
-  issue(0, 0);
-  if (nblk > 1) issue(1, 1);
+  // s_waitcnt vmcnt(n * LPW): all but this wave's loads of the n most recently
+  // issued blocks have landed (loads complete in order)
+  auto wait_blocks = [&](int n) __attribute__((always_inline)) {
+    if (n >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPW) : "memory");
+    else if (n == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+  static_assert(NS - 2 <= 2, "wait_blocks covers up to two newer blocks");
 
-  f32x16 o[ND];
-#pragma unroll
-  for (int i = 0; i < ND; ++i)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[i][e] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
-
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int st = blk % NS;
-    // this block's loads (this wave's share) have landed -- the next block's
-    // LPW loads may still be in flight, they complete in order -- and after
-    // the barrier every wave's have, and every wave is done with the stage
-    // that block blk + 2 loads into (it held block blk - 1)
-    if (blk + 1 < nblk)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    if (blk + 2 < nblk) issue(blk + 2, (blk + 2) % NS);
-    if (!active) continue;
-    const int t0 = blk * BT;
+  // ---- S^T = K Q^T of the block in stage st, two 32-token halves ----
+  auto qk = [&](int st, f32x16* sc) __attribute__((always_inline)) {
     const uint32_t kbase = lds_addr(s_kv[st][0]);
-    const uint32_t vbase = lds_addr(s_kv[st][1]);
-
-    // ---- S^T = K Q^T for the two 32-token halves ----
     uint32_t ka_addr[NK];
 #pragma unroll
     for (int k = 0; k < NK; ++k) ka_addr[k] = kbase + krel[k];
-    f32x16 s[2];
-    auto qk_half = [&](auto hfc) __attribute__((always_inline)) {
+    auto half = [&](auto hfc) __attribute__((always_inline)) {
       constexpr int hf = decltype(hfc)::value;
       uint4 ka[NK];
 #pragma unroll
       for (int k = 0; k < NK; k += 4)
         lds_b128x4<hf * 32 * ROWB>(ka_addr[k], ka_addr[k + 1], ka_addr[k + 2], ka_addr[k + 3], ka + k);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[hf][e] = 0.0f;
+      for (int e = 0; e < 16; ++e) sc[hf][e] = 0.0f;
 #pragma unroll
-      for (int k = 0; k < NK; ++k) s[hf] = mfma32<DT>(ka[k], qf[k], s[hf]);
+      for (int k = 0; k < NK; ++k) sc[hf] = mfma32<DT>(ka[k], qf[k], sc[hf]);
     };
-    qk_half(IC<0>{});
-    qk_half(IC<1>{});
-    // ---- mask, online softmax (exp2 domain) ----
-    // s[hf][4i + j]: token t0 + 32hf + 8i + 4g + j, q row my_i
+    half(IC<0>{});
+    half(IC<1>{});
+  };
+
+  f32x16 o[ND], osum;  // O^T and, in every one of its rows, the row sums of P
+#pragma unroll
+  for (int i = 0; i < ND; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[i][e] = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) osum[e] = 0.0f;
+  float m_run = -INFINITY;
+  // all-ones A operand: its MFMA with P^T sums P over the block's tokens
+  const uint32_t one2 = DT == kF16 ? 0x3c003c00u : 0x3f803f80u;
+  const uint4 ones = make_uint4(one2, one2, one2, one2);
+
+  // ---- mask, online softmax (exp2 domain) and O^T += V^T P^T of block blk ----
+  auto softmax_pv = [&](int blk, int st, f32x16* sc) __attribute__((always_inline)) {
+    const int t0 = blk * BT;
+    // sc[hf][4i + j]: token t0 + 32hf + 8i + 4g + j, q row my_i
     float mb = -INFINITY;
     if (t0 + BT - 1 <= sp + rt * 32) {  // wave-uniform: below the diagonal, no mask
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) mb = fmaxf(mb, s[hf][e]);
+        for (int e = 0; e < 16; ++e) mb = fmaxf(mb, sc[hf][e]);
     } else {
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
@@ -314,8 +322,8 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int t = t0 + 32 * hf + 8 * i + 4 * g + j;
-            const float x = t <= my_pos ? s[hf][4 * i + j] : -INFINITY;
-            s[hf][4 * i + j] = x;
+            const float x = t <= my_pos ? sc[hf][4 * i + j] : -INFINITY;
+            sc[hf][4 * i + j] = x;
             mb = fmaxf(mb, x);
           }
     }
@@ -331,21 +339,20 @@ __device__ void prefill_impl(const PrefillArgs& A) {
       const float m_new = fmaxf(m_run, m_blk);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
-      l_run *= alpha;
 #pragma unroll
       for (int i = 0; i < ND; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) osum[e] *= alpha;
     }
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        s[hf][e] = __builtin_amdgcn_exp2f(fmaf(s[hf][e], scale, -m_run));
-        l_run += s[hf][e];
-      }
+      for (int e = 0; e < 16; ++e) sc[hf][e] = __builtin_amdgcn_exp2f(fmaf(sc[hf][e], scale, -m_run));
 
-    // ---- O^T += V^T P^T, 16 tokens per MFMA ----
+    // O^T += V^T P^T, 16 tokens per MFMA
+    const uint32_t vbase = lds_addr(s_kv[st][1]);
     uint32_t va_addr[ND];
 #pragma unroll
     for (int db = 0; db < ND; ++db) va_addr[db] = vbase + vrel[db];
@@ -353,14 +360,15 @@ __device__ void prefill_impl(const PrefillArgs& A) {
       constexpr int hf = decltype(hfc)::value, mm = decltype(mmc)::value;
       // B = P^T: slots 0..3 = tokens 16mm + 4g + j, slots 4..7 = 16mm + 8 + 4g + j
       constexpr int i0 = 2 * mm, i1 = 2 * mm + 1;
-      const uint4 pb = make_uint4(pack2(s[hf][4 * i0], s[hf][4 * i0 + 1], DT),
-                                  pack2(s[hf][4 * i0 + 2], s[hf][4 * i0 + 3], DT),
-                                  pack2(s[hf][4 * i1], s[hf][4 * i1 + 1], DT),
-                                  pack2(s[hf][4 * i1 + 2], s[hf][4 * i1 + 3], DT));
+      const uint4 pb = make_uint4(pack2(sc[hf][4 * i0], sc[hf][4 * i0 + 1], DT),
+                                  pack2(sc[hf][4 * i0 + 2], sc[hf][4 * i0 + 3], DT),
+                                  pack2(sc[hf][4 * i1], sc[hf][4 * i1 + 1], DT),
+                                  pack2(sc[hf][4 * i1 + 2], sc[hf][4 * i1 + 3], DT));
       constexpr int off = (32 * hf + 16 * mm) * ROWB;  // first token of the lane's slots, less 4g
       uint2 va[ND][2];
 #pragma unroll
       for (int db = 0; db < ND; ++db) lds_tr16x2<off, off + 8 * ROWB>(va_addr[db], va[db]);
+      osum = mfma32<DT>(ones, pb, osum);
 #pragma unroll
       for (int db = 0; db < ND; ++db)
         o[db] = mfma32<DT>(make_uint4(va[db][0].x, va[db][0].y, va[db][1].x, va[db][1].y), pb, o[db]);
@@ -369,16 +377,47 @@ __device__ void prefill_impl(const PrefillArgs& A) {
     pv_step(IC<0>{}, IC<1>{});
     pv_step(IC<1>{}, IC<0>{});
     pv_step(IC<1>{}, IC<1>{});
+  };
+
+  // Iteration blk: (after its loads and a barrier) the scores of block blk+1
+  // go to the matrix cores while this wave's VALU does the softmax of block
+  // blk, then block blk's PV.  The barrier also tells every wave that block
+  // blk-1 is consumed, so its stage takes block blk + NS - 1.
+  auto step = [&](int blk, f32x16* cur, f32x16* nxt) __attribute__((always_inline)) {
+    if (blk + 1 < nblk) {
+      wait_blocks(min(NS - 3, nblk - 2 - blk));
+      __builtin_amdgcn_s_barrier();
+      if (blk + NS - 1 < nblk) {
+        issue(blk + NS - 1, (blk + NS - 1) % NS, pgn);
+        if (blk + NS < nblk) load_pages(blk + NS, pgn);
+      }
+      if (active) qk((blk + 1) % NS, nxt);
+    }
+    if (active) softmax_pv(blk, blk % NS, cur);
+  };
+
+  // every wave is done with the previous tile's last stage before it is refilled
+  if (k) __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int j = 0; j < NS - 1; ++j)
+    if (j < nblk) {
+      load_pages(j, pgn);
+      issue(j, j, pgn);
+    }
+  if (NS - 1 < nblk) load_pages(NS - 1, pgn);
+  wait_blocks(min(NS - 2, nblk - 1));
+  __builtin_amdgcn_s_barrier();
+  f32x16 sa[2], sb[2];
+  if (active) qk(0, sa);
+  for (int blk = 0; blk < nblk; blk += 2) {
+    step(blk, sa, sb);
+    if (blk + 1 < nblk) step(blk + 1, sb, sa);
   }
 
   // ---- normalise and store: lane holds dims 32db + 8i + 4g + j of row my_i ----
   if (!active) continue;
-  {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
-    l_run = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
   if (row_ok) {
-    const float inv = 1.0f / l_run;
+    const float inv = 1.0f / osum[0];
 #pragma unroll
     for (int db = 0; db < ND; ++db)
 #pragma unroll

@@ -11,6 +11,13 @@
 // The rotation rounds each product and the difference/sum separately
 // (contraction off), so results are reproducible bit for bit.
 //
+// Two kernels compute the same values.  luc_rope_append_{dt}: one workgroup
+// per row, element by element, any alignment.  luc_rope_append_vec_{dt}_d{D}:
+// one lane per 16-byte chunk pair -- elements i..i+7 and i+D/2..i+D/2+7 of
+// one head (a rotation unit) or elements i..i+7 of a v head -- with 16-byte
+// loads and stores, for 16-byte aligned rows (the host picks it when every
+// pointer and the row stride allow).
+//
 // Row -> (table row, position):
 //   decode mode  (cu_seqlens == nullptr): table row r, position positions[r]
 //   packed mode  (cu_seqlens != nullptr): row r belongs to the sequence b with
@@ -21,6 +28,24 @@
 namespace luc {
 
 enum : int { kRopeQ = 1, kRopeK = 2, kWriteKV = 4 };
+
+// Row -> (table row b, position), as above.
+__device__ inline void row_position(int row, const int* positions, const int* cu_seqlens,
+                                    const int* start_pos, int batch, int& seq, int& pos) {
+  seq = row;
+  if (cu_seqlens) {
+    int lo = 0, hi = batch - 1;  // last b with cu_seqlens[b] <= row
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (cu_seqlens[mid] <= row) lo = mid; else hi = mid - 1;
+    }
+    seq = lo;
+    pos = start_pos[seq] + (row - cu_seqlens[seq]);
+  } else {
+    pos = positions[row];
+  }
+}
+
 
 template <int DT>
 __device__ inline void rotate(uint16_t* x, const uint16_t* bias, int i1, int i2, float c, float s,
@@ -47,18 +72,8 @@ __device__ void rope_append_impl(uint16_t* q, const uint16_t* q_bias, uint16_t* 
                                  int table_stride, uint16_t* k_pool, uint16_t* v_pool, int layer,
                                  int num_layers, int hq, int hkv, int head_dim, int flags) {
   const int row = blockIdx.x;
-  int seq = row, pos;
-  if (cu_seqlens) {
-    int lo = 0, hi = batch - 1;  // last b with cu_seqlens[b] <= row
-    while (lo < hi) {
-      int mid = (lo + hi + 1) >> 1;
-      if (cu_seqlens[mid] <= row) lo = mid; else hi = mid - 1;
-    }
-    seq = lo;
-    pos = start_pos[seq] + (row - cu_seqlens[seq]);
-  } else {
-    pos = positions[row];
-  }
+  int seq, pos;
+  row_position(row, positions, cu_seqlens, start_pos, batch, seq, pos);
   // Rows whose position falls outside the table row (or is negative) are
   // left untouched rather than written out of bounds.
   if (pos < 0 || ((flags & kWriteKV) && pos >= table_stride * kPage)) return;
@@ -117,7 +132,123 @@ __device__ void rope_append_impl(uint16_t* q, const uint16_t* q_bias, uint16_t* 
   }
 }
 
+// 16-bit element e (0..7) of a 16-byte chunk.
+__device__ inline uint16_t elem(const uint4& v, int e) {
+  const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+  return (uint16_t)(e & 1 ? w >> 16 : w & 0xffffu);
+}
+__device__ inline uint4 pack8(const uint16_t* e) {
+  return make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                    e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
+}
+
+template <int DT, int D>
+__device__ void rope_append_vec_impl(uint16_t* q, const uint16_t* q_bias, uint16_t* k,
+                                     const uint16_t* k_bias, const uint16_t* v,
+                                     const uint16_t* v_bias, int64_t row_stride,
+                                     const float* cos_t, const float* sin_t, const int* positions,
+                                     const int* cu_seqlens, const int* start_pos, int batch,
+                                     const int* tables, int table_stride, uint16_t* k_pool,
+                                     uint16_t* v_pool, int layer, int num_layers, int hq, int hkv,
+                                     int flags, int rows) {
+#pragma clang fp contract(off)
+  constexpr int C = D / 16;  // 8-element chunks per half head
+  constexpr int HALF = D / 2;
+  const int nq = (flags & kRopeQ) ? hq : 0;
+  const int nk = (flags & (kRopeK | kWriteKV)) ? hkv : 0;
+  const int nv = (flags & kWriteKV) ? hkv : 0;
+  const int rot_units = (nq + nk) * C;
+  const int units = rot_units + nv * 2 * C;  // lanes per row
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int row = (int)(item / units);
+  if (row >= rows) return;
+  const int u = (int)(item - (int64_t)row * units);
+  const int64_t roff = (int64_t)row * row_stride;
+  const int64_t head_stride = (int64_t)kPage * D;
+  // The operands depend on the row only: their loads are issued before the
+  // row's position is looked up (cu_seqlens search, table), so the two
+  // latencies overlap.
+  const bool rot = u < rot_units;
+  const int hh = rot ? u / C : (u - rot_units) / (2 * C);
+  const int i = rot ? (u % C) * 8 : ((u - rot_units) % (2 * C)) * 8;
+  const bool isq = rot && hh < nq;
+  const int h = isq || !rot ? hh : hh - nq;
+  uint16_t* const x = (isq ? q : rot ? k : const_cast<uint16_t*>(v)) + roff + (int64_t)h * D;
+  const uint16_t* const bias = isq ? q_bias : rot ? k_bias : v_bias;
+  uint4 a = *(const uint4*)(x + i), b = make_uint4(0, 0, 0, 0);
+  if (rot) b = *(const uint4*)(x + i + HALF);
+  uint4 ba = make_uint4(0, 0, 0, 0), bb = ba;
+  if (bias) {
+    ba = *(const uint4*)(bias + h * D + i);
+    if (rot) bb = *(const uint4*)(bias + h * D + i + HALF);
+  }
+  int seq, pos;
+  row_position(row, positions, cu_seqlens, start_pos, batch, seq, pos);
+  if (pos < 0 || ((flags & kWriteKV) && pos >= table_stride * kPage)) return;
+  int64_t slot0 = 0;  // pool offset of (pos, head 0, dim 0)
+  if (flags & kWriteKV) {
+    const int64_t phys = tables[(int64_t)seq * table_stride + pos / kPage];
+    slot0 = ((phys * num_layers + layer) * hkv) * head_stride + (int64_t)(pos % kPage) * D;
+  }
+  if (rot) {
+    if (isq || (flags & kRopeK)) {
+      const float4* cp = (const float4*)(cos_t + (int64_t)pos * HALF + i);
+      const float4* sp = (const float4*)(sin_t + (int64_t)pos * HALF + i);
+      const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+      const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+      uint16_t o1[8], o2[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float b1 = bias ? St<DT>::load(elem(ba, e)) : 0.0f;
+        const float b2 = bias ? St<DT>::load(elem(bb, e)) : 0.0f;
+        const float v1 = St<DT>::load(elem(a, e)) + b1;
+        const float v2 = St<DT>::load(elem(b, e)) + b2;
+        const float p = v1 * cs[e];
+        const float r = v2 * sn[e];
+        const float m = v1 * sn[e];
+        const float n = v2 * cs[e];
+        o1[e] = St<DT>::store(p - r);
+        o2[e] = St<DT>::store(m + n);
+      }
+      a = pack8(o1);
+      b = pack8(o2);
+      *(uint4*)(x + i) = a;
+      *(uint4*)(x + i + HALF) = b;
+    }
+    if (!isq && (flags & kWriteKV)) {
+      uint16_t* dst = k_pool + slot0 + h * head_stride + i;
+      *(uint4*)dst = a;
+      *(uint4*)(dst + HALF) = b;
+    }
+  } else {
+    uint16_t o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      o[e] = St<DT>::store(St<DT>::load(elem(a, e)) + (bias ? St<DT>::load(elem(ba, e)) : 0.0f));
+    *(uint4*)(v_pool + slot0 + h * head_stride + i) = pack8(o);
+  }
+}
+
 }  // namespace luc
+
+#define LUC_ROPE_APPEND_VEC(NAME, DT, D)                                                          \
+  extern "C" __global__ __launch_bounds__(256) void NAME(                                         \
+      uint16_t* q, const uint16_t* q_bias, uint16_t* k, const uint16_t* k_bias,                   \
+      const uint16_t* v, const uint16_t* v_bias, int64_t row_stride, const float* cos_t,          \
+      const float* sin_t, const int* positions, const int* cu_seqlens, const int* start_pos,      \
+      int batch, const int* tables, int table_stride, uint16_t* k_pool, uint16_t* v_pool,         \
+      int layer, int num_layers, int hq, int hkv, int head_dim, int flags, int rows) {            \
+    luc::rope_append_vec_impl<DT, D>(q, q_bias, k, k_bias, v, v_bias, row_stride, cos_t, sin_t,   \
+                                     positions, cu_seqlens, start_pos, batch, tables,             \
+                                     table_stride, k_pool, v_pool, layer, num_layers, hq, hkv,    \
+                                     flags, rows);                                                \
+  }
+
+LUC_ROPE_APPEND_VEC(luc_rope_append_vec_bf16_d64, luc::kBF16, 64)
+LUC_ROPE_APPEND_VEC(luc_rope_append_vec_bf16_d128, luc::kBF16, 128)
+LUC_ROPE_APPEND_VEC(luc_rope_append_vec_f16_d64, luc::kF16, 64)
+LUC_ROPE_APPEND_VEC(luc_rope_append_vec_f16_d128, luc::kF16, 128)
 
 #define LUC_ROPE_APPEND(NAME, DT)                                                                 \
   extern "C" __global__ __launch_bounds__(256) void NAME(                                         \

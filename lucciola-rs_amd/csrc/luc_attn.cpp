@@ -144,14 +144,36 @@ struct AppendArgs {
 };
 
 int launch_append(const luc_ctx* ctx, void* stream, int dtype, int rows, AppendArgs a) {
-  hipFunction_t fn;
-  if (int rc = get_fn(ctx, std::string("luc_rope_append_") + dt_name(dtype), &fn)) return rc;
   void* args[] = {&a.q,         &a.q_bias,    &a.k,          &a.k_bias,   &a.v,
                   &a.v_bias,    &a.row_stride, &a.cos_t,     &a.sin_t,    &a.positions,
                   &a.cu_seqlens, &a.start_pos, &a.batch,     &a.tables,   &a.table_stride,
                   &a.k_pool,    &a.v_pool,    &a.layer,      &a.num_layers, &a.hq,
-                  &a.hkv,       &a.head_dim,  &a.flags};
-  return launch(fn, dim3(rows), dim3(128), stream, args);
+                  &a.hkv,       &a.head_dim,  &a.flags,      &rows};
+  // 16-byte chunk kernel when every row and bias starts on 16 bytes (the
+  // pools always do), else the element-wise kernel (same values)
+  auto al = [](const void* p) { return !p || aligned(p, 16); };
+  const bool rope = a.flags & (kRopeQ | kRopeK);
+  const bool vec = a.row_stride % 8 == 0 && al(a.q) && al(a.k) && al(a.v) && al(a.q_bias) &&
+                   al(a.k_bias) && al(a.v_bias) && (!rope || (al(a.cos_t) && al(a.sin_t)));
+  hipFunction_t fn;
+  if (!vec) {
+    if (int rc = get_fn(ctx, std::string("luc_rope_append_") + dt_name(dtype), &fn)) return rc;
+    return launch(fn, dim3(rows), dim3(128), stream, args);
+  }
+  if (int rc = get_fn(ctx, std::string("luc_rope_append_vec_") + dt_name(dtype) + "_d" +
+                               std::to_string(a.head_dim),
+                      &fn))
+    return rc;
+  // lanes per row: one per rotation unit (8 + 8 elements of a q or k head),
+  // one per 8 elements of a v head
+  const int chunks = a.head_dim / 16;
+  const int nq = (a.flags & kRopeQ) ? a.hq : 0;
+  const int nk = (a.flags & (kRopeK | kWriteKV)) ? a.hkv : 0;
+  const int nv = (a.flags & kWriteKV) ? a.hkv : 0;
+  const int64_t lanes = (int64_t)rows * ((nq + nk) * chunks + nv * 2 * chunks);
+  const int64_t grid = ceil_div(lanes, 256);
+  if (grid > INT32_MAX) return fail(LUC_E_INVALID, "too many rows for one launch");
+  return launch(fn, dim3((unsigned)grid), dim3(256), stream, args);
 }
 
 int check_rows(int num_tokens, int64_t row_stride, int min_row) {
@@ -359,6 +381,7 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
   std::vector<std::string> names;
   for (const char* dt : {"bf16", "f16"}) {
     names.push_back(std::string("luc_rope_append_") + dt);
+    for (int d : {64, 128}) names.push_back(std::string("luc_rope_append_vec_") + dt + "_d" + std::to_string(d));
     for (int d : {64, 128})
       for (int g = 1; g <= 8; ++g)
         names.push_back(std::string("luc_prefill_") + dt + "_d" + std::to_string(d) + "_g" +

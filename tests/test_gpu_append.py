@@ -22,15 +22,20 @@ def make_rows(rng, n, hq, hkv, d, dtype):
     return qkv, qb, kb, vb
 
 
+@pytest.mark.parametrize("pad", [0, 2], ids=["vec", "padded"])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (28, 4, 128), (12, 2, 128)])
-def test_rope_append_bit_exact(orc, luc, dtype, hq, hkv, d):
+def test_rope_append_bit_exact(orc, luc, dtype, hq, hkv, d, pad):
+    """pad=0: 16-byte aligned rows (the 16-byte chunk kernel); pad=2: a row
+    stride of row + 2 elements (the element-wise kernel).  Both bit-exact."""
     rng = np.random.default_rng(hq + d)
     positions = np.array([0, 1, 15, 16, 17, 31, 32, 255, 256, 511, 4095, 639], np.int32)
     n = len(positions)
     # every row (sequence) owns its pages, so no two rows share a cache slot
     L, layer, pages = 3, 1, n * 40 + 1
     qkv, qb, kb, vb = make_rows(rng, n, hq, hkv, d, dtype)
+    if pad:  # padding columns the kernels must leave alone
+        qkv = np.concatenate([qkv, pins.bits(rng.standard_normal((n, pad)), dtype)], axis=1)
     perm = rng.permutation(pages - 1).astype(np.int32)
     tables = np.full((n, 256), pages - 1, np.int32)
     tables[:, :40] = perm.reshape(n, 40)
@@ -45,7 +50,7 @@ def test_rope_append_bit_exact(orc, luc, dtype, hq, hkv, d):
     qd, kd = hq * d, hkv * d
     for r in range(n):
         row = oq[r]
-        qv, kv, vv = row[:qd], row[qd:qd + kd], row[qd + kd:]
+        qv, kv, vv = row[:qd], row[qd:qd + kd], row[qd + kd:qd + 2 * kd]
         q2, k2 = qv.copy(), kv.copy()
         orc.rope(q2, qb, k2, kb, cos, sin, int(positions[r]), d, hq, hkv, dtype)
         row[:qd], row[qd:qd + kd] = q2, k2
