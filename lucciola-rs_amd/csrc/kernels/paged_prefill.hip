@@ -11,10 +11,10 @@
 // flash_decoding call for that token computes (src/kernels/attention.cu:4-176),
 // since by then the cache holds those positions and nothing later.
 //
-// Work decomposition: workgroup = (sequence b, kv head h, group of up to 4 of
-// its G = Hq/Hkv q-heads, pair p of tiles of 32 prompt rows), one wave per
-// q-head over the same 32 rows, so the K and V tiles staged in LDS serve 4
-// heads (GQA).  Of a sequence's nt row tiles the workgroup takes tile nt-1-p
+// Work decomposition: workgroup = (sequence b, kv head h, pair p of tiles of
+// 32 prompt rows), one wave per q-head of the group of G = Hq/Hkv q-heads
+// (4 waves for G <= 4, else 8) over the same 32 rows, so the K and V tiles
+// staged in LDS serve every head of the group (GQA).  Of a sequence's nt row tiles the workgroup takes tile nt-1-p
 // and then tile p: causal tile t reads about t+1 token blocks, so every pair
 // carries the same work, the grid is one wave of equal workgroups and none
 // waits on a long tail.  For each tile the workgroup walks the tokens
@@ -126,24 +126,33 @@ __device__ inline void lds_tr16x2(uint32_t a, uint2* x) {
       : "memory");
 }
 
+// Waves per prefill workgroup for group size G (<= 8).
+constexpr int prefill_waves(int g) { return g <= 4 ? 4 : 8; }
+
 template <int DT, int D, int G>
 __device__ void prefill_impl(const PrefillArgs& A) {
-  constexpr int W = 4;            // waves per workgroup: up to 4 heads of the group
+  constexpr int W = prefill_waves(G);  // waves per workgroup: one per q-head of the group
   constexpr int NHG = (G + W - 1) / W;
   constexpr int BT = 64;          // tokens per block
   constexpr int CH = D / 8;       // 16-byte chunks per token row
   constexpr int ROWB = 2 * D;     // bytes per token row
   constexpr int KB = BT * ROWB;   // bytes of a K (or V) block
-  constexpr int LOADS = KB / 1024;       // 1 KB wave-wide loads per K (or V) block
+  // A stage holds SB consecutive blocks (a super-block): the waves meet at a
+  // barrier once per stage.  Two blocks when the LDS of one workgroup per CU
+  // allows it (d64, 8 waves), else one.
+  constexpr int SB = (D == 64 && W == 8) ? 2 : 1;
+  constexpr int KS = SB * KB;     // bytes of the K (or V) part of a stage
+  constexpr int LOADS = KS / 1024;       // 1 KB wave-wide loads per K (or V) part
   constexpr int TPL = 1024 / ROWB;       // tokens per 1 KB load
   constexpr int ND = D / 32;      // 32-dim output tiles
   constexpr int NK = D / 16;      // 16-dim k-steps of QK
-  // NS stages of K and V blocks, row-major, 16-byte chunk c of token t at
-  // slot c ^ (t & 7): block i is loaded NS - 2 iterations before its scores
+  // NS stages of K and V super-blocks, row-major, 16-byte chunk c of token t
+  // at slot c ^ (t & 7): super-block j is loaded NS - 2 stages before its
+  // scores
   constexpr int NS = D == 64 ? 4 : 3;
-  constexpr int LPW = 2 * LOADS / W;  // loads per wave per block
+  constexpr int LPW = 2 * LOADS / W;  // loads per wave per stage
   static_assert(LOADS % W == 0, "every wave issues the same number of K (and V) loads");
-  __shared__ __attribute__((aligned(16))) char s_kv[NS][2][KB];
+  __shared__ __attribute__((aligned(16))) char s_kv[NS][2][KS];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -212,28 +221,29 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   const int nkv = last + 1;  // tokens the tile reads
   const int nblk = (nkv + BT - 1) / BT;
 
-  // Page numbers of block blk that this wave's loads need: load jj covers
-  // TPL tokens of one page (TPL divides the page), jj = i * W + w for the K
-  // and the V block alike.  Wave-uniform, through the scalar cache, and read
+  // Page numbers of super-block sb that this wave's loads need: load jj
+  // covers TPL tokens of one page (TPL divides the page), jj = i * W + w for
+  // the K and the V part alike.  Wave-uniform, through the scalar cache, and read
   // one iteration before the loads they address, so no wait on them
   // precedes a load.
   constexpr int NPG = LOADS / W;
-  auto load_pages = [&](int blk, int* pg) __attribute__((always_inline)) {
+  auto load_pages = [&](int sb, int* pg) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NPG; ++i) {
-      const int tb = blk * BT + (i * W + w) * TPL;
+      const int tb = sb * SB * BT + (i * W + w) * TPL;
       pg[i] = ((const const_i32_p*)trow)[min(tb, nkv - 1) / kPage];
     }
   };
   int pgn[NPG];  // pages of the next block to issue
-  // Issue the K and V loads of block blk into stage st: 2*LOADS wave-wide
-  // loads shared round-robin by the waves.  Tokens past the context re-read
-  // token nkv - 1 (finite), so their zero weights contribute exactly zero.
-  auto issue = [&](int blk, int st, const int* pg) __attribute__((always_inline)) {
+  // Issue the K and V loads of super-block sb into stage st: 2*LOADS
+  // wave-wide loads shared round-robin by the waves.  Tokens past the context
+  // re-read token nkv - 1 (finite), so their zero weights contribute exactly
+  // zero.
+  auto issue = [&](int sb, int st, const int* pg) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int kv = i * W / LOADS, jj = i * W % LOADS + w;
-      const int tb = blk * BT + jj * TPL;
+      const int tb = sb * SB * BT + jj * TPL;
       const int page = pg[i % NPG];
       const int tl = jj * TPL + lane / CH;  // token within the block
       const int c = lane % CH;
@@ -263,17 +273,17 @@ __device__ void prefill_impl(const PrefillArgs& A) {
     for (int k = 0; k < NK; ++k) asm volatile("" ::"v"(qf[k].x), "v"(qf[k].y), "v"(qf[k].z), "v"(qf[k].w));
   }
   // s_waitcnt vmcnt(n * LPW): all but this wave's loads of the n most recently
-  // issued blocks have landed (loads complete in order)
+  // issued super-blocks have landed (loads complete in order)
   auto wait_blocks = [&](int n) __attribute__((always_inline)) {
     if (n >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPW) : "memory");
     else if (n == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   };
-  static_assert(NS - 2 <= 2, "wait_blocks covers up to two newer blocks");
+  static_assert(NS - 2 <= 2, "wait_blocks covers up to two newer super-blocks");
 
-  // ---- S^T = K Q^T of the block in stage st, two 32-token halves ----
-  auto qk = [&](int st, f32x16* sc) __attribute__((always_inline)) {
-    const uint32_t kbase = lds_addr(s_kv[st][0]);
+  // ---- S^T = K Q^T of block blk, two 32-token halves ----
+  auto qk = [&](int blk, f32x16* sc) __attribute__((always_inline)) {
+    const uint32_t kbase = lds_addr(s_kv[(blk / SB) % NS][0]) + (blk % SB) * KB;
     uint32_t ka_addr[NK];
 #pragma unroll
     for (int k = 0; k < NK; ++k) ka_addr[k] = kbase + krel[k];
@@ -305,7 +315,7 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   const uint4 ones = make_uint4(one2, one2, one2, one2);
 
   // ---- mask, online softmax (exp2 domain) and O^T += V^T P^T of block blk ----
-  auto softmax_pv = [&](int blk, int st, f32x16* sc) __attribute__((always_inline)) {
+  auto softmax_pv = [&](int blk, f32x16* sc) __attribute__((always_inline)) {
     const int t0 = blk * BT;
     // sc[hf][4i + j]: token t0 + 32hf + 8i + 4g + j, q row my_i
     float mb = -INFINITY;
@@ -352,7 +362,7 @@ __device__ void prefill_impl(const PrefillArgs& A) {
       for (int e = 0; e < 16; ++e) sc[hf][e] = __builtin_amdgcn_exp2f(fmaf(sc[hf][e], scale, -m_run));
 
     // O^T += V^T P^T, 16 tokens per MFMA
-    const uint32_t vbase = lds_addr(s_kv[st][1]);
+    const uint32_t vbase = lds_addr(s_kv[(blk / SB) % NS][1]) + (blk % SB) * KB;
     uint32_t va_addr[ND];
 #pragma unroll
     for (int db = 0; db < ND; ++db) va_addr[db] = vbase + vrel[db];
@@ -379,33 +389,38 @@ __device__ void prefill_impl(const PrefillArgs& A) {
     pv_step(IC<1>{}, IC<1>{});
   };
 
-  // Iteration blk: (after its loads and a barrier) the scores of block blk+1
-  // go to the matrix cores while this wave's VALU does the softmax of block
-  // blk, then block blk's PV.  The barrier also tells every wave that block
-  // blk-1 is consumed, so its stage takes block blk + NS - 1.
+  // Iteration blk: the scores of block blk+1 go to the matrix cores while
+  // this wave's VALU does the softmax of block blk, then block blk's PV.
+  // When block blk+1 starts super-block J, its loads are waited for first,
+  // and the barrier also tells every wave that super-block J-2 is consumed,
+  // so its stage takes super-block J + NS - 2.
+  const int nsb = (nblk + SB - 1) / SB;
   auto step = [&](int blk, f32x16* cur, f32x16* nxt) __attribute__((always_inline)) {
     if (blk + 1 < nblk) {
-      wait_blocks(min(NS - 3, nblk - 2 - blk));
-      __builtin_amdgcn_s_barrier();
-      if (blk + NS - 1 < nblk) {
-        issue(blk + NS - 1, (blk + NS - 1) % NS, pgn);
-        if (blk + NS < nblk) load_pages(blk + NS, pgn);
+      if ((blk + 1) % SB == 0) {
+        const int J = (blk + 1) / SB;
+        wait_blocks(min(NS - 3, nsb - 1 - J));
+        __builtin_amdgcn_s_barrier();
+        if (J + NS - 2 < nsb) {
+          issue(J + NS - 2, (J + NS - 2) % NS, pgn);
+          if (J + NS - 1 < nsb) load_pages(J + NS - 1, pgn);
+        }
       }
-      if (active) qk((blk + 1) % NS, nxt);
+      if (active) qk(blk + 1, nxt);
     }
-    if (active) softmax_pv(blk, blk % NS, cur);
+    if (active) softmax_pv(blk, cur);
   };
 
   // every wave is done with the previous tile's last stage before it is refilled
   if (k) __builtin_amdgcn_s_barrier();
 #pragma unroll
   for (int j = 0; j < NS - 1; ++j)
-    if (j < nblk) {
+    if (j < nsb) {
       load_pages(j, pgn);
       issue(j, j, pgn);
     }
-  if (NS - 1 < nblk) load_pages(NS - 1, pgn);
-  wait_blocks(min(NS - 2, nblk - 1));
+  if (NS - 1 < nsb) load_pages(NS - 1, pgn);
+  wait_blocks(min(NS - 2, nsb - 1));
   __builtin_amdgcn_s_barrier();
   f32x16 sa[2], sb[2];
   if (active) qk(0, sa);
@@ -433,7 +448,7 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 }  // namespace luc
 
 #define LUC_PREFILL(DTN, DT, D, G)                                                              \
-  extern "C" __global__ __launch_bounds__(256) void luc_prefill_##DTN##_d##D##_g##G(             \
+  extern "C" __global__ __launch_bounds__(64 * luc::prefill_waves(G)) void luc_prefill_##DTN##_d##D##_g##G(             \
       luc::PrefillArgs a) {                                                                     \
     luc::prefill_impl<DT, D, G>(a);                                                             \
   }

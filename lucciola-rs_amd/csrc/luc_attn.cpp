@@ -596,12 +596,13 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
                                std::to_string(head_dim) + "_g" + std::to_string(group),
                       &fn))
     return rc;
-  // workgroups: (sequence, kv head, group of up to 4 q-heads, pair of 32-row
-  // tiles), 4 waves.  A sequence within the bound has at most
+  // workgroups: (sequence, kv head, pair of 32-row tiles), one wave per
+  // q-head of the group.  A sequence within the bound has at most
   // min(total_rows, max_ctx) rows, so row_tiles tiles of 32 rows
   const int row_tiles = (int)ceil_div(std::min(total_rows, max_ctx), 32);
   const int pairs = (int)ceil_div(row_tiles, 2);
-  const int64_t grid = (int64_t)batch * num_kv_heads * ceil_div(group, 4) * pairs;
+  const int waves = group <= 4 ? 4 : 8;  // one per q-head of the group (paged_prefill.hip)
+  const int64_t grid = (int64_t)batch * num_kv_heads * ceil_div(group, waves) * pairs;
   if (grid > INT32_MAX) return fail(LUC_E_INVALID, "batch x kv heads x row tiles too large");
 
   // 1) bias + RoPE of every prompt row's q and k in place, cache write of the
@@ -625,7 +626,7 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
   p.layer = layer; p.num_layers = num_layers; p.hkv = num_kv_heads; p.max_ctx = max_ctx;
   p.pairs = pairs; p.qk_scale_log2 = sm_scale * 1.4426950408889634f;
   void* args[] = {&p};
-  return launch(fn, dim3((unsigned)grid), dim3(256), stream, args);
+  return launch(fn, dim3((unsigned)grid), dim3(64 * waves), stream, args);
 }
 
 }  // extern "C"
