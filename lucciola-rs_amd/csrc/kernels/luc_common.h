@@ -19,11 +19,13 @@ template <> struct St<kBF16> {
   // low / high half of a packed pair
   __device__ static inline float lo(uint32_t w) { return __uint_as_float(w << 16); }
   __device__ static inline float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  // round to nearest even; a NaN keeps its sign and top payload bits, quieted
+  // (branch-free: a select, not a divergent branch)
   __device__ static inline uint16_t store(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t quiet = (u >> 16) | 0x0040u;
+    return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
   }
   // f32 dot of two packed pairs, accumulated into c
   __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
@@ -40,7 +42,14 @@ template <> struct St<kF16> {
   __device__ static inline float hi(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
   }
-  __device__ static inline uint16_t store(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+  // round to nearest even (v_cvt_f16_f32, denormals kept); a NaN keeps its
+  // sign and top 10 payload bits, quieted (a select, not a branch)
+  __device__ static inline uint16_t store(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t quiet = ((u >> 16) & 0x8000u) | 0x7e00u | ((u >> 13) & 0x3ffu);
+    const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)f);
+    return (u & 0x7fffffffu) > 0x7f800000u ? (uint16_t)quiet : h;
+  }
   __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b), c,
                                   false);
@@ -155,6 +164,72 @@ __device__ inline void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// 16-bit element e (0..7) of a 16-byte chunk, and eight elements packed.
+__device__ inline uint16_t chunk_elem(const uint4& v, int e) {
+  const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+  return (uint16_t)(e & 1 ? w >> 16 : w & 0xffffu);
+}
+__device__ inline uint4 chunk_pack(const uint16_t* e) {
+  return make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                    e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
+}
+
+// RoPE of eight element pairs: x1 holds dims i..i+7 of a head, x2 dims
+// i+D/2..i+D/2+7, c and s the cos/sin of dims i..i+7 at the row's position
+// (c0|c1, s0|s1), b1/b2 the bias chunks (used when has_bias).  Each sum,
+// product and the final difference/sum rounds separately in f32 (contraction
+// off), then to storage -- the same bits wherever it runs
+// (src/kernels/rope.cu:31-52).
+template <int DT>
+__device__ inline void rope_rotate8(uint4& x1, uint4& x2, const uint4& b1, const uint4& b2,
+                                    bool has_bias, const float4& c0, const float4& c1,
+                                    const float4& s0, const float4& s1) {
+#pragma clang fp contract(off)
+  const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  float r1[8], r2[8];
+  bool nan = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float bb1 = has_bias ? St<DT>::load(chunk_elem(b1, e)) : 0.0f;
+    const float bb2 = has_bias ? St<DT>::load(chunk_elem(b2, e)) : 0.0f;
+    const float v1 = St<DT>::load(chunk_elem(x1, e)) + bb1;
+    const float v2 = St<DT>::load(chunk_elem(x2, e)) + bb2;
+    const float p = v1 * cs[e];
+    const float r = v2 * sn[e];
+    const float m = v1 * sn[e];
+    const float n = v2 * cs[e];
+    r1[e] = p - r;
+    r2[e] = m + n;
+    nan |= __builtin_isnan(r1[e]) | __builtin_isnan(r2[e]);
+  }
+  if (DT == kBF16 && !nan) {
+    // v_cvt_pk_bf16_f32: round to nearest even, f32 denormals kept (the
+    // kernels run with denormals enabled) -- the bits of St<kBF16>::store
+    // for every non-NaN value
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    uint32_t w1[4], w2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bf16x2 a = {(__bf16)r1[2 * e], (__bf16)r1[2 * e + 1]};
+      const bf16x2 b = {(__bf16)r2[2 * e], (__bf16)r2[2 * e + 1]};
+      w1[e] = __builtin_bit_cast(uint32_t, a);
+      w2[e] = __builtin_bit_cast(uint32_t, b);
+    }
+    x1 = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+    x2 = make_uint4(w2[0], w2[1], w2[2], w2[3]);
+  } else {
+    uint16_t o1[8], o2[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      o1[e] = St<DT>::store(r1[e]);
+      o2[e] = St<DT>::store(r2[e]);
+    }
+    x1 = chunk_pack(o1);
+    x2 = chunk_pack(o2);
+  }
 }
 
 // Online softmax: p = exp2(s - m) is kept <= 2^kLazyMax (exact in f16 range)

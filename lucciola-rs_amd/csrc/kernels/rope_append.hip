@@ -132,16 +132,6 @@ __device__ void rope_append_impl(uint16_t* q, const uint16_t* q_bias, uint16_t* 
   }
 }
 
-// 16-bit element e (0..7) of a 16-byte chunk.
-__device__ inline uint16_t elem(const uint4& v, int e) {
-  const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
-  return (uint16_t)(e & 1 ? w >> 16 : w & 0xffffu);
-}
-__device__ inline uint4 pack8(const uint16_t* e) {
-  return make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
-                    e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
-}
-
 template <int DT, int D>
 __device__ void rope_append_vec_impl(uint16_t* q, const uint16_t* q_bias, uint16_t* k,
                                      const uint16_t* k_bias, const uint16_t* v,
@@ -183,36 +173,46 @@ __device__ void rope_append_vec_impl(uint16_t* q, const uint16_t* q_bias, uint16
     if (rot) bb = *(const uint4*)(bias + h * D + i + HALF);
   }
   int seq, pos;
-  row_position(row, positions, cu_seqlens, start_pos, batch, seq, pos);
+  if (cu_seqlens) {
+    // The workgroup's first row is looked up once, through the scalar cache;
+    // lanes whose row lies in the same sequence take it from there, the
+    // others (a workgroup that straddles a sequence boundary) search alone.
+    typedef __attribute__((address_space(4))) const int const_i32_p;
+    const const_i32_p* cu = (const const_i32_p*)cu_seqlens;
+    const int row_first = (int)((int64_t)blockIdx.x * blockDim.x / units);
+    int lo = 0, hi = batch - 1;  // last b with cu_seqlens[b] <= row_first
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (cu[mid] <= row_first) lo = mid; else hi = mid - 1;
+    }
+    if (row < cu[lo + 1]) {
+      seq = lo;
+      pos = ((const const_i32_p*)start_pos)[lo] + (row - cu[lo]);
+    } else {
+      row_position(row, positions, cu_seqlens, start_pos, batch, seq, pos);
+    }
+  } else {
+    seq = row;
+    pos = positions[row];
+  }
   if (pos < 0 || ((flags & kWriteKV) && pos >= table_stride * kPage)) return;
+  // the rotation's cos/sin and the page number both depend on the position
+  // only: issued together
+  const bool rope = rot && (isq || (flags & kRopeK));
+  float4 c0 = make_float4(0.f, 0.f, 0.f, 0.f), c1 = c0, s0 = c0, s1 = c0;
+  if (rope) {
+    const float4* cp = (const float4*)(cos_t + (int64_t)pos * HALF + i);
+    const float4* sp = (const float4*)(sin_t + (int64_t)pos * HALF + i);
+    c0 = cp[0]; c1 = cp[1]; s0 = sp[0]; s1 = sp[1];
+  }
   int64_t slot0 = 0;  // pool offset of (pos, head 0, dim 0)
   if (flags & kWriteKV) {
     const int64_t phys = tables[(int64_t)seq * table_stride + pos / kPage];
     slot0 = ((phys * num_layers + layer) * hkv) * head_stride + (int64_t)(pos % kPage) * D;
   }
   if (rot) {
-    if (isq || (flags & kRopeK)) {
-      const float4* cp = (const float4*)(cos_t + (int64_t)pos * HALF + i);
-      const float4* sp = (const float4*)(sin_t + (int64_t)pos * HALF + i);
-      const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
-      const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-      const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-      uint16_t o1[8], o2[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float b1 = bias ? St<DT>::load(elem(ba, e)) : 0.0f;
-        const float b2 = bias ? St<DT>::load(elem(bb, e)) : 0.0f;
-        const float v1 = St<DT>::load(elem(a, e)) + b1;
-        const float v2 = St<DT>::load(elem(b, e)) + b2;
-        const float p = v1 * cs[e];
-        const float r = v2 * sn[e];
-        const float m = v1 * sn[e];
-        const float n = v2 * cs[e];
-        o1[e] = St<DT>::store(p - r);
-        o2[e] = St<DT>::store(m + n);
-      }
-      a = pack8(o1);
-      b = pack8(o2);
+    if (rope) {
+      rope_rotate8<DT>(a, b, ba, bb, bias != nullptr, c0, c1, s0, s1);
       *(uint4*)(x + i) = a;
       *(uint4*)(x + i + HALF) = b;
     }
@@ -225,8 +225,8 @@ __device__ void rope_append_vec_impl(uint16_t* q, const uint16_t* q_bias, uint16
     uint16_t o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      o[e] = St<DT>::store(St<DT>::load(elem(a, e)) + (bias ? St<DT>::load(elem(ba, e)) : 0.0f));
-    *(uint4*)(v_pool + slot0 + h * head_stride + i) = pack8(o);
+      o[e] = St<DT>::store(St<DT>::load(chunk_elem(a, e)) + (bias ? St<DT>::load(chunk_elem(ba, e)) : 0.0f));
+    *(uint4*)(v_pool + slot0 + h * head_stride + i) = chunk_pack(o);
   }
 }
 

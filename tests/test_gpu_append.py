@@ -81,6 +81,78 @@ def test_rope_append_bit_exact(orc, luc, dtype, hq, hkv, d, pad):
     assert np.array_equal(from_dev(t_vp), ov)
 
 
+def special_values(rng, shape, dtype):
+    """A mix that exercises every rounding path of the rotation: ordinary
+    values, values whose rotated results are subnormal, values near the top of
+    the range (sums overflow to inf), infinities, NaNs, signed zeros."""
+    big = 3.0e38 if dtype == "bf16" else 6.0e4
+    tiny = 1.0e-39 if dtype == "bf16" else 3.0e-6
+    n = int(np.prod(shape))
+    kind = rng.integers(0, 8, n)
+    x = rng.standard_normal(n)
+    x = np.where(kind == 1, x * tiny, x)
+    x = np.where(kind == 2, np.sign(x) * big * rng.uniform(0.5, 1.0, n), x)
+    x = np.where(kind == 3, np.inf * np.sign(x), x)
+    x = np.where(kind == 4, np.nan, x)
+    x = np.where(kind == 5, np.copysign(0.0, x), x)
+    b = pins.bits(x.reshape(shape), dtype)
+    # NaNs with other payloads and signs, set bit by bit
+    nan = rng.random(b.shape) < 0.02
+    payload = (0x7fc1 if dtype == "bf16" else 0x7e01) | (rng.integers(0, 2, b.shape) << 15)
+    return np.where(nan, payload, b).astype(np.uint16)
+
+
+@pytest.mark.parametrize("pad", [0, 2], ids=["vec", "padded"])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_rope_append_special_values_bit_exact(orc, luc, dtype, pad):
+    """Subnormal results, overflow to inf, inf/NaN inputs and signed zeros:
+    the GPU rotation and rounding match the oracle bit for bit (NaN results:
+    NaN on both sides), through the 16-byte chunk kernel (pad=0) and the
+    element-wise one (pad=2)."""
+    rng = np.random.default_rng(77)
+    hq, hkv, d = 14, 2, 64
+    n = 24
+    positions = rng.integers(0, 4096, n).astype(np.int32)
+    row = (hq + 2 * hkv) * d
+    qkv = special_values(rng, (n, row + pad), dtype)
+    qb = special_values(rng, (hq * d,), dtype)
+    kb = pins.bits(rng.standard_normal(hkv * d) * 0.2, dtype)
+    vb = special_values(rng, (hkv * d,), dtype)
+    L, layer, pages = 1, 0, n * 256 + 1
+    tables = (np.arange(n * 256, dtype=np.int32).reshape(n, 256))
+    kp = np.zeros((pages, L, hkv, 16, d), np.uint16)
+    vp = np.zeros((pages, L, hkv, 16, d), np.uint16)
+    rope = rope_cache(luc, d)
+    cos, sin = rope.cos.cpu().numpy(), rope.sin.cpu().numpy()
+    oq, ok_, ov = qkv.copy(), kp.copy(), vp.copy()
+    qd, kd = hq * d, hkv * d
+    for r in range(n):
+        rw = oq[r]
+        q2, k2 = rw[:qd].copy(), rw[qd:qd + kd].copy()
+        orc.rope(q2, qb, k2, kb, cos, sin, int(positions[r]), d, hq, hkv, dtype)
+        rw[:qd], rw[qd:qd + kd] = q2, k2
+        orc.kv_update(ok_, ov, k2, np.ascontiguousarray(rw[qd + kd:qd + 2 * kd]), vb,
+                      np.ascontiguousarray(tables[r]), layer, int(positions[r]), L, hkv, d, 16, dtype)
+    t_qkv, t_kp, t_vp = to_dev(qkv, dtype), to_dev(kp, dtype), to_dev(vp, dtype)
+    say(f"  [gpu] rope_append special values {dtype} pad={pad}")
+    luc.rope_append(t_qkv, to_dev(qb, dtype), t_qkv[:, qd:], to_dev(kb, dtype), t_qkv[:, qd + kd:],
+                    to_dev(vb, dtype), qkv.shape[1], rope.cos, rope.sin,
+                    torch.from_numpy(positions).cuda(), torch.from_numpy(tables).cuda(), t_kp, t_vp,
+                    n, layer, L, hq, hkv, d)
+    torch.cuda.synchronize()
+    # IEEE 754 leaves the sign and payload of a NaN that arithmetic produces
+    # unspecified (x86 and the GPU propagate them differently): NaN must meet
+    # NaN, every other value its exact bits
+    top = 0x7c00 if dtype == "f16" else 0x7f80
+    for name, got, want in (("qkv", from_dev(t_qkv), oq), ("k_pool", from_dev(t_kp), ok_),
+                            ("v_pool", from_dev(t_vp), ov)):
+        gnan, wnan = (got & 0x7fff) > top, (want & 0x7fff) > top
+        bad = np.argwhere((got != want) & ~(gnan & wnan))
+        assert bad.size == 0, (f"{name}: {len(bad)} differ, first at {bad[:4].tolist()}: "
+                               f"got {[hex(v) for v in got[tuple(bad[:4].T)]]} "
+                               f"want {[hex(v) for v in want[tuple(bad[:4].T)]]}")
+
+
 def test_engine_api_decode_loop(orc, luc):
     """The reference's single-sequence loop through the engine mirror: for
     pos in 0..S-1, apply_rope -> KVCache.update -> apply_flash_decoding

@@ -138,12 +138,16 @@ def test_prefill_matches_decode_steps(orc, luc):
 
 def test_prefill_beyond_max_ctx_gives_nan(orc, luc):
     """A sequence whose prompt runs past the host bound max_ctx is flagged
-    with NaN outputs; the others are computed normally."""
+    with NaN outputs; the others are computed normally.  RoPE and the cache
+    write still cover every row the table can hold, flagged or not."""
     cfg = wl.PrefillConfig("over", 2, 0, 14, 2, 64, "bf16", 0, 0, 0.5)
     h = wl.host_prefill_inputs(cfg, seed=5, rows=[50, 20], starts=[0, 100])
     got = gpu_prefill(luc, h, max_ctx=60)  # sequence 1 reaches position 119
     o = orc.to_f32(got["out"], "bf16")
     assert np.all(np.isfinite(o[:50])) and np.all(np.isnan(o[50:]))
+    want = oracle_prefill(orc, luc, h)
+    assert np.array_equal(got["qkv"], want["qkv"]), "RoPE'd q/k differ"
+    assert np.array_equal(got["k_pool"], want["k_pool"]) and np.array_equal(got["v_pool"], want["v_pool"])
 
 
 def test_prefill_long_prompt_beyond_max_ctx_all_flagged(orc, luc):
@@ -156,5 +160,7 @@ def test_prefill_long_prompt_beyond_max_ctx_all_flagged(orc, luc):
     o = orc.to_f32(got["out"], "bf16")
     assert np.all(np.isnan(o[30:]))
     want = oracle_prefill(orc, luc, h)
+    assert np.array_equal(got["qkv"], want["qkv"]), "RoPE'd q/k differ"
+    assert np.array_equal(got["k_pool"], want["k_pool"]) and np.array_equal(got["v_pool"], want["v_pool"])
     err = float(np.max(np.abs(o[:30] - orc.to_f32(want["out"], "bf16")[:30])))
     assert err <= TOL["bf16"]
