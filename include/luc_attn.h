@@ -167,8 +167,7 @@ int luc_decode_step(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qk
  * [Hq][head_dim].  max_ctx is a host-side upper bound of start_pos[b] plus the
  * rows of b; a sequence beyond it gets NaN outputs.  qkv must be 16-byte
  * aligned with a row stride that is a multiple of 8 elements; out 8-byte
- * aligned with a row stride that is a multiple of 4; the RoPE tables and
- * q_bias 16-byte aligned.  Biases may be NULL.  Rows whose position lies outside
+ * aligned with a row stride that is a multiple of 4.  Biases may be NULL.  Rows whose position lies outside
  * the table row (or is negative) are left untouched, as in luc_rope_append.
  * Attention runs on bf16/fp16 MFMA (v_mfma_f32_32x32x16). */
 int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qkv_row_stride,

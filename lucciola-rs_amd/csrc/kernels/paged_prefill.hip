@@ -3,10 +3,9 @@
 // Semantics (the reference's per-token prefill loop, Qwen2Model::forward_layer
 // src/models.rs:485-550): the prompt rows of sequence b are packed rows
 // cu_seqlens[b] .. cu_seqlens[b+1]-1 of qkv, at positions start_pos[b] + i.
-// By the time this kernel runs, every row's k is roped in place and its roped
-// k and v + v_bias are in the cache (the append kernel, launched first on the
-// same stream); q + q_bias is roped here, as it is loaded, and written back in
-// place (bit for bit the append kernel's rotation).  Row i of sequence b and q-head qh then attends to
+// By the time this kernel runs, every row's q and k are roped in place and its
+// roped k and v + v_bias are in the cache (the append kernel, launched first
+// on the same stream).  Row i of sequence b and q-head qh then attends to
 // cache positions 0..start_pos[b] + i through table row b -- the cached prefix
 // and the prompt rows up to itself -- exactly what the reference's
 // flash_decoding call for that token computes (src/kernels/attention.cu:4-176),
@@ -59,7 +58,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 struct PrefillArgs {
-  uint16_t* qkv;  // row r at qkv + r*qkv_stride: [q (Hq*D) | k | v]
+  const uint16_t* qkv;  // row r at qkv + r*qkv_stride: [q (Hq*D) | k | v], q roped
   int64_t qkv_stride;
   const uint16_t* k_pool;  // [blocks][num_layers][Hkv][16][D]
   const uint16_t* v_pool;
@@ -71,12 +70,6 @@ struct PrefillArgs {
   int64_t out_stride;
   int32_t batch, layer, num_layers, hkv, max_ctx, pairs;  // pairs: tile pairs per sequence
   float qk_scale_log2;  // sm_scale * log2(e)
-  // q's RoPE happens here when cos_t is set: q + q_bias rotated at the row's
-  // position, written back in place (16-byte aligned [pos][D/2] tables and
-  // q_bias)
-  const uint16_t* q_bias;
-  const float* cos_t;
-  const float* sin_t;
 };
 
 template <int DT>
@@ -183,36 +176,11 @@ __device__ void prefill_impl(const PrefillArgs& A) {
     // positions outside the host bound: flagged with NaN, never truncated
     // (such a sequence may have more tiles than the grid has pairs: the
     // workgroups of its group stride over all its rows)
-    // q is still roped in place where the cache could hold the position
     if (active)
       for (int r = pair * 32 + (lane & 31); r < nrows; r += A.pairs * 32) {
         uint16_t* const orow = A.out + (int64_t)(row0 + r) * A.out_stride + (int64_t)qh * D;
         for (int d = 0; d < D; d += 8)
           for (int j = 0; j < 4; ++j) orow[d + 4 * g + j] = St<DT>::store(__builtin_nanf(""));
-        const int pos = sp + r;
-        if (A.cos_t && pos >= 0 && pos < A.table_stride * kPage) {
-          uint16_t* const q = A.qkv + (int64_t)(row0 + r) * A.qkv_stride + (int64_t)qh * D;
-          for (int c = g; c < D / 16; c += 2) {  // this lane's half of the 8-dim chunks
-            const int d0 = 8 * c;
-            const int64_t crow = (int64_t)pos * (D / 2) + d0;
-            uint4 x1 = *(const uint4*)(q + d0), x2 = *(const uint4*)(q + d0 + D / 2);
-            uint4 b1 = make_uint4(0, 0, 0, 0), b2 = b1;
-            if (A.q_bias) {
-              uint16_t e1[8], e2[8];
-              for (int e = 0; e < 8; ++e) {
-                e1[e] = A.q_bias[qh * D + d0 + e];
-                e2[e] = A.q_bias[qh * D + d0 + D / 2 + e];
-              }
-              b1 = chunk_pack(e1);
-              b2 = chunk_pack(e2);
-            }
-            rope_rotate8<DT>(x1, x2, b1, b2, A.q_bias != nullptr, *(const float4*)(A.cos_t + crow),
-                             *(const float4*)(A.cos_t + crow + 4), *(const float4*)(A.sin_t + crow),
-                             *(const float4*)(A.sin_t + crow + 4));
-            *(uint4*)(q + d0) = x1;
-            *(uint4*)(q + d0 + D / 2) = x2;
-          }
-        }
       }
     return;
   }
@@ -289,40 +257,14 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   // Q^T fragments (B operand): lane l holds q row my_i, dims (l/32)*8 + 16k .. +8
   // (loaded before the first blocks, so the block waits below can count
   // only block loads)
-  // q, and for its RoPE the cos/sin and bias chunks, are loaded before the
-  // tile's first K/V loads are issued, and rotated after: their latency
-  // overlaps the K/V loads', and the waits the rotation needs count only
-  // the older loads.  The roped q goes back in place at the end of the tile.
+  // Q^T fragments (B operand): lane l holds q row my_i, dims (l/32)*8 + 16k .. +8
+  // (loaded before the tile's first K/V loads are issued, so the block waits
+  // below count only block loads)
   uint4 qf[NK];
-  uint16_t* const qrow = A.qkv + (int64_t)(row0 + min(my_i, nrows - 1)) * A.qkv_stride + (int64_t)qh * D;
+  {
+    const uint16_t* qrow = A.qkv + (int64_t)(row0 + min(my_i, nrows - 1)) * A.qkv_stride + (int64_t)qh * D;
 #pragma unroll
-  for (int k = 0; k < NK; ++k) qf[k] = *(const uint4*)(qrow + g * 8 + 16 * k);
-  // RoPE pairs dims d and d + D/2: chunks k and k + NK/2 of this lane
-  float4 rc[NK / 2][4];
-  uint4 rb[NK / 2][2];
-  if (A.cos_t) {
-    const int64_t crow = (int64_t)(sp + min(my_i, nrows - 1)) * (D / 2);
-#pragma unroll
-    for (int k = 0; k < NK / 2; ++k) {
-      const int d0 = g * 8 + 16 * k;
-      rc[k][0] = *(const float4*)(A.cos_t + crow + d0);
-      rc[k][1] = *(const float4*)(A.cos_t + crow + d0 + 4);
-      rc[k][2] = *(const float4*)(A.sin_t + crow + d0);
-      rc[k][3] = *(const float4*)(A.sin_t + crow + d0 + 4);
-      rb[k][0] = rb[k][1] = make_uint4(0, 0, 0, 0);
-      if (A.q_bias) {
-        rb[k][0] = *(const uint4*)(A.q_bias + qh * D + d0);
-        rb[k][1] = *(const uint4*)(A.q_bias + qh * D + d0 + D / 2);
-      }
-    }
-  }
-  auto rope_q = [&]() __attribute__((always_inline)) {
-    if (A.cos_t) {
-#pragma unroll
-      for (int k = 0; k < NK / 2; ++k)
-        rope_rotate8<DT>(qf[k], qf[k + NK / 2], rb[k][0], rb[k][1], A.q_bias != nullptr, rc[k][0],
-                         rc[k][1], rc[k][2], rc[k][3]);
-    }
+    for (int k = 0; k < NK; ++k) qf[k] = *(const uint4*)(qrow + g * 8 + 16 * k);
     if (neg_scale) {  // S = -(K Q^T) exactly: sign flips commute with rounding
 #pragma unroll
       for (int k = 0; k < NK; ++k) {
@@ -330,7 +272,9 @@ __device__ void prefill_impl(const PrefillArgs& A) {
         qf[k].z ^= 0x80008000u; qf[k].w ^= 0x80008000u;
       }
     }
-  };
+#pragma unroll
+    for (int k = 0; k < NK; ++k) asm volatile("" ::"v"(qf[k].x), "v"(qf[k].y), "v"(qf[k].z), "v"(qf[k].w));
+  }
   // s_waitcnt vmcnt(n * LPW): all but this wave's loads of the n most recently
   // issued super-blocks have landed (loads complete in order)
   auto wait_blocks = [&](int n) __attribute__((always_inline)) {
@@ -479,7 +423,6 @@ __device__ void prefill_impl(const PrefillArgs& A) {
       issue(j, j, pgn);
     }
   if (NS - 1 < nsb) load_pages(NS - 1, pgn);
-  rope_q();
   wait_blocks(min(NS - 2, nsb - 1));
   __builtin_amdgcn_s_barrier();
   f32x16 sa[2], sb[2];
@@ -489,16 +432,8 @@ __device__ void prefill_impl(const PrefillArgs& A) {
     if (blk + 1 < nblk) step(blk + 1, sb, sa);
   }
 
-  // ---- the roped q back in place; normalise and store: lane holds dims
-  // 32db + 8i + 4g + j of row my_i ----
+  // ---- normalise and store: lane holds dims 32db + 8i + 4g + j of row my_i ----
   if (!active) continue;
-  if (A.cos_t && row_ok) {
-    const uint32_t flip = neg_scale ? 0x80008000u : 0u;
-#pragma unroll
-    for (int k = 0; k < NK; ++k)
-      *(uint4*)(qrow + g * 8 + 16 * k) =
-          make_uint4(qf[k].x ^ flip, qf[k].y ^ flip, qf[k].z ^ flip, qf[k].w ^ flip);
-  }
   if (row_ok) {
     const float inv = 1.0f / osum[0];
 #pragma unroll

@@ -340,9 +340,6 @@ struct PrefillArgs {
   int64_t out_stride;
   int32_t batch, layer, num_layers, hkv, max_ctx, pairs;
   float qk_scale_log2;
-  const void* q_bias;
-  const float* cos_t;
-  const float* sin_t;
 };
 
 int launch_decode(DecodeLaunch& L, void* stream) {
@@ -589,8 +586,6 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
     return fail(LUC_E_INVALID, "qkv must be 16-byte aligned with a row stride that is a multiple of 8");
   if (!aligned(out, 8) || out_row_stride % 4)
     return fail(LUC_E_INVALID, "out must be 8-byte aligned with a row stride that is a multiple of 4");
-  if (!aligned(cos_table, 16) || !aligned(sin_table, 16) || !aligned(q_bias, 16))
-    return fail(LUC_E_INVALID, "RoPE tables and q_bias must be 16-byte aligned");
   if ((int64_t)table_stride * LUC_BLOCK_SIZE < max_ctx)
     return fail(LUC_E_INVALID, "table_stride %d pages cannot hold max_ctx %d", table_stride, max_ctx);
   if (batch == 0 || total_rows == 0) return LUC_OK;
@@ -610,9 +605,8 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
   const int64_t grid = (int64_t)batch * num_kv_heads * ceil_div(group, waves) * pairs;
   if (grid > INT32_MAX) return fail(LUC_E_INVALID, "batch x kv heads x row tiles too large");
 
-  // 1) bias + RoPE of every prompt row's k in place, cache write of the roped
-  //    k and v + v_bias (models.rs:505-534 for each row; q's RoPE is the
-  //    attention kernel's, as it loads q)
+  // 1) bias + RoPE of every prompt row's q and k in place, cache write of the
+  //    roped k and v + v_bias (models.rs:505-534 for each row)
   uint16_t* base = static_cast<uint16_t*>(qkv);
   AppendArgs a;
   a.q = base; a.q_bias = q_bias; a.k = base + (int64_t)num_q_heads * head_dim; a.k_bias = k_bias;
@@ -621,18 +615,16 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
   a.cu_seqlens = cu_seqlens; a.start_pos = start_pos; a.batch = batch;
   a.tables = block_tables; a.table_stride = table_stride; a.k_pool = k_pool; a.v_pool = v_pool;
   a.layer = layer; a.num_layers = num_layers; a.hq = num_q_heads; a.hkv = num_kv_heads;
-  a.head_dim = head_dim; a.flags = kRopeK | kWriteKV;  // q: roped by the attention kernel
+  a.head_dim = head_dim; a.flags = kRopeQ | kRopeK | kWriteKV;
   if (int rc = launch_append(ctx, stream, dtype, total_rows, a)) return rc;
 
-  // 2) RoPE of q (written back in place) and causal attention of every row
-  //    over the cache (models.rs:536-549 per row)
+  // 2) causal attention of every row over the cache (models.rs:536-549 per row)
   PrefillArgs p{};
   p.qkv = qkv; p.qkv_stride = qkv_row_stride; p.k_pool = k_pool; p.v_pool = v_pool;
   p.tables = block_tables; p.table_stride = table_stride; p.cu_seqlens = cu_seqlens;
   p.start_pos = start_pos; p.out = out; p.out_stride = out_row_stride; p.batch = batch;
   p.layer = layer; p.num_layers = num_layers; p.hkv = num_kv_heads; p.max_ctx = max_ctx;
   p.pairs = pairs; p.qk_scale_log2 = sm_scale * 1.4426950408889634f;
-  p.q_bias = q_bias; p.cos_t = cos_table; p.sin_t = sin_table;
   void* args[] = {&p};
   return launch(fn, dim3((unsigned)grid), dim3(64 * waves), stream, args);
 }
