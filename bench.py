@@ -23,7 +23,13 @@ Also reported:
                 `traffic` is the HBM bytes per launch read from the committed
                 rocprofv3 PMC summary, if present;
   cpu_baseline  the oracle (C restatement of the reference's attention, OpenMP)
-                on one full layer step of the same workload on the host.
+                on one full layer step of the same workload on the host;
+  prefill       luc_paged_prefill on prefill_4x2048 (4 prompts x 2048 rows from
+                an empty cache, 14q/2kv, d=64, bf16): RoPE + cache append
+                kernel, then the causal attention kernel on bf16 MFMA; time per
+                call (HIP events over a graph of back-to-back calls) and the
+                attention's algorithmic FLOP rate against the 2.5 PFLOP/s dense
+                bf16 peak.
 """
 from __future__ import annotations
 
@@ -38,6 +44,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_batch32_mixed_traffic.json")
 
 
@@ -52,6 +59,7 @@ def parse():
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--eager", action="store_true", help="launch eagerly instead of a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (reference for PMC byte counters)")
     return ap.parse_args()
@@ -82,6 +90,59 @@ def cpu_baseline(cfg, seed, budget_s=10.0):
         times.append(run())
     t = statistics.median(times)
     return dict(t=t, threads=threads, reps=len(times), ctx=h.ctx)
+
+
+def prefill_bench(lib, torch, reps=50):
+    """Microseconds per luc_paged_prefill call on prefill_4x2048, replayed from
+    a HIP graph, and the attention's algorithmic FLOPs."""
+    import numpy as np
+    from lucciola_rs_amd import workloads as wl
+    from lucciola_rs_amd.engine import RopeCache, sm_scale
+
+    cfg = wl.PREFILL_CONFIGS["prefill_4x2048"]
+    h = wl.host_prefill_inputs(cfg, seed=1, poison=False)
+    dev = torch.device("cuda:0")
+    to = lambda x: wl.bits_to_tensor(np.ascontiguousarray(x), cfg.dtype).to(dev)
+    qkv, kp, vp = to(h.qkv), to(h.k_pool), to(h.v_pool)
+    tables = torch.from_numpy(h.tables).to(dev)
+    cu = torch.from_numpy(h.cu_seqlens).to(dev)
+    sp = torch.from_numpy(h.start_pos).to(dev)
+    rope = RopeCache(4096, cfg.head_dim, 1e6, lib=lib, device=dev)
+    total = int(h.cu_seqlens[-1])
+    out = torch.empty((total, cfg.hq * cfg.head_dim), dtype=cfg.torch_dtype, device=dev)
+
+    def call():
+        # q/k are roped in place on every call: the same work each time
+        lib.paged_prefill(qkv, None, None, None, rope.cos, rope.sin, kp, vp, tables, cu, sp, total,
+                          h.max_ctx, 0, 1, cfg.hq, cfg.hkv, cfg.head_dim, sm_scale(cfg.head_dim), out)
+
+    for _ in range(5):
+        call()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            call()
+    g.replay()
+    torch.cuda.synchronize()
+    runs = []
+    for _ in range(5):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        runs.append(e0.elapsed_time(e1) * 1e3 / reps)
+    us = statistics.median(runs)
+    flops = wl.prefill_flops(cfg, np.diff(h.cu_seqlens), h.start_pos)
+    tflops = flops / (us * 1e-6) / 1e12
+    return {"workload": cfg.name, "batch": cfg.batch, "rows": cfg.rows, "q_heads": cfg.hq,
+            "kv_heads": cfg.hkv, "head_dim": cfg.head_dim, "dtype": cfg.dtype,
+            "call": "luc_paged_prefill (RoPE + append kernel, causal attention kernel)",
+            "us_per_call": round(us, 2), "attention_flops": int(flops),
+            "achieved_tflops": round(tflops, 1), "peak_tflops": PEAK_BF16_TFLOPS,
+            "frac": round(tflops / PEAK_BF16_TFLOPS, 4)}
 
 
 def main():
@@ -180,6 +241,8 @@ def main():
         if tr.get("workload") == args.workload and tr.get("split_tokens", 0) == args.split_tokens:
             traffic = tr.get("hbm_bytes_per_launch")
 
+    prefill = None if args.no_prefill else prefill_bench(lib, torch)
+
     cpu = None
     if not args.no_cpu_baseline:
         cb = cpu_baseline(cfg, args.seed)
@@ -219,6 +282,7 @@ def main():
                      "us_per_launch": round(dec_ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": int(dec_bytes)},
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     print(json.dumps(res), flush=True)
 

@@ -18,18 +18,21 @@
 // combine kernel.
 //
 // Decode kernel work decomposition:
-//   Workgroup = one wave = (split, sequence b, kv head h), split-major, so the
+//   Workgroup = 4 waves = (split, sequence b, kv head h), split-major, so the
 //   splits every sequence has are dispatched first and the workgroups of
 //   splits past a context exit at once.  The G = Hq/Hkv q-heads of kv head h
 //   are processed together, so each KV page is read from HBM once per kv
-//   head (GQA).
-//   Prologue: positions[b], the split's block-table entries and q are loaded
-//   together (one memory round trip before the KV stream).  q stays in 2G
-//   registers, spread so that DPP row_newbcast hands every lane the q word it
-//   needs as an operand of v_dot2c (no LDS traffic for q).
-//   The wave walks its split in 8 KB tiles of K (64 tokens at head_dim 64, 32
-//   at 128), in pairs: both tiles of a pair are issued, tile i is computed
-//   while tile i+1 lands.  Per tile:
+//   head (GQA).  Wave w takes tiles w, w + 4, ... of the split: 8 KB tiles of
+//   K (64 tokens at head_dim 64, 32 at 128).  The _t1 kernels give each wave
+//   one tile (a split of 4 tiles); the _t2 kernels walk two tiles at a time,
+//   tile i computed while tile i+1 lands.
+//   Prologue: the wave's block-table entries come through the scalar cache;
+//   in the single-tile kernels q (or, in the step variant, q, k, v, their
+//   biases and the cos/sin rows) arrive by direct-to-LDS loads issued between
+//   the tile's K and V loads, so no vector-memory round trip precedes the KV
+//   stream.  q is then held in 2G registers, spread so that DPP row_newbcast
+//   hands every lane the q word it needs as an operand of v_dot2c.
+//   Per tile:
 //     1. K goes straight from HBM into LDS (global_load_lds_dwordx4; one
 //        wave-wide load = 1 KB of a page), each token row XOR-swizzled by
 //        16-byte chunk so the per-token LDS reads are conflict-free; V goes
@@ -38,13 +41,15 @@
 //        soon as K has landed.
 //     2. Scores: lane = token (x2 lanes per token at head_dim 128), all G
 //        heads with v_dot2c_f32_{f16,bf16}, q by DPP broadcast.
-//     3. Online softmax in the exp2 domain, wave max by a DPP reduction; o is
-//        rescaled only when the running max moves.
+//     3. Online softmax in the exp2 domain with a lazy reference point: the
+//        running max moves (wave max by a DPP reduction, rescale of o) only
+//        when a score passes it by more than kLazyMax.
 //     4. o += p * V with V in its load layout.  fp16: p of tokens t and
 //        t + TILE/2 packed as an fp16 pair, V of the same two tokens paired by
 //        v_perm, one v_dot2_f32_f16 per (head, dim).  bf16: f32 FMA.
-//   The wave's token groups are reduced with permlane swaps (reduce-scatter).
-//   A sequence with one split writes its output; otherwise each split writes
+//   Each wave's token groups are reduced with permlane swaps
+//   (reduce-scatter); the 4 waves merge their (m, l, o) through LDS.  A
+//   sequence with one split writes its output; otherwise each split writes
 //   (m, l, o) to the workspace.
 // Combine kernel: one workgroup per (sequence, kv head) merges the splits
 // with the log-sum-exp rule.  The step variant also writes the roped q and k
