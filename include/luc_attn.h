@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define LUC_ABI_VERSION 1
+#define LUC_ABI_VERSION 2
 #define LUC_BLOCK_SIZE 16
 
 typedef struct luc_ctx luc_ctx;
@@ -107,9 +107,10 @@ int luc_rope_append(luc_ctx* ctx, void* stream, int dtype, void* q, const void* 
  * sizes (0 when every sequence fits one split; the workspace may then be
  * NULL).  split_tokens: tokens per split-K chunk, rounded up to a multiple of
  * 64 (head_dim 64) or 32 (head_dim 128); 0 = the library's choice.
- * The workspace must be 256-byte aligned; its contents need no
- * initialisation.  Launches that may run concurrently (different streams)
- * need separate workspaces. */
+ * The workspace must be 256-byte aligned and zero-filled once before its
+ * first use; every launch leaves it ready for the next (its split arrival
+ * counters return to zero).  Launches that may run concurrently (different
+ * streams) need separate workspaces. */
 size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                        int head_dim, int max_ctx, int split_tokens);
 
@@ -123,8 +124,9 @@ size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_he
  * whose context exceeds it, or is empty, gets NaN outputs, as the reference
  * yields NaN for an empty context.  sm_scale is 1/sqrt(head_dim) in the
  * engine (kernels.rs:264).  Work is split into split-K chunks whose partials
- * go to `workspace` (see luc_paged_decode_workspace_size) and are merged by a
- * log-sum-exp combine launch on the same stream. */
+ * go to `workspace` (see luc_paged_decode_workspace_size); the last chunk of a
+ * sequence to finish merges them with the log-sum-exp rule, in the same
+ * launch. */
 int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t out_row_stride,
                      const void* q, int64_t q_row_stride, const void* k_pool, const void* v_pool,
                      const int32_t* block_tables, int table_stride, const int32_t* positions,

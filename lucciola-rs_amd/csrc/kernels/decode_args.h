@@ -24,6 +24,7 @@ struct luc_decode_args {
   int32_t max_ctx, split_tokens, max_splits;
   float* ws_ml;             // [batch*Hkv][max_splits][G][2]  (max, sum) per split
   float* ws_o;              // [batch*Hkv][max_splits][G*head_dim]
+  int32_t* ws_cnt;          // [batch*Hkv] split arrivals, zero between launches
   uint16_t* out;            // row b at out + b*out_stride, [Hq*head_dim]
   int64_t out_stride;
 };

@@ -14,8 +14,11 @@
 // v + v_bias (src/kernels/kv_cache.cu).  Attention takes the new token's K/V
 // from LDS, so it does not depend on the order of the cache write.
 //
-// Two launches per step: the split-K decode kernel, then the log-sum-exp
-// combine kernel.
+// One launch per step.  A sequence's splits write (m, l, o) partials; the
+// last workgroup of a (sequence, kv head) to finish -- an arrival counter in
+// the workspace -- merges them with the log-sum-exp rule and writes the
+// output (the partials and the counter by agent-scope accesses, coherent
+// across XCDs).
 //
 // Decode kernel work decomposition:
 //   Workgroup = 4 waves = (split, sequence b, kv head h), split-major, so the
@@ -50,10 +53,9 @@
 //   Each wave's token groups are reduced with permlane swaps
 //   (reduce-scatter); the 4 waves merge their (m, l, o) through LDS.  A
 //   sequence with one split writes its output; otherwise each split writes
-//   (m, l, o) to the workspace.
-// Combine kernel: one workgroup per (sequence, kv head) merges the splits
-// with the log-sum-exp rule.  The step variant also writes the roped q and k
-// of the new token back in place (after every split has read them).
+//   (m, l, o) to the workspace and the last split to arrive merges them.
+//   The step variant's last workgroup also writes the roped q and k of the
+//   new token back in place (after every split has read them).
 #include "decode_args.h"
 #include "luc_common.h"
 
@@ -299,6 +301,126 @@ __device__ __attribute__((always_inline)) inline float pick(const float (&x)[N],
   return r;
 }
 
+// Split partials cross workgroups that may run on different XCDs, whose L2
+// caches are not coherent with each other within a launch: they are written
+// and read by agent-scope relaxed atomic accesses (global_store/load with the
+// sc1 scope bit), which are coherent per access, instead of whole-cache
+// write-back/invalidate fences.  A writer waits for its stores to complete
+// before it counts its arrival; the merging split reads after it has seen the
+// count.
+__device__ inline void ws_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float ws_load(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Log-sum-exp merge of the nsplit partials of one (sequence, kv head) by the
+// NT threads of a workgroup -- the reference's partition merge
+// (attention.cu:140-174) over splits: M = max m_s, L = sum l_s 2^(m_s - M),
+// O = sum o_s 2^(m_s - M) / L.  s_w (G x 256 floats) and s_L (G floats) are
+// LDS scratch.
+template <int DT, int D, int G, int NT>
+__device__ void lse_merge(const DecodeArgs& A, int bh, int nsplit, uint16_t* out_row, float* s_w,
+                          float* s_L) {
+  constexpr int GD = G * D;
+  constexpr int NE = (GD + NT - 1) / NT;  // output elements per thread
+  constexpr int SB = 16;                  // splits per batch of o loads
+  constexpr int GW = (G + NT / 64 - 1) / (NT / 64);  // heads per wave
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const float* ml = A.ws_ml + (int64_t)bh * A.max_splits * G * 2;
+  const float* po = A.ws_o + (int64_t)bh * A.max_splits * GD;
+  // o of the first SB splits and (m, l) of every split go out together
+  // (wave w reads heads w, w + NT/64, ...)
+  float ob[SB][NE];
+  auto load_batch = [&](int s0) {
+#pragma unroll
+    for (int j = 0; j < SB; ++j)
+#pragma unroll
+      for (int c = 0; c < NE; ++c) {
+        const int e = min((int)threadIdx.x + NT * c, GD - 1);
+        ob[j][c] = ws_load(po + (int64_t)min(s0 + j, nsplit - 1) * GD + e);
+      }
+  };
+  float mv[GW][4], lv[GW][4];
+  load_batch(0);
+#pragma unroll
+  for (int gi = 0; gi < GW; ++gi) {
+    const int g = min(w + (NT / 64) * gi, G - 1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int s = lane + 64 * k;
+      mv[gi][k] = s < nsplit ? ws_load(ml + ((int64_t)s * G + g) * 2) : -INFINITY;
+      lv[gi][k] = s < nsplit ? ws_load(ml + ((int64_t)s * G + g) * 2 + 1) : 0.0f;
+    }
+  }
+  // weights of the splits: 2^(m_s - M), and L = sum l_s 2^(m_s - M)
+#pragma unroll
+  for (int gi = 0; gi < GW; ++gi) {
+    const int g = w + (NT / 64) * gi;
+    if (g < G) {
+      const float M =
+          wave_max(fmaxf(fmaxf(mv[gi][0], mv[gi][1]), fmaxf(mv[gi][2], mv[gi][3])));
+      float L = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float wgt = __builtin_amdgcn_exp2f(mv[gi][k] - M);  // 0 past nsplit
+        s_w[g * 256 + lane + 64 * k] = wgt;
+        L = fmaf(wgt, lv[gi][k], L);
+      }
+      L = wave_sum(L);
+      if (lane == 0) s_L[g] = L;
+    }
+  }
+  __syncthreads();
+  float acc[NE];
+#pragma unroll
+  for (int c = 0; c < NE; ++c) acc[c] = 0.0f;
+  for (int s0 = 0; s0 < nsplit; s0 += SB) {
+    if (s0 > 0) load_batch(s0);
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      if (s0 + j < nsplit) {
+#pragma unroll
+        for (int c = 0; c < NE; ++c) {
+          const int e = min((int)threadIdx.x + NT * c, GD - 1);
+          acc[c] = fmaf(s_w[(e / D) * 256 + s0 + j], ob[j][c], acc[c]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < NE; ++c) {
+    const int e = threadIdx.x + NT * c;
+    if (e < GD) out_row[e] = St<DT>::store(acc[c] / s_L[e / D]);
+  }
+}
+
+// The step variant's roped q (G heads) and k of the new token, written back
+// into the qkv row by the NT threads of the workgroup that finishes (b, h)
+// last, after every split has read them: the same rotation as the kernel's
+// own, recomputed from the untouched row.
+template <int DT, int D, int G, int NT>
+__device__ void qk_writeback(const DecodeArgs& A, int b, int h, int pos) {
+  constexpr int HD = D / 2;
+  constexpr int GD = G * D;
+  const float* crow = A.cos_t + (int64_t)pos * HD;
+  const float* srow = A.sin_t + (int64_t)pos * HD;
+  uint16_t* qrow = A.q + (int64_t)b * A.q_stride + (int64_t)h * GD;
+  uint16_t* krow = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
+  for (int idx = threadIdx.x; idx < (G + 1) * HD; idx += NT) {
+    const int g = idx / HD, j = idx % HD;
+    uint16_t* x = g < G ? qrow + g * D : krow;
+    const uint16_t* bias = g < G ? (A.q_bias ? A.q_bias + ((int64_t)h * G + g) * D : nullptr)
+                                 : (A.k_bias ? A.k_bias + (int64_t)h * D : nullptr);
+    uint16_t o1, o2;
+    rot_pair<DT>(x[j], bias ? bias[j] : 0, x[j + HD], bias ? bias[j + HD] : 0, crow[j], srow[j],
+                 o1, o2);
+    x[j] = o1;
+    x[j + HD] = o2;
+  }
+}
+
 template <int DT, int D, int G, bool APPEND, int W, int NB>
 __device__ void decode_impl(const DecodeArgs& A) {
   using S = DecodeGeo<D>;
@@ -344,6 +466,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   __shared__ __attribute__((aligned(16))) uint16_t s_vnew[APPEND ? W : 1][APPEND ? D : 8];
   __shared__ __attribute__((aligned(16))) char s_qr[FASTQ ? W : 1][FASTQ ? NQ * 256 : 16];
   __shared__ __attribute__((aligned(16))) char s_pa[FASTA ? W : 1][FASTA ? PBYTES : 16];
+  static_assert((G * 256 + G) * 4 <= W * NB * S::KBYTES, "merge weights fit the K buffers");
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave of the workgroup
@@ -931,125 +1054,41 @@ __device__ void decode_impl(const DecodeArgs& A) {
     if (nsplit == 1) {
       out_row[e] = St<DT>::store(O / L);
     } else {
-      A.ws_o[rec * GD + e] = O;
+      // partials by agent-scope stores (coherent across the XCDs' L2s), read
+      // back the same way by the split that merges
+      ws_store(A.ws_o + rec * GD + e, O);
       if (e % D == 0) {
-        A.ws_ml[(rec * G + g) * 2] = M;
-        A.ws_ml[(rec * G + g) * 2 + 1] = L;
+        ws_store(A.ws_ml + (rec * G + g) * 2, M);
+        ws_store(A.ws_ml + (rec * G + g) * 2 + 1, L);
       }
     }
   }
-}
 
-// Log-sum-exp merge of the splits of one (sequence, kv head) -- the
-// reference's partition merge (attention.cu:140-174) over splits:
-// M = max m_s, L = sum l_s 2^(m_s - M), O = sum o_s 2^(m_s - M) / L.  The step
-// variant also writes the roped q (G heads) and k of the new token back into
-// the qkv row, after every split of the decode launch has read them.
-template <int DT, int D, int G, bool APPEND>
-__device__ void combine_impl(const DecodeArgs& A) {
-  constexpr int NT = 256;
-  constexpr int HD = D / 2;
-  constexpr int GD = G * D;
-  constexpr int NE = (GD + NT - 1) / NT;  // output elements per thread
-  constexpr int SB = 16;                  // splits per batch of o loads
-  __shared__ float s_w[G][256];           // split weights
-  __shared__ float s_L[G];
-  const int bh = blockIdx.x;
-  const int b = bh / A.hkv, h = bh - b * A.hkv;
-  const int pos = A.positions[b];
-  const int ctx = pos + 1;
-  if (ctx < 1 || ctx > A.max_ctx) return;  // the decode kernel wrote NaN
-  const int nsplit = (ctx + A.split_tokens - 1) / A.split_tokens;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  // The partials go out first: o of the first SB splits and (m, l) of every
-  // split (wave w reads heads w, w + 4, ...), so that their round trip
-  // overlaps the step variant's q/k write-back below.
-  constexpr int GW = (G + NT / 64 - 1) / (NT / 64);  // heads per wave
-  const float* ml = A.ws_ml + (int64_t)bh * A.max_splits * G * 2;
-  const float* po = A.ws_o + (int64_t)bh * A.max_splits * GD;
-  float ob[SB][NE];
-  auto load_batch = [&](int s0) {
-#pragma unroll
-    for (int j = 0; j < SB; ++j)
-#pragma unroll
-      for (int c = 0; c < NE; ++c) {
-        const int e = min((int)threadIdx.x + NT * c, GD - 1);
-        ob[j][c] = po[(int64_t)min(s0 + j, nsplit - 1) * GD + e];
-      }
-  };
-  float mv[GW][4], lv[GW][4];
+  // ---- the last split of (b, h) to finish merges the partials ----
   if (nsplit > 1) {
-    load_batch(0);
-#pragma unroll
-    for (int gi = 0; gi < GW; ++gi) {
-      const int g = min(w + (NT / 64) * gi, G - 1);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int s = lane + 64 * k;
-        mv[gi][k] = s < nsplit ? ml[((int64_t)s * G + g) * 2] : -INFINITY;
-        lv[gi][k] = s < nsplit ? ml[((int64_t)s * G + g) * 2 + 1] : 0.0f;
-      }
+    // this wave's partial stores have completed (at agent scope) before the
+    // workgroup's arrival is counted
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    // whether this workgroup is the last split of (b, h) to finish, passed
+    // through the p exchange buffer (unused from here on)
+    uint32_t* const s_last = &s_p[0][0];
+    if (threadIdx.x == 0) {
+      const int old = __hip_atomic_fetch_add(A.ws_cnt + bh, 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+      *s_last = old == nsplit - 1;
+      // the counter goes back to zero for the next launch
+      if (old == nsplit - 1)
+        __hip_atomic_store(A.ws_cnt + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    __syncthreads();
+    if (!*s_last) return;
+    // every other split's partial is complete: the agent-scope loads of
+    // lse_merge see them
+    float* const s_w = (float*)&s_k[0][0][0];  // the records were read above
+    lse_merge<DT, D, G, 64 * W>(A, bh, nsplit, out_row, s_w, s_w + G * 256);
   }
-  if constexpr (APPEND) {
-    const float* crow = A.cos_t + (int64_t)pos * HD;
-    const float* srow = A.sin_t + (int64_t)pos * HD;
-    uint16_t* qrow = A.q + (int64_t)b * A.q_stride + (int64_t)h * GD;
-    uint16_t* krow = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
-    for (int idx = threadIdx.x; idx < (G + 1) * HD; idx += NT) {
-      const int g = idx / HD, j = idx % HD;
-      uint16_t* x = g < G ? qrow + g * D : krow;
-      const uint16_t* bias = g < G ? (A.q_bias ? A.q_bias + ((int64_t)h * G + g) * D : nullptr)
-                                   : (A.k_bias ? A.k_bias + (int64_t)h * D : nullptr);
-      uint16_t o1, o2;
-      rot_pair<DT>(x[j], bias ? bias[j] : 0, x[j + HD], bias ? bias[j + HD] : 0, crow[j], srow[j],
-                   o1, o2);
-      x[j] = o1;
-      x[j + HD] = o2;
-    }
-  }
-  if (nsplit <= 1) return;  // the decode kernel wrote the output
-  // weights of the splits: 2^(m_s - M), and L = sum l_s 2^(m_s - M)
-#pragma unroll
-  for (int gi = 0; gi < GW; ++gi) {
-    const int g = w + (NT / 64) * gi;
-    if (g < G) {
-      const float M =
-          wave_max(fmaxf(fmaxf(mv[gi][0], mv[gi][1]), fmaxf(mv[gi][2], mv[gi][3])));
-      float L = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float wgt = __builtin_amdgcn_exp2f(mv[gi][k] - M);  // 0 past nsplit
-        s_w[g][lane + 64 * k] = wgt;
-        L = fmaf(wgt, lv[gi][k], L);
-      }
-      L = wave_sum(L);
-      if (lane == 0) s_L[g] = L;
-    }
-  }
-  __syncthreads();
-  float acc[NE];
-#pragma unroll
-  for (int c = 0; c < NE; ++c) acc[c] = 0.0f;
-  for (int s0 = 0; s0 < nsplit; s0 += SB) {
-    if (s0 > 0) load_batch(s0);
-#pragma unroll
-    for (int j = 0; j < SB; ++j) {
-      if (s0 + j < nsplit) {
-#pragma unroll
-        for (int c = 0; c < NE; ++c) {
-          const int e = min((int)threadIdx.x + NT * c, GD - 1);
-          acc[c] = fmaf(s_w[e / D][s0 + j], ob[j][c], acc[c]);
-        }
-      }
-    }
-  }
-  uint16_t* out_row = A.out + (int64_t)b * A.out_stride + (int64_t)h * GD;
-#pragma unroll
-  for (int c = 0; c < NE; ++c) {
-    const int e = threadIdx.x + NT * c;
-    if (e < GD) out_row[e] = St<DT>::store(acc[c] / s_L[e / D]);
-  }
+  if constexpr (APPEND) qk_writeback<DT, D, G, 64 * W>(A, b, h, pos);
 }
 
 }  // namespace luc
@@ -1070,15 +1109,7 @@ __device__ void combine_impl(const DecodeArgs& A) {
 
 #define LUC_DECODE(DTN, DT, D, G)                                                                  \
   LUC_DECODE_KERNELS(DTN, DT, D, G, 1, 2)                                                          \
-  LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2)                                                          \
-  extern "C" __global__ __launch_bounds__(256) void luc_decode_combine_##DTN##_d##D##_g##G(        \
-      luc::DecodeArgs a) {                                                                         \
-    luc::combine_impl<DT, D, G, false>(a);                                                         \
-  }                                                                                                \
-  extern "C" __global__ __launch_bounds__(256) void luc_decode_step_combine_##DTN##_d##D##_g##G(   \
-      luc::DecodeArgs a) {                                                                         \
-    luc::combine_impl<DT, D, G, true>(a);                                                          \
-  }
+  LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2)
 
 #define LUC_DECODE_GROUPS(DTN, DT, D)                                                              \
   LUC_DECODE(DTN, DT, D, 1)                                                                        \

@@ -226,24 +226,26 @@ int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requeste
 // Workspace layout (each section 256-byte aligned):
 //   [(max, sum) per (b, kv head, split, head of the group): f32 x2]
 //   [o per (b, kv head, split): f32 x group x head_dim]
+//   [split arrivals per (b, kv head): int32, zero between launches]
 int64_t align256(int64_t n) { return ceil_div(n, 256) * 256; }
 int64_t ml_bytes(int batch, int hq, int max_splits) {
   return align256((int64_t)batch * hq * max_splits * 2 * 4);
 }
+int64_t o_bytes(int batch, int hq, int head_dim, int max_splits) {
+  return align256((int64_t)batch * hq * max_splits * head_dim * 4);
+}
 
-size_t workspace_bytes_for(int batch, int hq, int head_dim, int max_ctx, int split_tokens) {
+size_t workspace_bytes_for(int batch, int hq, int hkv, int head_dim, int max_ctx, int split_tokens) {
   const int64_t max_splits = ceil_div(max_ctx, split_tokens);
   if (max_splits <= 1) return 0;
   return (size_t)(ml_bytes(batch, hq, (int)max_splits) +
-                  (int64_t)batch * hq * max_splits * head_dim * 4);
+                  o_bytes(batch, hq, head_dim, (int)max_splits) + align256((int64_t)batch * hkv * 4));
 }
 
 struct DecodeLaunch {
   luc_decode_args a{};
-  hipFunction_t fn = nullptr;       // split-K decode
-  hipFunction_t combine = nullptr;  // log-sum-exp merge (+ q/k write-back for the step)
+  hipFunction_t fn = nullptr;  // split-K decode with the merge in its last split
   dim3 grid;
-  bool need_combine = false;
 };
 
 // Shared argument checks and argument block of the two decode entry points.
@@ -275,7 +277,7 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
     return fail(LUC_E_UNSUPPORTED, "max_ctx %d exceeds %d splits of %d tokens", max_ctx,
                 kMaxSplits, kMaxSplitTokens);
   const int max_splits = (int)ceil_div(max_ctx, st);
-  const size_t need = workspace_bytes_for(batch, num_q_heads, head_dim, max_ctx, st);
+  const size_t need = workspace_bytes_for(batch, num_q_heads, num_kv_heads, head_dim, max_ctx, st);
   if (need && (!workspace || workspace_bytes < need))
     return fail(LUC_E_WORKSPACE, "workspace %zu bytes, %zu needed", workspace_bytes, need);
   if (need && !aligned(workspace, 256)) return fail(LUC_E_INVALID, "workspace must be 256-byte aligned");
@@ -294,11 +296,7 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
                                (one_tile ? "_t1" : "_t2"),
                       &L->fn))
     return rc;
-  if (int rc = get_fn(ctx, std::string(step ? "luc_decode_step_combine_" : "luc_decode_combine_") +
-                               suffix, &L->combine))
-    return rc;
   L->grid = dim3((unsigned)grid);
-  L->need_combine = step || max_splits > 1;
   luc_decode_args& a = L->a;
   a.q = static_cast<uint16_t*>(const_cast<void*>(q));
   a.q_stride = q_row_stride;
@@ -319,6 +317,8 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
     char* ws = static_cast<char*>(workspace);
     a.ws_ml = reinterpret_cast<float*>(ws);
     a.ws_o = reinterpret_cast<float*>(ws + ml_bytes(batch, num_q_heads, max_splits));
+    a.ws_cnt = reinterpret_cast<int32_t*>(ws + ml_bytes(batch, num_q_heads, max_splits) +
+                                          o_bytes(batch, num_q_heads, head_dim, max_splits));
   }
   a.out = static_cast<uint16_t*>(out);
   a.out_stride = out_row_stride;
@@ -344,9 +344,7 @@ struct PrefillArgs {
 
 int launch_decode(DecodeLaunch& L, void* stream) {
   void* args[] = {&L.a};
-  if (int rc = launch(L.fn, L.grid, dim3(kDecodeWaves * 64), stream, args)) return rc;
-  if (!L.need_combine) return LUC_OK;
-  return launch(L.combine, dim3(L.a.batch * L.a.hkv), dim3(256), stream, args);
+  return launch(L.fn, L.grid, dim3(kDecodeWaves * 64), stream, args);
 }
 
 }  // namespace
@@ -388,16 +386,11 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
                         std::to_string(g));
     for (int d : {64, 128})
       for (int g = 1; g <= 8; ++g)
-        for (const char* kind : {"luc_decode_", "luc_decode_step_", "luc_decode_combine_",
-                                 "luc_decode_step_combine_"}) {
+        for (const char* kind : {"luc_decode_", "luc_decode_step_"}) {
           const std::string n = std::string(kind) + dt + "_d" + std::to_string(d) + "_g" +
                                 std::to_string(g);
-          if (std::string(kind).find("combine") != std::string::npos) {
-            names.push_back(n);
-          } else {
-            names.push_back(n + "_t1");
-            names.push_back(n + "_t2");
-          }
+          names.push_back(n + "_t1");
+          names.push_back(n + "_t2");
         }
   }
   for (const auto& n : names) {
@@ -515,7 +508,7 @@ size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_he
   if (head_dim != 64 && head_dim != 128) return 0;
   const int st = split_tokens_for(batch, num_kv_heads, head_dim, max_ctx, split_tokens);
   if (st == 0) return 0;
-  return workspace_bytes_for(batch, num_q_heads, head_dim, max_ctx, st);
+  return workspace_bytes_for(batch, num_q_heads, num_kv_heads, head_dim, max_ctx, st);
 }
 
 int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t out_row_stride,
