@@ -7,16 +7,16 @@ peak) at B=32, one MI355X.
 Workload (default `batch32_mixed`): B=32 sequences, Qwen2.5-0.5B heads
 (14 q / 2 kv, head_dim 64), fp16, contexts U{128..4096} (seeded), page size 16,
 16384-page pool handed out by a seeded shuffle, 24 layers.  A step is one
-layer's decode step for the whole batch (luc_decode_step): RoPE(q, k) + paged
-append of one new token per sequence, split-K paged attention, log-sum-exp
-combine.  Successive steps walk the 24 layers so the working set (~830 MB)
+layer's decode step for the whole batch (luc_decode_step, one launch): RoPE(q,
+k) + paged append of one new token per sequence, split-K paged attention whose
+last split per sequence merges the partials (log-sum-exp).  Successive steps walk the 24 layers so the working set (~830 MB)
 does not fit the 256 MB Infinity Cache.  Inputs are resident in HBM before
 timing; the K steps are replayed from a HIP graph, bracketed by
 torch.cuda.synchronize().
 
 Also reported:
   roofline      the paged decode operation (luc_paged_decode: the split-K
-                decode kernel and its combine kernel): algorithmic bytes per
+                decode kernel, merge included): algorithmic bytes per
                 launch (K+V over every context token, q, output, block table)
                 over its average duration, measured with HIP events around a
                 graph of back-to-back launches on the launch stream;
@@ -272,13 +272,13 @@ def main():
                    "kv_heads": cfg.hkv, "head_dim": cfg.head_dim,
                    "ctx": f"U{{{cfg.ctx_lo}..{cfg.ctx_hi}}}", "mean_ctx": float(np.mean(ctx)),
                    "page_size": 16, "pool_pages": cfg.pool_pages, "layers_rotated": L,
-                   "step": "luc_decode_step: rope+append+split-K decode, then combine (one layer)",
+                   "step": "luc_decode_step: rope + append + split-K decode with in-kernel LSE merge (one launch, one layer)",
                    "bytes_per_step": int(step_bytes),
                    "launch": "eager" if args.eager else "hip graph",
                    "split_tokens": args.split_tokens or "auto"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": traffic, "kernel": "luc_paged_decode (luc_decode_* + luc_decode_combine_*)",
+                     "traffic": traffic, "kernel": "luc_paged_decode (luc_decode_*, merge in the last split)",
                      "us_per_launch": round(dec_ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": int(dec_bytes)},
         "cpu_baseline": cpu,

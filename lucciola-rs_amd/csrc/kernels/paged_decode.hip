@@ -398,26 +398,17 @@ __device__ void lse_merge(const DecodeArgs& A, int bh, int nsplit, uint16_t* out
 
 // The step variant's roped q (G heads) and k of the new token, written back
 // into the qkv row by the NT threads of the workgroup that finishes (b, h)
-// last, after every split has read them: the same rotation as the kernel's
-// own, recomputed from the untouched row.
-template <int DT, int D, int G, int NT>
-__device__ void qk_writeback(const DecodeArgs& A, int b, int h, int pos) {
-  constexpr int HD = D / 2;
-  constexpr int GD = G * D;
-  const float* crow = A.cos_t + (int64_t)pos * HD;
-  const float* srow = A.sin_t + (int64_t)pos * HD;
-  uint16_t* qrow = A.q + (int64_t)b * A.q_stride + (int64_t)h * GD;
-  uint16_t* krow = A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D;
-  for (int idx = threadIdx.x; idx < (G + 1) * HD; idx += NT) {
-    const int g = idx / HD, j = idx % HD;
-    uint16_t* x = g < G ? qrow + g * D : krow;
-    const uint16_t* bias = g < G ? (A.q_bias ? A.q_bias + ((int64_t)h * G + g) * D : nullptr)
-                                 : (A.k_bias ? A.k_bias + (int64_t)h * D : nullptr);
-    uint16_t o1, o2;
-    rot_pair<DT>(x[j], bias ? bias[j] : 0, x[j + HD], bias ? bias[j + HD] : 0, crow[j], srow[j],
-                 o1, o2);
-    x[j] = o1;
-    x[j + HD] = o2;
+// last, after every split has read the row: copied from the LDS copies the
+// workgroup's wave 0 roped (every split ropes the same values).
+template <int D, int G, int NT>
+__device__ void qk_writeback(const DecodeArgs& A, int b, int h, const uint16_t* sq,
+                             const uint16_t* sk) {
+  constexpr int QW = G * D / 2;  // 32-bit words of q
+  uint32_t* qrow = (uint32_t*)(A.q + (int64_t)b * A.q_stride + (int64_t)h * G * D);
+  uint32_t* krow = (uint32_t*)(A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D);
+  for (int i = threadIdx.x; i < QW + D / 2; i += NT) {
+    if (i < QW) qrow[i] = ((const uint32_t*)sq)[i];
+    else krow[i - QW] = ((const uint32_t*)sk)[i - QW];
   }
 }
 
@@ -1083,12 +1074,14 @@ __device__ void decode_impl(const DecodeArgs& A) {
     }
     __syncthreads();
     if (!*s_last) return;
+    if constexpr (APPEND) qk_writeback<D, G, 64 * W>(A, b, h, s_q[0], s_knew[0]);
     // every other split's partial is complete: the agent-scope loads of
     // lse_merge see them
     float* const s_w = (float*)&s_k[0][0][0];  // the records were read above
     lse_merge<DT, D, G, 64 * W>(A, bh, nsplit, out_row, s_w, s_w + G * 256);
+  } else if constexpr (APPEND) {
+    qk_writeback<D, G, 64 * W>(A, b, h, s_q[0], s_knew[0]);
   }
-  if constexpr (APPEND) qk_writeback<DT, D, G, 64 * W>(A, b, h, pos);
 }
 
 }  // namespace luc
