@@ -441,8 +441,11 @@ __device__ void decode_impl(const DecodeArgs& A) {
   constexpr int NSM = 6 * SR / 256;  // loads for the six small regions
   constexpr int PBYTES = PA_SM + 6 * SR;
   // Per wave: NB K tile buffers (the first one later holds the wave's merge
-  // record: o[G*D], m[G], l[G]), the p exchange, and for the step variant the
-  // roped q and the new token's k and v.
+  // record: o[G*D], m[G], l[G]) and the p exchange.  The step variant's roped
+  // q and new token's k and v: per wave in the two-tile kernels; one copy per
+  // workgroup in the single-tile kernels (FASTA), where wave 0 loads the
+  // operand block and ropes it for all four (so the workgroup fits 40 KB of
+  // LDS: four per CU).
   // merge record: after the reduce-scatter, writer lane (j = lane / 16,
   // chunk pv_ch) holds the o values j * NV/4 + k, k < NV/4 (value v: head
   // v / 8, dim pv_ch * 8 + v % 8); it stores them at slot j * CH + pv_ch,
@@ -452,15 +455,17 @@ __device__ void decode_impl(const DecodeArgs& A) {
   static_assert(REC_ML + 2 * G <= S::KBYTES / 4, "merge record fits a K buffer");
   __shared__ __attribute__((aligned(16))) char s_k[W][NB][S::KBYTES];
   __shared__ __attribute__((aligned(16))) uint32_t s_p[W][PWORDS];
-  __shared__ __attribute__((aligned(16))) uint16_t s_q[APPEND ? W : 1][APPEND ? GD : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t s_knew[APPEND ? W : 1][APPEND ? D : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t s_vnew[APPEND ? W : 1][APPEND ? D : 8];
+  constexpr int NOP = (APPEND && !FASTA) ? W : 1;  // copies of the step operands
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[NOP][APPEND ? GD : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t s_knew[NOP][APPEND ? D : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t s_vnew[NOP][APPEND ? D : 8];
   __shared__ __attribute__((aligned(16))) char s_qr[FASTQ ? W : 1][FASTQ ? NQ * 256 : 16];
-  __shared__ __attribute__((aligned(16))) char s_pa[FASTA ? W : 1][FASTA ? PBYTES : 16];
+  __shared__ __attribute__((aligned(16))) char s_pa[1][FASTA ? PBYTES : 16];
   static_assert((G * 256 + G) * 4 <= W * NB * S::KBYTES, "merge weights fit the K buffers");
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave of the workgroup
+  const int qi = NOP == 1 ? 0 : w;  // this wave's copy of the step operands
   const int pairs = A.batch * A.hkv;
   const int split = blockIdx.x / pairs;
   const int bh = blockIdx.x - split * pairs;
@@ -616,8 +621,9 @@ __device__ void decode_impl(const DecodeArgs& A) {
       for (int i = 0; i < NQ; ++i)
         dma4((const char*)qrow + min(i * 256 + lane * 4, GD * 2 - 4), (lds_char*)s_qr[w] + i * 256);
     }
-    if constexpr (FASTA) {
-      // the operand block; a missing bias reads the operand itself (ignored)
+    if (FASTA && w == 0) {
+      // the workgroup's operand block (wave 0 only); a missing bias reads the
+      // operand itself (ignored)
       const char* krow = (const char*)(A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D);
       const char* vrow = (const char*)(A.v_new + (int64_t)b * A.q_stride + (int64_t)h * D);
       const char* qb = A.q_bias ? (const char*)(A.q_bias + (int64_t)h * GD) : (const char*)qrow;
@@ -625,7 +631,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       const char* vb = A.v_bias ? (const char*)(A.v_bias + (int64_t)h * D) : vrow;
       const char* cr = (const char*)(A.cos_t + (int64_t)pos * HD);
       const char* sr = (const char*)(A.sin_t + (int64_t)pos * HD);
-      lds_char* pa = (lds_char*)s_pa[w];
+      lds_char* pa = (lds_char*)s_pa[0];
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
         const int off = min(i * 256 + lane * 4, GD * 2 - 4);
@@ -694,17 +700,17 @@ __device__ void decode_impl(const DecodeArgs& A) {
         const int g = idx / HD, j = idx % HD;
         uint16_t o1, o2;
         rot_pair<DT>(rx1[i], rb1[i], rx2[i], rb2[i], rc[i], rs[i], o1, o2);
-        uint16_t* dst = g < G ? s_q[w] + g * D : s_knew[w];
+        uint16_t* dst = g < G ? s_q[qi] + g * D : s_knew[qi];
         dst[j] = o1;
         dst[j + HD] = o2;
       }
     }
 #pragma unroll
     for (int i = 0; i < S::QKL; ++i)
-      s_vnew[w][lane + 64 * i] = St<DT>::store(St<DT>::load(rv[i]) + St<DT>::load(rvb[i]));
+      s_vnew[qi][lane + 64 * i] = St<DT>::store(St<DT>::load(rv[i]) + St<DT>::load(rvb[i]));
     wave_lds_sync();
 #pragma unroll
-    for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)s_q[w])[q_word(m)];
+    for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)s_q[qi])[q_word(m)];
   }
 
   float m_run[G], l_lane[G], o[G][8];
@@ -723,7 +729,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       if (owns && pos >= t0 && pos < t0 + S::TILE && lane < S::CH) {
         const int t = pos - t0;  // the new token's K row (swizzled slots)
         *(uint4*)(kb + t * S::ROWB + lane * 16) =
-            *(const uint4*)(s_knew[w] + ((lane ^ (t & 7)) * 8));
+            *(const uint4*)(s_knew[qi] + ((lane ^ (t & 7)) * 8));
       }
       wave_lds_sync();
     }
@@ -804,7 +810,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
         const int t = pos - t0;
 #pragma unroll
         for (int r = 0; r < S::LOADS; ++r)
-          if (r == t / S::TPL && pv_tok == t % S::TPL) vr[r] = *(const uint4*)(s_vnew[w] + pv_ch * 8);
+          if (r == t / S::TPL && pv_tok == t % S::TPL) vr[r] = *(const uint4*)(s_vnew[qi] + pv_ch * 8);
       }
     }
     // tokens past the split: V must contribute exactly zero (p is 0 there,
@@ -863,19 +869,14 @@ __device__ void decode_impl(const DecodeArgs& A) {
 
   if constexpr (NB == 1) {
     // at most one tile per wave (the split is W tiles)
-    if (ntw > 0) {
-      LUC_WAIT_VM(8);  // K and q
-      if constexpr (FASTQ) {  // q words from LDS: qd[m] = word q_word(m)
-        const uint32_t qa = lds_addr(s_qr[w]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
-        read_q_words<0, 2 * G, HD>(qa, qd);
-#pragma unroll
-        for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
-      }
-      if constexpr (FASTA) {
-        // bias + RoPE of q (G heads) and k of the new token, in dword pairs
-        // (dims j, j + 1 and j + D/2, j + D/2 + 1) from the operand block;
-        // v + v_bias
-        const uint32_t pa = lds_addr(s_pa[w]);
+    if constexpr (FASTA) {
+      // wave 0 (it always has a tile) ropes the workgroup's operands: bias +
+      // RoPE of q (G heads) and k of the new token, in dword pairs (dims j,
+      // j + 1 and j + D/2, j + D/2 + 1) from the operand block; v + v_bias.
+      // Every wave, with or without a tile, meets it at the barrier.
+      if (w == 0) {
+        LUC_WAIT_VM(8);  // K and the operand block
+        const uint32_t pa = lds_addr(s_pa[0]);
         constexpr int NP2 = (G + 1) * HD / 2;
         const bool hqb = A.q_bias != nullptr, hkb = A.k_bias != nullptr, hvb = A.v_bias != nullptr;
 #pragma unroll
@@ -898,11 +899,11 @@ __device__ void decode_impl(const DecodeArgs& A) {
             const uint32_t lo = (uint32_t)o1a | ((uint32_t)o1b << 16);
             const uint32_t hi = (uint32_t)o2a | ((uint32_t)o2b << 16);
             if (g < G) {  // (two stores with known targets: no alias with the loads into LDS)
-              *(uint32_t*)(s_q[w] + g * D + j) = lo;
-              *(uint32_t*)(s_q[w] + g * D + j + HD) = hi;
+              *(uint32_t*)(s_q[qi] + g * D + j) = lo;
+              *(uint32_t*)(s_q[qi] + g * D + j + HD) = hi;
             } else {
-              *(uint32_t*)(s_knew[w] + j) = lo;
-              *(uint32_t*)(s_knew[w] + j + HD) = hi;
+              *(uint32_t*)(s_knew[qi] + j) = lo;
+              *(uint32_t*)(s_knew[qi] + j + HD) = hi;
             }
           }
         }
@@ -912,12 +913,24 @@ __device__ void decode_impl(const DecodeArgs& A) {
           if (!hvb) vbv = 0u;
           const uint16_t lo = St<DT>::store(St<DT>::load(vv & 0xffff) + St<DT>::load(vbv & 0xffff));
           const uint16_t hi = St<DT>::store(St<DT>::load(vv >> 16) + St<DT>::load(vbv >> 16));
-          *(uint32_t*)(s_vnew[w] + 2 * lane) = (uint32_t)lo | ((uint32_t)hi << 16);
+          *(uint32_t*)(s_vnew[qi] + 2 * lane) = (uint32_t)lo | ((uint32_t)hi << 16);
         }
-        wave_lds_sync();
-        // q words (as in the plain kernel; compiler-visible reads of LDS would
-        // wait for every outstanding load)
-        const uint32_t qa = lds_addr(s_q[w]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // its LDS writes are done
+      }
+      __builtin_amdgcn_s_barrier();
+    }
+    if (ntw > 0) {
+      LUC_WAIT_VM(8);  // K and q
+      if constexpr (FASTQ) {  // q words from LDS: qd[m] = word q_word(m)
+        const uint32_t qa = lds_addr(s_qr[w]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
+        read_q_words<0, 2 * G, HD>(qa, qd);
+#pragma unroll
+        for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
+      }
+      if constexpr (FASTA) {
+        // q words of the shared roped copy (asm reads: compiler-visible reads
+        // of LDS would wait for every outstanding load)
+        const uint32_t qa = lds_addr(s_q[0]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
         read_q_words<0, 2 * G, HD>(qa, qd);
 #pragma unroll
         for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
@@ -972,8 +985,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
         phys = page_of((pos - s_begin) / kPage);
       }
       const int64_t slot = phys * page_stride + head_off + (int64_t)(pos % kPage) * D + lane * 8;
-      *(uint4*)(A.k_pool + slot) = *(const uint4*)(s_knew[w] + lane * 8);
-      *(uint4*)(A.v_pool + slot) = *(const uint4*)(s_vnew[w] + lane * 8);
+      *(uint4*)(A.k_pool + slot) = *(const uint4*)(s_knew[qi] + lane * 8);
+      *(uint4*)(A.v_pool + slot) = *(const uint4*)(s_vnew[qi] + lane * 8);
     }
   }
 
