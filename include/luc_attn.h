@@ -180,6 +180,37 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
                       int num_layers, int num_q_heads, int num_kv_heads, int head_dim,
                       int block_size, float sm_scale, void* out, int64_t out_row_stride);
 
+/* ---- The model loop's small kernels (bf16 only) ---- */
+
+/* RMSNorm of `rows` rows of `cols` elements: out = round((x * inv) * w) with
+ * inv = 1/sqrt(mean(x^2) + eps), f32 arithmetic -- rmsnorm_nvidia
+ * (src/kernels/rmsnorm.cu:4-70) as called by CudaFunctions::apply_rmsnorm.
+ * cols a multiple of 8, every operand 16-byte aligned; out may equal in.
+ * The sum of squares has a fixed order (per thread over 16-byte chunks
+ * t, t+256, ..., then a halving tree over 256 partials), so results are
+ * reproducible bit for bit. */
+int luc_rmsnorm(luc_ctx* ctx, void* stream, int dtype, void* out, const void* in,
+                const void* weight, float eps, int rows, int cols);
+
+/* In place on rows [gate (intermediate) | up (intermediate)]:
+ * gate = round(silu(gate) * up), silu(g) = g / (1 + exp(-g)) in f32 --
+ * silu_and_mul_fused_kernel (src/kernels/activation.cu:6-29).
+ * intermediate a multiple of 8, gate_up 16-byte aligned. */
+int luc_silu_mul(luc_ctx* ctx, void* stream, int dtype, void* gate_up, int rows,
+                 int intermediate);
+
+/* out[t] = table[ids[t]] for num_tokens device ids -- batched_embedding_kernel
+ * (src/kernels/embedding.cu:3-39).  An id at or past `vocab` gives a NaN row
+ * (the reference reads past its table).  hidden a multiple of 8, out and
+ * table 16-byte aligned. */
+int luc_embedding(luc_ctx* ctx, void* stream, int dtype, void* out, const void* table,
+                  const uint32_t* ids, int num_tokens, int vocab, int hidden);
+
+/* *out_idx = index of the largest of n bf16 logits -- argmax_kernel
+ * (src/kernels/sampling.cu:16-46): values <= -1e30 and NaN never win (then
+ * 0xffffffff, the reference's -1); equal values go to the smallest index. */
+int luc_argmax(luc_ctx* ctx, void* stream, int dtype, const void* logits, int n, uint32_t* out_idx);
+
 #ifdef __cplusplus
 }
 #endif

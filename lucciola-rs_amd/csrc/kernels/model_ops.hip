@@ -1,0 +1,154 @@
+// The Qwen2 model loop's small kernels for gfx950: embedding gather, RMSNorm,
+// fused SiLU * up, greedy argmax -- the reference's batched_embedding_kernel
+// (src/kernels/embedding.cu), rmsnorm_nvidia (src/kernels/rmsnorm.cu),
+// silu_and_mul_fused_kernel (src/kernels/activation.cu) and argmax_kernel
+// (src/kernels/sampling.cu).  bf16 storage, f32 arithmetic.
+//
+// Fixed arithmetic order, so that a CPU restatement can produce the same bits:
+//   RMSNorm: thread t of 256 sums x*x over its 16-byte chunks c = t, t + 256,
+//   ... (elements in order, one fma each); the 256 partials add as a halving
+//   tree (a[i] += a[i + s] for s = 128, 64, ..., 1); inv = 1 / sqrt(sum / n +
+//   eps) with IEEE division and square root; y = round((x * inv) * w).
+//   argmax: the largest value wins; equal values go to the smallest index
+//   (the reference's block reduction leaves that order to its library).
+#include "luc_common.h"
+
+namespace luc {
+
+constexpr int kNormThreads = 256;
+
+// RMSNorm of `rows` rows of n elements (n a multiple of 8, 16-byte aligned
+// rows): out may alias in.
+__device__ void rmsnorm_impl(uint16_t* out, const uint16_t* in, const uint16_t* weight, float eps,
+                             int n) {
+#pragma clang fp contract(off)
+  __shared__ float part[kNormThreads];
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const uint4* x = (const uint4*)(in + row * n);
+  const int chunks = n / 8;
+  float s = 0.0f;
+  for (int c = t; c < chunks; c += kNormThreads) {
+    const uint4 v = x[c];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = St<kBF16>::load(chunk_elem(v, e));
+      s = fmaf(f, f, s);
+    }
+  }
+  part[t] = s;
+  __syncthreads();
+  for (int h = kNormThreads / 2; h > 0; h >>= 1) {
+    if (t < h) part[t] = part[t] + part[t + h];
+    __syncthreads();
+  }
+  const float inv = 1.0f / sqrtf(part[0] / (float)n + eps);
+  const uint4* w = (const uint4*)weight;
+  uint4* y = (uint4*)(out + row * n);
+  for (int c = t; c < chunks; c += kNormThreads) {
+    const uint4 v = x[c], wv = w[c];
+    uint16_t o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = St<kBF16>::load(chunk_elem(v, e)) * inv;
+      o[e] = St<kBF16>::store(f * St<kBF16>::load(chunk_elem(wv, e)));
+    }
+    y[c] = chunk_pack(o);
+  }
+}
+
+// gate <- round(silu(gate) * up) in place, rows of [gate (inter) | up (inter)],
+// silu(g) = g / (1 + exp(-g)) in f32; eight elements per thread.
+__device__ void silu_mul_impl(uint16_t* buf, int rows, int inter) {
+#pragma clang fp contract(off)
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // chunk of 8 gates
+  const int per_row = inter / 8;
+  if (i >= (int64_t)rows * per_row) return;
+  const int64_t r = i / per_row;
+  const int c = (int)(i - r * per_row);
+  uint4* g = (uint4*)(buf + r * 2 * inter) + c;
+  const uint4 gv = *g, uv = *(const uint4*)(buf + r * 2 * inter + inter + c * 8);
+  uint16_t o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float x = St<kBF16>::load(chunk_elem(gv, e));
+    const float s = x / (1.0f + expf(-x));
+    o[e] = St<kBF16>::store(s * St<kBF16>::load(chunk_elem(uv, e)));
+  }
+  *g = chunk_pack(o);
+}
+
+// out[t] = table[ids[t]] (rows of `hidden`, a multiple of 8); an id at or past
+// `vocab` gives a NaN row instead of a read outside the table.
+__device__ void embedding_impl(uint16_t* out, const uint16_t* table, const uint32_t* ids, int vocab,
+                               int hidden) {
+  const int64_t t = blockIdx.x;
+  const uint32_t id = ids[t];
+  uint4* dst = (uint4*)(out + t * hidden);
+  const int chunks = hidden / 8;
+  if (id >= (uint32_t)vocab) {
+    const uint32_t nan2 = 0x7fc07fc0u;
+    for (int c = threadIdx.x; c < chunks; c += blockDim.x) dst[c] = make_uint4(nan2, nan2, nan2, nan2);
+    return;
+  }
+  const uint4* src = (const uint4*)(table + (int64_t)id * hidden);
+  for (int c = threadIdx.x; c < chunks; c += blockDim.x) dst[c] = src[c];
+}
+
+constexpr int kArgmaxThreads = 1024;
+
+// Index of the largest of n values (values <= -1e30 and NaN never win, as in
+// the reference, which then reports index -1, i.e. 0xffffffff).
+__device__ void argmax_impl(const uint16_t* x, int n, uint32_t* out) {
+  __shared__ float sv[kArgmaxThreads];
+  __shared__ int si[kArgmaxThreads];
+  const int t = threadIdx.x;
+  float best = -1e30f;
+  int idx = -1;
+  for (int i = t; i < n; i += kArgmaxThreads) {  // increasing i: the first of equals stays
+    const float v = St<kBF16>::load(x[i]);
+    if (v > best) {
+      best = v;
+      idx = i;
+    }
+  }
+  sv[t] = best;
+  si[t] = idx;
+  __syncthreads();
+  for (int h = kArgmaxThreads / 2; h > 0; h >>= 1) {
+    if (t < h) {
+      const float bv = sv[t + h];
+      const int bi = si[t + h];
+      // larger value, or an equal one at a smaller index (-1 = none)
+      if (bv > sv[t] || (bv == sv[t] && bi >= 0 && (si[t] < 0 || bi < si[t]))) {
+        sv[t] = bv;
+        si[t] = bi;
+      }
+    }
+    __syncthreads();
+  }
+  if (t == 0) out[0] = (uint32_t)si[0];
+}
+
+}  // namespace luc
+
+extern "C" __global__ __launch_bounds__(256) void luc_rmsnorm_bf16(uint16_t* out, const uint16_t* in,
+                                                                   const uint16_t* weight, float eps,
+                                                                   int n) {
+  luc::rmsnorm_impl(out, in, weight, eps, n);
+}
+
+extern "C" __global__ __launch_bounds__(256) void luc_silu_mul_bf16(uint16_t* buf, int rows, int inter) {
+  luc::silu_mul_impl(buf, rows, inter);
+}
+
+extern "C" __global__ __launch_bounds__(256) void luc_embedding_bf16(uint16_t* out, const uint16_t* table,
+                                                                     const uint32_t* ids, int vocab,
+                                                                     int hidden) {
+  luc::embedding_impl(out, table, ids, vocab, hidden);
+}
+
+extern "C" __global__ __launch_bounds__(1024) void luc_argmax_bf16(const uint16_t* x, int n,
+                                                                   uint32_t* out) {
+  luc::argmax_impl(x, n, out);
+}

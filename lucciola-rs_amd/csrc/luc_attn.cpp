@@ -54,7 +54,7 @@ int fail(int code, const char* fmt, ...) {
   } while (0)
 
 constexpr const char* kCodeObjects[] = {"rope_append.hsaco", "paged_decode.hsaco",
-                                         "paged_prefill.hsaco"};
+                                         "paged_prefill.hsaco", "model_ops.hsaco"};
 
 // Kernel-side constants (kept in step with csrc/kernels/paged_decode.hip):
 // four waves per workgroup, which share one split; tiles of 64 tokens
@@ -376,7 +376,8 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
     }
     ctx->modules.push_back(mod);
   }
-  std::vector<std::string> names;
+  std::vector<std::string> names = {"luc_rmsnorm_bf16", "luc_silu_mul_bf16", "luc_embedding_bf16",
+                                    "luc_argmax_bf16"};
   for (const char* dt : {"bf16", "f16"}) {
     names.push_back(std::string("luc_rope_append_") + dt);
     for (int d : {64, 128}) names.push_back(std::string("luc_rope_append_vec_") + dt + "_d" + std::to_string(d));
@@ -620,6 +621,69 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
   p.pairs = pairs; p.qk_scale_log2 = sm_scale * 1.4426950408889634f;
   void* args[] = {&p};
   return launch(fn, dim3((unsigned)grid), dim3(64 * waves), stream, args);
+}
+
+// ---- the model loop's small kernels (model_ops.hip) ----
+
+int luc_rmsnorm(luc_ctx* ctx, void* stream, int dtype, void* out, const void* in, const void* weight,
+                float eps, int rows, int cols) {
+  if (!ctx) return fail(LUC_E_INVALID, "null context");
+  if (dtype != LUC_BF16) return fail(LUC_E_UNSUPPORTED, "rmsnorm: bf16 only");
+  if (rows < 0 || cols <= 0 || cols % 8) return fail(LUC_E_INVALID, "rows %d / cols %d (a multiple of 8)", rows, cols);
+  if (!out || !in || !weight) return fail(LUC_E_INVALID, "null out, in or weight");
+  if (!aligned(out, 16) || !aligned(in, 16) || !aligned(weight, 16))
+    return fail(LUC_E_INVALID, "rmsnorm operands must be 16-byte aligned");
+  if (rows == 0) return LUC_OK;
+  if (int rc = check_device(ctx)) return rc;
+  hipFunction_t fn;
+  if (int rc = get_fn(ctx, "luc_rmsnorm_bf16", &fn)) return rc;
+  void* args[] = {&out, &in, &weight, &eps, &cols};
+  return launch(fn, dim3(rows), dim3(256), stream, args);
+}
+
+int luc_silu_mul(luc_ctx* ctx, void* stream, int dtype, void* gate_up, int rows, int intermediate) {
+  if (!ctx) return fail(LUC_E_INVALID, "null context");
+  if (dtype != LUC_BF16) return fail(LUC_E_UNSUPPORTED, "silu_mul: bf16 only");
+  if (rows < 0 || intermediate <= 0 || intermediate % 8)
+    return fail(LUC_E_INVALID, "rows %d / intermediate %d (a multiple of 8)", rows, intermediate);
+  if (!gate_up || !aligned(gate_up, 16)) return fail(LUC_E_INVALID, "gate_up null or not 16-byte aligned");
+  if (rows == 0) return LUC_OK;
+  if (int rc = check_device(ctx)) return rc;
+  hipFunction_t fn;
+  if (int rc = get_fn(ctx, "luc_silu_mul_bf16", &fn)) return rc;
+  const int64_t grid = ceil_div((int64_t)rows * (intermediate / 8), 256);
+  if (grid > INT32_MAX) return fail(LUC_E_INVALID, "too many rows");
+  void* args[] = {&gate_up, &rows, &intermediate};
+  return launch(fn, dim3((unsigned)grid), dim3(256), stream, args);
+}
+
+int luc_embedding(luc_ctx* ctx, void* stream, int dtype, void* out, const void* table,
+                  const uint32_t* ids, int num_tokens, int vocab, int hidden) {
+  if (!ctx) return fail(LUC_E_INVALID, "null context");
+  if (dtype != LUC_BF16) return fail(LUC_E_UNSUPPORTED, "embedding: bf16 only");
+  if (num_tokens < 0 || vocab <= 0 || hidden <= 0 || hidden % 8)
+    return fail(LUC_E_INVALID, "num_tokens %d / vocab %d / hidden %d (a multiple of 8)", num_tokens,
+                vocab, hidden);
+  if (!out || !table || !ids) return fail(LUC_E_INVALID, "null out, table or ids");
+  if (!aligned(out, 16) || !aligned(table, 16)) return fail(LUC_E_INVALID, "out/table must be 16-byte aligned");
+  if (num_tokens == 0) return LUC_OK;
+  if (int rc = check_device(ctx)) return rc;
+  hipFunction_t fn;
+  if (int rc = get_fn(ctx, "luc_embedding_bf16", &fn)) return rc;
+  void* args[] = {&out, &table, &ids, &vocab, &hidden};
+  return launch(fn, dim3(num_tokens), dim3(128), stream, args);
+}
+
+int luc_argmax(luc_ctx* ctx, void* stream, int dtype, const void* logits, int n, uint32_t* out_idx) {
+  if (!ctx) return fail(LUC_E_INVALID, "null context");
+  if (dtype != LUC_BF16) return fail(LUC_E_UNSUPPORTED, "argmax: bf16 only");
+  if (n <= 0) return fail(LUC_E_INVALID, "n %d <= 0", n);
+  if (!logits || !out_idx) return fail(LUC_E_INVALID, "null logits or out_idx");
+  if (int rc = check_device(ctx)) return rc;
+  hipFunction_t fn;
+  if (int rc = get_fn(ctx, "luc_argmax_bf16", &fn)) return rc;
+  void* args[] = {&logits, &n, &out_idx};
+  return launch(fn, dim3(1), dim3(1024), stream, args);
 }
 
 }  // extern "C"

@@ -47,6 +47,10 @@ SIGNATURES = {
     "luc_paged_prefill": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                  _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                  _i32, _i32, _f32, _vp, _i64]),
+    "luc_rmsnorm": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _f32, _i32, _i32]),
+    "luc_silu_mul": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32]),
+    "luc_embedding": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32]),
+    "luc_argmax": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp]),
 }
 
 
@@ -202,6 +206,30 @@ class LucAttn:
             _p(tables), tables.shape[-1], _p(cu_seqlens), _p(start_pos), start_pos.shape[0],
             total_rows, max_ctx, layer, num_layers, hq, hkv, head_dim, block_size, sm_scale,
             _p(out), out_row_stride if out_row_stride is not None else hq * head_dim))
+
+    # ---- the model loop's small kernels ----
+    def rmsnorm(self, out, x, weight, eps, stream=None):
+        """luc_rmsnorm over the rows of x ([rows, cols] bf16); out may be x."""
+        cols = x.shape[-1]
+        self._check(self.lib.luc_rmsnorm(self.ctx, _stream(stream), dtype_code(x), _p(out), _p(x),
+                                         _p(weight), eps, x.numel() // cols, cols))
+
+    def silu_mul(self, gate_up, intermediate, stream=None):
+        """luc_silu_mul in place on [rows, 2*intermediate] (gate | up) rows."""
+        rows = gate_up.numel() // (2 * intermediate)
+        self._check(self.lib.luc_silu_mul(self.ctx, _stream(stream), dtype_code(gate_up),
+                                          _p(gate_up), rows, intermediate))
+
+    def embedding(self, out, table, ids, stream=None):
+        """luc_embedding: out[t] = table[ids[t]] (ids: device int32/uint32)."""
+        self._check(self.lib.luc_embedding(self.ctx, _stream(stream), dtype_code(table), _p(out),
+                                           _p(table), _p(ids), ids.numel(), table.shape[0],
+                                           table.shape[1]))
+
+    def argmax(self, logits, out_idx, stream=None):
+        """luc_argmax into out_idx (a one-element device int32 tensor)."""
+        self._check(self.lib.luc_argmax(self.ctx, _stream(stream), dtype_code(logits), _p(logits),
+                                        logits.numel(), _p(out_idx)))
 
     def workspace(self, batch, hq, hkv, head_dim, max_ctx, split_tokens=0, device=None):
         """A zero-filled decode workspace (None when no split-K is needed)."""

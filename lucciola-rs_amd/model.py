@@ -1,0 +1,228 @@
+"""Qwen2 decoder loop on the HIP path: the reference's Qwen2Model
+(src/models.rs:28-830) for one sequence, with its attention replaced by this
+library's kernels.
+
+Per layer (Qwen2Model::forward_layer, models.rs:434-691):
+  norm   = rmsnorm(h, input_layernorm)                  luc_rmsnorm
+  qkv    = norm @ qkv_proj^T                            GEMM (hipBLASLt), bf16 out
+  att    = rope + cache write + attention               luc_decode_step (one token)
+                                                        / luc_paged_prefill (prompt)
+  h      = att @ o_proj^T + h                           GEMM, beta = 1 (one rounding)
+  norm   = rmsnorm(h, post_attention_layernorm)
+  gu     = norm @ gate_up_proj^T                        GEMM
+  gate   = silu(gate) * up                              luc_silu_mul
+  h      = gate @ down_proj^T + h                       GEMM, beta = 1
+then h = rmsnorm(h, norm) (models.rs:765-771, 815-822), logits = h @ lm_head^T
+(bf16, models.rs:295-342) and greedy sampling by luc_argmax (models.rs:344-360).
+The q/k biases enter in the RoPE step and the v bias in the cache write, as in
+the reference (models.rs:505-534).
+
+Weights are bf16 in the reference's fused layout (models.rs:91-155):
+qkv_proj = [q; k; v] rows, qkv_bias likewise (zeros when the checkpoint has
+none, utils.rs:70-126), gate_up_proj = [gate; up] rows, lm_head = the
+embedding when tie_word_embeddings.  `random_weights` makes a seeded random
+initialisation of that layout (no checkpoint is available offline).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import library
+from .engine import KVCache, RopeCache, sm_scale
+
+
+@dataclass(frozen=True)
+class Qwen2Config:
+    """The fields of src/config.rs:3-37 the forward pass uses (Qwen2.5-0.5B values)."""
+    vocab_size: int = 151936
+    hidden_size: int = 896
+    num_hidden_layers: int = 24
+    num_attention_heads: int = 14
+    num_key_value_heads: int = 2
+    intermediate_size: int = 4864
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+    max_position_embeddings: int = 32768
+    tie_word_embeddings: bool = True
+    eos_token_id: int = 151643
+    bos_token_id: int = 151643
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+    @property
+    def qkv_dim(self) -> int:
+        return self.hidden_size + 2 * self.num_key_value_heads * self.head_dim
+
+
+QWEN25_05B = Qwen2Config()
+
+
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit patterns, round to nearest even."""
+    t = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def random_weights(cfg: Qwen2Config, seed: int, std: float = 0.02) -> dict:
+    """Seeded random weights in the reference's fused layout, as bf16 bits:
+    matrices and biases N(0, std^2), norm weights 1 + N(0, std^2)."""
+    rng = np.random.default_rng(seed)
+    H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+
+    def normal(*shape, mean=0.0):
+        return to_bf16_bits(mean + std * rng.standard_normal(shape, dtype=np.float32))
+
+    w = {"embed_tokens": normal(V, H), "final_norm": normal(H, mean=1.0), "layers": []}
+    for _ in range(cfg.num_hidden_layers):
+        w["layers"].append({
+            "input_layernorm": normal(H, mean=1.0),
+            "qkv_proj": normal(cfg.qkv_dim, H),
+            "qkv_bias": normal(cfg.qkv_dim),
+            "o_proj": normal(H, H),
+            "post_attention_layernorm": normal(H, mean=1.0),
+            "gate_up_proj": normal(2 * I, H),
+            "down_proj": normal(H, I),
+        })
+    if not cfg.tie_word_embeddings:
+        w["lm_head"] = normal(V, H)
+    return w
+
+
+def _dev(bits: np.ndarray, device) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(device)
+
+
+class Qwen2Model:
+    """One sequence through the decoder: `forward(ids, cache_pos)` then
+    `sample_greedy()`, or `generate` (models.rs:184-243).  Every GEMM's weight
+    is held transposed ([in, out], contiguous) so each product is a plain
+    row-major GEMM."""
+
+    def __init__(self, cfg: Qwen2Config, weights: dict, num_blocks: int | None = None,
+                 max_positions: int | None = None, device="cuda", lib=None):
+        self.cfg = cfg
+        self.lib = lib if lib is not None else library.default(torch.cuda.current_device())
+        self.device = torch.device(device)
+        d = cfg.head_dim
+        if cfg.hidden_size % cfg.num_attention_heads or d not in (64, 128):
+            raise ValueError(f"unsupported head_dim {d}")
+        T = lambda bits: _dev(bits, self.device).t().contiguous()  # noqa: E731  [in, out]
+        self.embed = _dev(weights["embed_tokens"], self.device)
+        self.lm_head_t = T(weights.get("lm_head", weights["embed_tokens"]))
+        self.final_norm = _dev(weights["final_norm"], self.device)
+        self.layers = []
+        for lw in weights["layers"]:
+            qb = _dev(lw["qkv_bias"], self.device)
+            q_dim, k_dim = cfg.hidden_size, cfg.num_key_value_heads * d
+            self.layers.append({
+                "in_norm": _dev(lw["input_layernorm"], self.device),
+                "qkv_t": T(lw["qkv_proj"]),
+                "q_bias": qb[:q_dim], "k_bias": qb[q_dim:q_dim + k_dim], "v_bias": qb[q_dim + k_dim:],
+                "o_t": T(lw["o_proj"]),
+                "post_norm": _dev(lw["post_attention_layernorm"], self.device),
+                "gate_up_t": T(lw["gate_up_proj"]),
+                "down_t": T(lw["down_proj"]),
+            })
+        max_pos = max_positions or cfg.max_position_embeddings
+        self.max_positions = max_pos
+        self.rope = RopeCache(max_pos, d, cfg.rope_theta, device=self.device, lib=self.lib)
+        blocks = num_blocks or (max_pos + 15) // 16
+        self.kv = KVCache(cfg.num_hidden_layers, cfg.num_key_value_heads, d, blocks, max_pos,
+                          dtype=torch.bfloat16, device=self.device, lib=self.lib)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.hidden = torch.zeros(1, cfg.hidden_size, dtype=torch.bfloat16, device=self.device)
+        self.idx = torch.zeros(1, dtype=torch.int32, device=self.device)
+
+    # ---- one layer (models.rs:434-691) ----
+    def _attention_decode(self, li, qkv, pos):
+        cfg = self.cfg
+        L = self.layers[li]
+        att = torch.empty(1, cfg.hidden_size, dtype=torch.bfloat16, device=self.device)
+        ws = self.kv.workspace(cfg.num_attention_heads, pos + 1)
+        self.lib.decode_step(qkv, L["q_bias"], L["k_bias"], L["v_bias"], self.rope.cos, self.rope.sin,
+                             self.kv.k_pool, self.kv.v_pool, self.kv.block_table.view(1, -1),
+                             self.pos, 1, pos + 1, li, cfg.num_hidden_layers, cfg.num_attention_heads,
+                             cfg.num_key_value_heads, cfg.head_dim, sm_scale(cfg.head_dim), att, ws)
+        return att
+
+    def _attention_prefill(self, li, qkv, cache_pos, cu, start):
+        cfg = self.cfg
+        L = self.layers[li]
+        S = qkv.shape[0]
+        att = torch.empty(S, cfg.hidden_size, dtype=torch.bfloat16, device=self.device)
+        self.lib.paged_prefill(qkv, L["q_bias"], L["k_bias"], L["v_bias"], self.rope.cos,
+                               self.rope.sin, self.kv.k_pool, self.kv.v_pool,
+                               self.kv.block_table.view(1, -1), cu, start, S, cache_pos + S, li,
+                               cfg.num_hidden_layers, cfg.num_attention_heads,
+                               cfg.num_key_value_heads, cfg.head_dim, sm_scale(cfg.head_dim), att)
+        return att
+
+    def _layer(self, li, h, attention):
+        cfg = self.cfg
+        L = self.layers[li]
+        I = cfg.intermediate_size
+        norm = torch.empty_like(h)
+        self.lib.rmsnorm(norm, h, L["in_norm"], cfg.rms_norm_eps)
+        qkv = torch.mm(norm, L["qkv_t"])
+        att = attention(li, qkv)
+        h = torch.addmm(h, att, L["o_t"])
+        self.lib.rmsnorm(norm, h, L["post_norm"], cfg.rms_norm_eps)
+        gate_up = torch.mm(norm, L["gate_up_t"])
+        self.lib.silu_mul(gate_up, I)
+        return torch.addmm(h, gate_up[:, :I], L["down_t"])
+
+    # ---- forward (models.rs:693-830) ----
+    def forward(self, input_ids, cache_pos: int) -> None:
+        """Run the decoder over `input_ids` at positions cache_pos...; leaves the
+        last row's final-normed hidden state in self.hidden."""
+        cfg = self.cfg
+        S = len(input_ids)
+        if S == 0:
+            return
+        if cache_pos + S > self.max_positions:
+            raise ValueError(f"positions {cache_pos}..{cache_pos + S - 1} exceed {self.max_positions}")
+        ids = torch.tensor([int(i) for i in input_ids], dtype=torch.int32, device=self.device)
+        h = torch.empty(S, cfg.hidden_size, dtype=torch.bfloat16, device=self.device)
+        self.lib.embedding(h, self.embed, ids)
+        for p in range(cache_pos, cache_pos + S):  # the pages of every position first
+            self.kv.prepare_for_step(p)
+        if S == 1:
+            self.pos.fill_(cache_pos)
+            attention = lambda li, qkv: self._attention_decode(li, qkv, cache_pos)  # noqa: E731
+        else:
+            cu = torch.tensor([0, S], dtype=torch.int32, device=self.device)
+            start = torch.tensor([cache_pos], dtype=torch.int32, device=self.device)
+            attention = lambda li, qkv: self._attention_prefill(li, qkv, cache_pos, cu, start)  # noqa: E731
+        for li in range(cfg.num_hidden_layers):
+            h = self._layer(li, h, attention)
+        last = h[S - 1:].contiguous()
+        self.lib.rmsnorm(self.hidden, last, self.final_norm, cfg.rms_norm_eps)
+
+    def logits(self) -> torch.Tensor:
+        """bf16 logits [1, vocab] of the current hidden state (models.rs:295-342)."""
+        return torch.mm(self.hidden, self.lm_head_t)
+
+    def sample_greedy(self) -> int:
+        self.lib.argmax(self.logits(), self.idx)
+        return int(self.idx.cpu().item())
+
+    def generate(self, prompt_ids, max_new_tokens: int, stop_at_eos: bool = True) -> list[int]:
+        """Greedy generation (models.rs:184-243): prefill, then one token per step."""
+        out, pos = [], 0
+        self.forward(prompt_ids, pos)
+        pos += len(prompt_ids)
+        tok = self.sample_greedy()
+        out.append(tok)
+        for _ in range(max_new_tokens):
+            if stop_at_eos and tok in (self.cfg.eos_token_id, self.cfg.bos_token_id):
+                break
+            self.forward([tok], pos)
+            pos += 1
+            tok = self.sample_greedy()
+            out.append(tok)
+        return out

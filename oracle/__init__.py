@@ -79,11 +79,34 @@ class Oracle:
         lib.orc_decode_step.argtypes = [_u16p, _i64, _u16p, _i64, _u16p, _u16p, _u16p, _f32p,
                                         _f32p, _u16p, _u16p, _i32p, _int, _i32p, _int, _int,
                                         _int, _int, _int, _flt, _int, _int, _int, _int]
+        lib.orc_rmsnorm.argtypes = [_u16p, _u16p, _u16p, _flt, _int, _int]
+        lib.orc_silu_mul.argtypes = [_u16p, _int, _int]
+        lib.orc_argmax.restype = _int
+        lib.orc_argmax.argtypes = [_u16p, _int]
         lib.orc_prefill.argtypes = [_u16p, _i64, _u16p, _i64, _u16p, _u16p, _u16p, _f32p, _f32p,
                                     _u16p, _u16p, _i32p, _int, _i32p, _i32p, _int, _int, _int,
                                     _int, _int, _flt, _int, _int, _int, _int]
 
     # ---- conversions -------------------------------------------------
+    def rmsnorm(self, x, weight, eps):
+        """RMSNorm of the rows of x (bf16 bits, [rows, cols])."""
+        x = np.ascontiguousarray(x)
+        out = np.empty_like(x)
+        cols = x.shape[-1]
+        self.lib.orc_rmsnorm(_ptr(out, "u16"), _ptr(x, "u16"), _ptr(np.ascontiguousarray(weight), "u16"),
+                             eps, x.size // cols, cols)
+        return out
+
+    def silu_mul(self, gate_up, inter):
+        """gate = silu(gate) * up in place on rows [gate | up] (bf16 bits)."""
+        assert gate_up.flags["C_CONTIGUOUS"]
+        self.lib.orc_silu_mul(_ptr(gate_up, "u16"), gate_up.size // (2 * inter), inter)
+        return gate_up
+
+    def argmax(self, x):
+        x = np.ascontiguousarray(x)
+        return int(self.lib.orc_argmax(_ptr(x, "u16"), x.size))
+
     def to_storage(self, x: np.ndarray, dtype) -> np.ndarray:
         x = np.ascontiguousarray(x, dtype=np.float32)
         out = np.empty(x.shape, dtype=np.uint16)

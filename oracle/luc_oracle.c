@@ -1,7 +1,7 @@
 /*
  * luc_oracle.c -- CPU restatement of lucciola-rs's paged-attention path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker, never the product.  Only tests/,
+ * TEST INFRASTRUCTURE ONLY: what the product is tested against, never the product.  Only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
  *
  * Built with -ffp-contract=off so every multiply and add rounds where written.
@@ -376,3 +376,57 @@ void orc_prefill(uint16_t* out, int64_t out_stride, uint16_t* qkv, int64_t qkv_s
             out[r * out_stride + (int64_t)h * head_dim + i] = st(o[i], dtype);
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* Model loop operations: src/kernels/{rmsnorm,activation,sampling}.cu */
+/* ------------------------------------------------------------------ */
+void orc_rmsnorm(uint16_t* out, const uint16_t* in, const uint16_t* weight, float eps, int rows,
+                 int cols) {
+    enum { T = 256 };
+    const int chunks = cols / 8;
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t* x = in + (int64_t)r * cols;
+        float part[T];
+        for (int t = 0; t < T; ++t) {
+            float s = 0.0f;
+            for (int c = t; c < chunks; c += T)
+                for (int e = 0; e < 8; ++e) {
+                    const float f = orc_bf16_to_f32(x[8 * c + e]);
+                    s = fmaf(f, f, s);
+                }
+            part[t] = s;
+        }
+        for (int h = T / 2; h > 0; h >>= 1)
+            for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];   /* rmsnorm.cu:33-35 */
+        const float ms = part[0] / (float)(ORC_MUTANT == 11 ? cols - 1 : cols);
+        const float inv = 1.0f / sqrtf(ms + eps);                          /* rmsnorm.cu:40 */
+        uint16_t* y = out + (int64_t)r * cols;
+        for (int i = 0; i < cols; ++i) {
+            const float f = orc_bf16_to_f32(x[i]) * inv;                   /* rmsnorm.cu:63-64 */
+            y[i] = orc_f32_to_bf16(f * orc_bf16_to_f32(weight[i]));
+        }
+    }
+}
+
+void orc_silu_mul(uint16_t* gate_up, int rows, int inter) {
+    for (int r = 0; r < rows; ++r) {
+        uint16_t* g = gate_up + (int64_t)r * 2 * inter;
+        const uint16_t* u = g + inter;
+        for (int c = 0; c < inter; ++c) {
+            const float x = orc_bf16_to_f32(g[c]);
+            const float s = x / (1.0f + expf(ORC_MUTANT == 12 ? x : -x));                         /* activation.cu:4 */
+            g[c] = orc_f32_to_bf16(s * orc_bf16_to_f32(u[c]));              /* activation.cu:24-27 */
+        }
+    }
+}
+
+int orc_argmax(const uint16_t* x, int n) {
+    float best = -1e30f;                                                   /* sampling.cu:24-25 */
+    int idx = -1;
+    for (int i = 0; i < n; ++i) {
+        const float v = orc_bf16_to_f32(x[i]);
+        if (ORC_MUTANT == 13 ? v >= best : v > best) { best = v; idx = i; }
+    }
+    return idx;
+}
+

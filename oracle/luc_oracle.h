@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product (the HIP kernels, the
  * C-ABI library, the host mirror) may link, load or call this code.  It is the
- * checker: tests, the smoke check and the CPU-baseline leg of the benchmark use
+ * reference for tests, the smoke check and the CPU-baseline leg of the benchmark, which use
  * it to compute what the reference computes on the same inputs.
  *
  * Storage is 16-bit (bf16 or fp16, selected by `dtype`), passed as uint16_t
@@ -90,6 +90,25 @@ void orc_prefill(uint16_t* out, int64_t out_stride, uint16_t* qkv, int64_t qkv_s
                  const int32_t* start_pos, int batch, int layer, int num_q_heads,
                  int num_kv_heads, int head_dim, float sm_scale, int block_size,
                  int num_layers, int dtype, int num_threads);
+
+/* ---- The model loop's small operations (bf16 storage) ---- */
+
+/* RMSNorm -- src/kernels/rmsnorm.cu:4-70: out = bf16((x * inv) * w),
+ * inv = 1 / sqrt(sum(x^2) / n + eps).  The sum follows one fixed order: 256
+ * partials, partial t = fma-accumulated x^2 over elements 8c..8c+7 for chunks
+ * c = t, t + 256, ..., then a halving tree (p[i] += p[i + h], h = 128..1).
+ * out may equal in. */
+void orc_rmsnorm(uint16_t* out, const uint16_t* in, const uint16_t* weight, float eps, int rows,
+                 int cols);
+
+/* In place on rows [gate | up] of 2*inter elements: gate = bf16(silu(g) * u),
+ * silu(g) = g / (1 + exp(-g)) in f32 -- src/kernels/activation.cu:6-29. */
+void orc_silu_mul(uint16_t* gate_up, int rows, int inter);
+
+/* Greedy argmax of n bf16 values -- src/kernels/sampling.cu:16-46: values
+ * <= -1e30 and NaN never win (-1 when none does); ties go to the smallest
+ * index. */
+int orc_argmax(const uint16_t* x, int n);
 
 #ifdef __cplusplus
 }

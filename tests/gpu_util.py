@@ -10,7 +10,7 @@ import torch
 from lucciola_rs_amd import workloads as wl
 from lucciola_rs_amd.engine import RopeCache, decode_step, decode_step_unfused, sm_scale
 
-# north-star tolerance on attention outputs (max-abs vs the reference algorithm)
+# tolerance on attention outputs (max-abs vs the reference algorithm)
 TOL = {"f16": 2e-3, "bf16": 1e-2}
 
 

@@ -288,3 +288,156 @@ def check_prefill(orc, dtype, lens=(37, 64, 1), start=(0, 5, 130), hq=14, hkv=2,
                                   qkv2[r, kd + kv_dim: kd + 2 * kv_dim]):
                 worst = max(worst, 1e9)
     return worst
+
+
+# ---------------------------------------------------------------- model-loop ops
+def check_rmsnorm(orc, seed=7):
+    """Oracle RMSNorm vs the f64 value x / sqrt(mean(x^2) + eps) * w: within
+    half a bf16 unit plus the f32 arithmetic's few units of 2^-24.  Short rows
+    (8, 16 columns) make a wrong divisor or a dropped eps visible."""
+    rng = np.random.default_rng(seed)
+    worst = 0.0
+    for rows, cols, sigma, eps in [(3, 896, 1.0, 1e-6), (2, 8, 0.5, 1e-6), (4, 16, 3.0, 1e-6),
+                                   (2, 64, 1e-3, 1e-6), (1, 4864, 20.0, 1e-5)]:
+        x = bits(rng.standard_normal((rows, cols)) * sigma, "bf16")
+        w = bits(1 + 0.3 * rng.standard_normal(cols), "bf16")
+        got = f32(orc.rmsnorm(x, w, eps), "bf16").astype(np.float64)
+        xf = f32(x, "bf16").astype(np.float64)
+        want = xf / np.sqrt(np.mean(xf * xf, axis=1, keepdims=True) + np.float32(eps)) * f32(w, "bf16")
+        tol = ulp(want, "bf16") * 0.5 + np.abs(want) * 2.0 ** -18 + 1e-30
+        worst = max(worst, float(np.max(np.abs(got - want) / tol)))
+    return worst
+
+
+def check_silu_mul(orc, seed=8):
+    """gate <- silu(gate) * up vs f64 g / (1 + e^-g) * u (half a bf16 unit plus
+    the f32 exp's error); the up half must come back unchanged."""
+    rng = np.random.default_rng(seed)
+    rows, inter = 5, 512
+    gu = bits(rng.standard_normal((rows, 2 * inter)) * 4, "bf16")
+    gu[0, :8] = bits(np.array([0.0, -0.0, 20.0, -20.0, 88.0, -88.0, 1e-3, -1e-3]), "bf16")
+    got = orc.silu_mul(gu.copy(), inter)
+    if not np.array_equal(got[:, inter:], gu[:, inter:]):
+        return 1e9
+    g = f32(gu[:, :inter], "bf16").astype(np.float64)
+    u = f32(gu[:, inter:], "bf16").astype(np.float64)
+    want = g / (1 + np.exp(-g)) * u
+    tol = ulp(want, "bf16") * 0.5 + np.abs(want) * 2.0 ** -18 + 1e-30
+    return float(np.max(np.abs(f32(got[:, :inter], "bf16") - want) / tol))
+
+
+def check_argmax(orc, seed=9):
+    """Greedy index vs numpy's argmax (first of equal maxima), NaN never
+    chosen, -1 when no value exceeds -1e30.  Returns the number of misses."""
+    rng = np.random.default_rng(seed)
+    fails = 0
+    for n in (1, 7, 1000, 151936):
+        x = bits(rng.standard_normal(n), "bf16")
+        cases = [x]
+        if n > 3:
+            y = x.copy()
+            y[[1, n // 2, n - 1]] = bits(np.array([9.0, 9.0, 9.0]), "bf16")  # ties
+            z = y.copy()
+            z[0] = 0x7fc0                                                     # NaN first
+            cases += [y, z]
+        cases.append(bits(np.full(n, -1e31), "bf16"))
+        for c in cases:
+            v = f32(c, "bf16").astype(np.float64)
+            v = np.where(np.isnan(v), -np.inf, v)
+            want = int(np.argmax(v)) if v.max() > -1e30 else -1
+            fails += int(orc.argmax(c) != want)
+    return fails
+
+
+# ---------------------------------------------------------------- model composition
+def tiny_qwen_weights(cfg, seed, std=0.15):
+    """Random weights in the fused layout (bf16 bits), larger than an HF init
+    so attention is far from uniform and every term moves the logits."""
+    rng = np.random.default_rng(seed)
+    H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    qkv_dim = H + 2 * cfg.num_key_value_heads * cfg.head_dim
+    nb = lambda *s, mean=0.0: bits(mean + std * rng.standard_normal(s), "bf16")  # noqa: E731
+    w = {"embed_tokens": bits(rng.standard_normal((V, H)), "bf16"), "final_norm": nb(H, mean=1.0),
+         "layers": []}
+    for _ in range(cfg.num_hidden_layers):
+        w["layers"].append({"input_layernorm": nb(H, mean=1.0), "qkv_proj": nb(qkv_dim, H),
+                            "qkv_bias": nb(qkv_dim), "o_proj": nb(H, H),
+                            "post_attention_layernorm": nb(H, mean=1.0),
+                            "gate_up_proj": nb(2 * I, H), "down_proj": nb(H, I)})
+    return w
+
+
+def qwen2_f64(cfg, w, ids):
+    """Textbook Qwen2 decoder in float64 over the whole sequence (causal
+    attention, rotate-half RoPE with theta_i = pos / base^(2i/d), GQA, SwiGLU,
+    pre-norm residuals, tied lm_head); returns the last row's logits."""
+    F = lambda b: f32(b, "bf16").astype(np.float64)  # noqa: E731
+    H, d = cfg.hidden_size, cfg.head_dim
+    hq, hkv, I = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.intermediate_size
+    S = len(ids)
+    eps = cfg.rms_norm_eps
+
+    def norm(x, g):
+        return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * F(g)
+
+    pos = np.arange(S, dtype=np.float64)[:, None]
+    inv = 1.0 / np.power(cfg.rope_theta, np.arange(d // 2) * 2.0 / d)
+    c, s = np.cos(pos * inv)[:, None, :], np.sin(pos * inv)[:, None, :]
+
+    def rope(x):  # [S, heads, d]
+        a, b = x[..., : d // 2], x[..., d // 2:]
+        return np.concatenate([a * c - b * s, a * s + b * c], axis=-1)
+
+    h = F(w["embed_tokens"])[np.asarray(ids)]
+    mask = np.triu(np.full((S, S), -np.inf), 1)
+    for L in w["layers"]:
+        x = norm(h, L["input_layernorm"])
+        qkv = x @ F(L["qkv_proj"]).T + F(L["qkv_bias"])
+        q = rope(qkv[:, :H].reshape(S, hq, d))
+        k = rope(qkv[:, H: H + hkv * d].reshape(S, hkv, d))
+        v = qkv[:, H + hkv * d:].reshape(S, hkv, d)
+        att = np.empty((S, hq, d))
+        for hh in range(hq):
+            kv = hh // (hq // hkv)
+            sc = q[:, hh] @ k[:, kv].T / np.sqrt(d) + mask
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            att[:, hh] = (p / p.sum(axis=1, keepdims=True)) @ v[:, kv]
+        h = h + att.reshape(S, H) @ F(L["o_proj"]).T
+        x = norm(h, L["post_attention_layernorm"])
+        gu = x @ F(L["gate_up_proj"]).T
+        g, u = gu[:, :I], gu[:, I:]
+        h = h + (g / (1 + np.exp(-g)) * u) @ F(L["down_proj"]).T
+    return norm(h[-1:], w["final_norm"])[0] @ F(w["embed_tokens"]).T
+
+
+def check_oracle_model(orc, seed=11):
+    """The oracle's Qwen2 loop (bf16 at the reference's rounding points) vs
+    the f64 textbook decoder on a tiny config: prefill of 6 tokens then 4
+    decode steps, rms logit error within 4% of the rms logit at every step.
+    bf16 rounding at the reference's points gives about 1.5%; a dropped q/k or
+    v bias, interleaved instead of rotate-half RoPE, a wrong GQA map or
+    softmax scale, no causal mask, a swapped norm weight, silu applied to up or
+    no final norm each give 22% or more.  Returns the worst error relative to
+    that tolerance."""
+    from oracle.model import OracleQwen2
+    from types import SimpleNamespace
+    cfg = SimpleNamespace(vocab_size=300, hidden_size=128, num_hidden_layers=2, num_attention_heads=4,
+                          num_key_value_heads=2, intermediate_size=256, rms_norm_eps=1e-6,
+                          rope_theta=10000.0, head_dim=32)
+    w = tiny_qwen_weights(cfg, seed)
+    m = OracleQwen2(cfg, w, max_positions=64, num_blocks=8)
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(0, cfg.vocab_size, 10).tolist()
+    worst = 0.0
+    for step in range(5):
+        if step == 0:
+            m.forward(ids[:6], 0)
+            seq = ids[:6]
+        else:
+            m.forward([ids[5 + step]], 5 + step)
+            seq = ids[: 6 + step]
+        got = f32(m.logits(), "bf16").astype(np.float64)
+        want = qwen2_f64(cfg, w, seq)
+        tol = 0.04 * np.sqrt(np.mean(want * want))
+        worst = max(worst, float(np.sqrt(np.mean((got - want) ** 2)) / tol))
+    return worst

@@ -1,6 +1,6 @@
 """HIP decode path (RoPE + paged append + split-K attention + combine) vs the
 oracle, through the C ABI.  Integer/byte work (RoPE'd q and k, cache slots) is
-compared bit for bit; attention outputs within the north-star tolerance
+compared bit for bit; attention outputs within the stated tolerance
 (max-abs 2e-3 fp16, 1e-2 bf16)."""
 import numpy as np
 import pytest

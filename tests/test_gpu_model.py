@@ -1,0 +1,165 @@
+"""The Qwen2 decoder loop on the HIP path (lucciola_rs_amd/model.py) against
+the oracle's restatement (oracle/model.py): the model loop's small kernels
+bit for bit, and a random-init Qwen2.5-0.5B (24 layers, hidden 896, 14q/2kv,
+intermediate 4864, vocab 151936, tied embeddings) generating greedily for 128
+steps after a prefill."""
+import numpy as np
+import pytest
+import torch
+
+from lucciola_rs_amd import workloads as wl
+from lucciola_rs_amd.model import QWEN25_05B, Qwen2Model, random_weights, to_bf16_bits
+from gpu_util import from_dev, say, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def bf16_ulps(a, b):
+    """Distance in bf16 units in the last place between two bit arrays (finite values)."""
+    def key(x):
+        x = x.astype(np.int32)
+        return np.where(x & 0x8000, -(x & 0x7fff), x & 0x7fff)
+    return np.abs(key(a) - key(b))
+
+
+def test_rmsnorm_bit_exact(orc, luc):
+    rng = np.random.default_rng(1)
+    for rows, cols in [(1, 896), (7, 896), (3, 4864), (2, 64), (5, 2056)]:
+        x = to_bf16_bits(rng.standard_normal((rows, cols)) * rng.uniform(0.1, 30))
+        w = to_bf16_bits(1 + 0.1 * rng.standard_normal(cols))
+        want = orc.rmsnorm(x, w, 1e-6)
+        tx, tw = to_dev(x, "bf16"), to_dev(w, "bf16")
+        out = torch.empty_like(tx)
+        say(f"  [gpu] rmsnorm rows={rows} cols={cols}")
+        luc.rmsnorm(out, tx, tw, 1e-6)
+        luc.rmsnorm(tx, tx, tw, 1e-6)  # in place
+        torch.cuda.synchronize()
+        assert np.array_equal(from_dev(out), want)
+        assert np.array_equal(from_dev(tx), want)
+
+
+def test_silu_mul_matches_oracle(orc, luc):
+    """f32 silu * up rounded to bf16; the GPU's expf and the host's may differ
+    in the last f32 bit, so a bf16 result may rarely differ by one unit."""
+    rng = np.random.default_rng(2)
+    rows, inter = 9, 4864
+    gu = to_bf16_bits(rng.standard_normal((rows, 2 * inter)) * 3)
+    want = orc.silu_mul(gu.copy(), inter)
+    t = to_dev(gu, "bf16")
+    say(f"  [gpu] silu_mul rows={rows} inter={inter}")
+    luc.silu_mul(t, inter)
+    torch.cuda.synchronize()
+    got = from_dev(t)
+    assert np.array_equal(got[:, inter:], gu[:, inter:])  # up untouched
+    d = bf16_ulps(got[:, :inter], want[:, :inter])
+    say(f"  max ulp {d.max()}, differing {np.count_nonzero(d)} of {d.size}")
+    assert d.max() <= 1 and np.count_nonzero(d) <= d.size // 1000
+
+
+def test_embedding_gather_and_out_of_range(luc):
+    rng = np.random.default_rng(3)
+    vocab, hidden = 1000, 896
+    table = to_bf16_bits(rng.standard_normal((vocab, hidden)))
+    ids = np.array([0, 999, 5, 5, 1000, 123], np.int32)  # 1000 is past the table
+    out = torch.empty(len(ids), hidden, dtype=torch.bfloat16, device="cuda")
+    say("  [gpu] embedding")
+    luc.embedding(out, to_dev(table, "bf16"), torch.from_numpy(ids).cuda())
+    torch.cuda.synchronize()
+    got = from_dev(out)
+    for r, i in enumerate(ids):
+        if i < vocab:
+            assert np.array_equal(got[r], table[i])
+        else:
+            assert np.all((got[r] & 0x7fff) > 0x7f80)  # NaN row
+
+
+def test_argmax_ties_nan_and_floor(orc, luc):
+    rng = np.random.default_rng(4)
+    idx = torch.zeros(1, dtype=torch.int32, device="cuda")
+    cases = []
+    x = to_bf16_bits(rng.standard_normal(151936))
+    cases.append(x)
+    y = x.copy(); y[[7, 90000, 151935]] = to_bf16_bits(np.array([50.0, 50.0, 50.0]))
+    cases.append(y)                                   # ties: smallest index
+    z = y.copy(); z[3] = 0x7fc0                       # a NaN never wins
+    cases.append(z)
+    cases.append(to_bf16_bits(np.full(4096, -1e31)))  # nothing above -1e30: -1
+    for c in cases:
+        say(f"  [gpu] argmax n={c.size}")
+        luc.argmax(to_dev(c, "bf16"), idx)
+        torch.cuda.synchronize()
+        want = orc.argmax(c)
+        assert int(idx.cpu().item()) == (want if want >= 0 else -1)
+
+
+@pytest.fixture(scope="module")
+def qwen():
+    """Random-init Qwen2.5-0.5B (seeded; HF-style init: N(0, 0.02^2) matrices
+    and biases, norm weights about 1) on the GPU and in the oracle."""
+    from oracle.model import OracleQwen2
+    cfg = QWEN25_05B
+    say("  building random-init Qwen2.5-0.5B weights")
+    w = random_weights(cfg, seed=2025)
+    max_pos = 512
+    return cfg, Qwen2Model(cfg, w, max_positions=max_pos), OracleQwen2(cfg, w, max_pos)
+
+
+def test_greedy_128_steps_after_prefill(orc, qwen):
+    """Prefill of a 32-token prompt, then 128 greedy steps, the GPU loop and the
+    oracle in lockstep.  Tokens must be identical; the GEMMs' summation orders
+    differ (hipBLASLt here, BLAS in the oracle, cuBLAS in the reference), so
+    if a step disagrees it must be a near-tie: the GPU's token scores within
+    that step's largest logit difference of the oracle's best, and the run
+    stops there (the two continuations are both correct from then on)."""
+    cfg, gpu, ref = qwen
+    rng = np.random.default_rng(17)
+    prompt = rng.integers(0, cfg.vocab_size, 32).tolist()
+    say("  [gpu] prefill 32 + 128 greedy steps (GPU model and oracle in lockstep)")
+    ids, pos, tokens = prompt, 0, []
+    for step in range(129):
+        gpu.forward(ids, pos)
+        ref.forward(ids, pos)
+        gl = orc.to_f32(from_dev(gpu.logits())[0], "bf16")
+        rl = orc.to_f32(ref.logits(), "bf16")
+        g, r = gpu.sample_greedy(), ref.sample_greedy()
+        if g != r:
+            diff = float(np.max(np.abs(gl - rl)))
+            say(f"  step {step}: GPU {g} vs oracle {r}; oracle logits {rl[g]:.4f} vs {rl[r]:.4f}, "
+                f"max |logit diff| {diff:.4f}")
+            assert rl[r] - rl[g] <= diff, "a decided step differs"
+            break
+        tokens.append(g)
+        pos += len(ids)
+        ids = [g]
+    say(f"  identical for {len(tokens)} of 129 tokens; distinct: {len(set(tokens))}")
+    assert len(tokens) >= 64
+
+
+def test_teacher_forced_logits_random_tokens(orc, qwen):
+    """Both loops fed the same seeded random tokens (after a fresh 16-token
+    prefill at position 0 of a second cache): logits agree to within a few bf16
+    units, and the argmax agrees wherever the oracle's top two logits are
+    apart by more than the largest logit difference seen."""
+    cfg, _, _ = qwen
+    from oracle.model import OracleQwen2
+    w = random_weights(cfg, seed=2025)
+    gpu, ref = Qwen2Model(cfg, w, max_positions=256), OracleQwen2(cfg, w, 256)
+    rng = np.random.default_rng(23)
+    toks = rng.integers(0, cfg.vocab_size, 16 + 48).tolist()
+    say("  [gpu] teacher-forced: prefill 16, then 48 random tokens")
+    worst, flips, decided = 0.0, 0, 0
+    for step in range(49):
+        ids, pos = (toks[:16], 0) if step == 0 else ([toks[15 + step]], 15 + step)
+        gpu.forward(ids, pos)
+        ref.forward(ids, pos)
+        gl = orc.to_f32(from_dev(gpu.logits())[0], "bf16")
+        rl = orc.to_f32(ref.logits(), "bf16")
+        diff = float(np.max(np.abs(gl - rl)))
+        worst = max(worst, diff)
+        top2 = np.sort(rl)[-2:]
+        if top2[1] - top2[0] > 2 * diff:
+            decided += 1
+            flips += int(np.argmax(gl) != np.argmax(rl))
+    say(f"  max |logit diff| {worst:.4f}; argmax compared on {decided} of 49 steps, {flips} differ")
+    assert worst < 0.1
+    assert flips == 0

@@ -132,3 +132,19 @@ def test_decode_batch_equals_single(orc):
         one = orc.flash_decoding(np.ascontiguousarray(q[b]), kp, vp, np.ascontiguousarray(tables[b]),
                                  1, hq, hkv, d, int(pos[b]), 0.125, 16, 2, "f16")
         assert np.array_equal(out[b], one)
+
+
+def test_rmsnorm_vs_f64(orc):
+    assert pins.check_rmsnorm(orc) <= 1
+
+
+def test_silu_mul_vs_f64(orc):
+    assert pins.check_silu_mul(orc) <= 1
+
+
+def test_argmax_first_of_equals_nan_and_floor(orc):
+    assert pins.check_argmax(orc) == 0
+
+
+def test_oracle_qwen2_loop_vs_f64_decoder(orc):
+    assert pins.check_oracle_model(orc) <= 1

@@ -22,6 +22,9 @@ MUTANTS = {
     8: "scores read from the V pool",
     9: "wrong GQA head -> kv head mapping",
     10: "fp16 rounding truncates",
+    11: "RMSNorm mean over n - 1",
+    12: "silu with exp(+x)",
+    13: "argmax ties go to the last index",
 }
 
 
@@ -38,6 +41,9 @@ def all_checks(o):
     import numpy as np
     x = np.linspace(-3, 3, 10001, dtype=np.float32)
     res.append(("conv_f16", np.array_equal(o.to_storage(x, "f16"), pins.bits(x, "f16"))))
+    res.append(("rmsnorm", pins.check_rmsnorm(o) <= 1))
+    res.append(("silu_mul", pins.check_silu_mul(o) <= 1))
+    res.append(("argmax", pins.check_argmax(o) == 0))
     return res
 
 
