@@ -49,6 +49,7 @@ class Qwen2Config:
     tie_word_embeddings: bool = True
     eos_token_id: int = 151643
     bos_token_id: int = 151643
+    rope_scaling_factor: float | None = None  # rope_scaling.factor (config.rs:22-27)
 
     @property
     def head_dim(self) -> int:
@@ -130,13 +131,22 @@ class Qwen2Model:
             })
         max_pos = max_positions or cfg.max_position_embeddings
         self.max_positions = max_pos
-        self.rope = RopeCache(max_pos, d, cfg.rope_theta, device=self.device, lib=self.lib)
+        self.rope = RopeCache(max_pos, d, cfg.rope_theta, cfg.rope_scaling_factor, device=self.device,
+                              lib=self.lib)
         blocks = num_blocks or (max_pos + 15) // 16
         self.kv = KVCache(cfg.num_hidden_layers, cfg.num_key_value_heads, d, blocks, max_pos,
                           dtype=torch.bfloat16, device=self.device, lib=self.lib)
         self.pos = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.hidden = torch.zeros(1, cfg.hidden_size, dtype=torch.bfloat16, device=self.device)
         self.idx = torch.zeros(1, dtype=torch.int32, device=self.device)
+
+    @classmethod
+    def from_checkpoint(cls, directory: str, **kw) -> "Qwen2Model":
+        """Qwen2Model::new (models.rs:45-183): config.json + *.safetensors of a
+        directory, loaded by the reference's rules (checkpoint.load_checkpoint)."""
+        from .checkpoint import load_checkpoint
+        cfg, w = load_checkpoint(directory)
+        return cls(cfg, w, **kw)
 
     # ---- one layer (models.rs:434-691) ----
     def _attention_decode(self, li, qkv, pos):

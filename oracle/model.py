@@ -53,7 +53,8 @@ class OracleQwen2:
                 "o_t": T(lw["o_proj"]), "post_norm": lw["post_attention_layernorm"],
                 "gate_up_t": T(lw["gate_up_proj"]), "down_t": T(lw["down_proj"]),
             })
-        self.cos, self.sin = self.o.rope_table(max_positions, d, cfg.rope_theta)
+        self.cos, self.sin = self.o.rope_table(max_positions, d, cfg.rope_theta,
+                                               getattr(cfg, "rope_scaling_factor", None))
         blocks = num_blocks or (max_positions + PAGE - 1) // PAGE
         shape = (blocks, cfg.num_hidden_layers, cfg.num_key_value_heads, PAGE, d)
         self.k_pool = np.zeros(shape, np.uint16)

@@ -7,11 +7,16 @@ import numpy as np
 import pytest
 import torch
 
-from lucciola_rs_amd import workloads as wl
 from lucciola_rs_amd.model import QWEN25_05B, Qwen2Model, random_weights, to_bf16_bits
 from gpu_util import from_dev, say, to_dev
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _needs_device():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
 
 
 def bf16_ulps(a, b):
@@ -97,6 +102,8 @@ def qwen():
     """Random-init Qwen2.5-0.5B (seeded; HF-style init: N(0, 0.02^2) matrices
     and biases, norm weights about 1) on the GPU and in the oracle."""
     from oracle.model import OracleQwen2
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
     cfg = QWEN25_05B
     say("  building random-init Qwen2.5-0.5B weights")
     w = random_weights(cfg, seed=2025)
@@ -163,3 +170,40 @@ def test_teacher_forced_logits_random_tokens(orc, qwen):
     say(f"  max |logit diff| {worst:.4f}; argmax compared on {decided} of 49 steps, {flips} differ")
     assert worst < 0.1
     assert flips == 0
+
+
+def test_greedy_from_checkpoint_second_shape(orc, tmp_path):
+    """A written-then-loaded checkpoint at another head shape (hidden 256, 4q/2kv,
+    3 layers, vocab 1000, untied lm_head, rope scaling 2): the GPU loop and the
+    oracle in lockstep for a 20-token prompt and 48 greedy steps, with the same
+    near-tie rule as above."""
+    from oracle.model import OracleQwen2
+    from lucciola_rs_amd.checkpoint import load_checkpoint, write_checkpoint
+    from lucciola_rs_amd.model import Qwen2Config
+    cfg = Qwen2Config(vocab_size=1000, hidden_size=256, num_hidden_layers=3, num_attention_heads=4,
+                      num_key_value_heads=2, intermediate_size=512, max_position_embeddings=4096,
+                      tie_word_embeddings=False, rope_scaling_factor=2.0, eos_token_id=999,
+                      bos_token_id=998)
+    write_checkpoint(str(tmp_path), cfg, random_weights(cfg, seed=31, std=0.08), shards=2)
+    gpu = Qwen2Model.from_checkpoint(str(tmp_path), max_positions=128)
+    cfg2, w2 = load_checkpoint(str(tmp_path))
+    ref = OracleQwen2(cfg2, w2, 128)
+    ids = np.random.default_rng(19).integers(0, cfg.vocab_size, 20).tolist()
+    pos, tokens = 0, []
+    say("  [gpu] checkpoint model: prefill 20 + 48 greedy steps in lockstep")
+    for step in range(49):
+        gpu.forward(ids, pos)
+        ref.forward(ids, pos)
+        g, r = gpu.sample_greedy(), ref.sample_greedy()
+        if g != r:
+            gl = orc.to_f32(from_dev(gpu.logits())[0], "bf16")
+            rl = orc.to_f32(ref.logits(), "bf16")
+            diff = float(np.max(np.abs(gl - rl)))
+            say(f"  step {step}: GPU {g} vs oracle {r}; {rl[g]:.4f} vs {rl[r]:.4f}, diff {diff:.4f}")
+            assert rl[r] - rl[g] <= diff
+            break
+        tokens.append(g)
+        pos += len(ids)
+        ids = [g]
+    say(f"  identical for {len(tokens)} of 49 tokens; distinct: {len(set(tokens))}")
+    assert len(tokens) >= 24

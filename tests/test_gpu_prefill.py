@@ -1,6 +1,6 @@
 """HIP causal prefill (RoPE + cache write + MFMA attention of packed prompts)
 vs the oracle, through the C ABI.  Roped q/k (in place) and the cache are
-compared bit for bit; attention outputs within the north-star tolerance
+compared bit for bit; attention outputs within the stated tolerance
 (max-abs 2e-3 fp16, 1e-2 bf16)."""
 import numpy as np
 import pytest
