@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define LUC_ABI_VERSION 2
+#define LUC_ABI_VERSION 3
 #define LUC_BLOCK_SIZE 16
 
 typedef struct luc_ctx luc_ctx;
@@ -50,7 +50,8 @@ typedef enum luc_status {
     LUC_E_UNSUPPORTED = -2, /* head_dim / block_size / group size outside what is built */
     LUC_E_LOAD = -3,        /* code object or kernel symbol could not be loaded */
     LUC_E_HIP = -4,         /* a HIP runtime call failed */
-    LUC_E_WORKSPACE = -5    /* workspace missing or smaller than required */
+    LUC_E_WORKSPACE = -5,   /* workspace missing or smaller than required */
+    LUC_E_NOMEM = -6        /* the page allocator's free list is short */
 } luc_status;
 
 /* ABI version compiled into the library (LUC_ABI_VERSION). */
@@ -109,8 +110,10 @@ int luc_rope_append(luc_ctx* ctx, void* stream, int dtype, void* q, const void* 
  * 64 (head_dim 64) or 32 (head_dim 128); 0 = the library's choice.
  * The workspace must be 256-byte aligned and zero-filled once before its
  * first use; every launch leaves it ready for the next (its split arrival
- * counters return to zero).  Launches that may run concurrently (different
- * streams) need separate workspaces. */
+ * counters, the first 256 KiB, return to zero), whatever the batch and
+ * max_ctx of the next call, as long as the workspace is large enough for it.
+ * Split-K calls handle batch x num_kv_heads <= 65536.  Launches that may run
+ * concurrently (different streams) need separate workspaces. */
 size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                        int head_dim, int max_ctx, int split_tokens);
 
@@ -210,6 +213,42 @@ int luc_embedding(luc_ctx* ctx, void* stream, int dtype, void* out, const void* 
  * (src/kernels/sampling.cu:16-46): values <= -1e30 and NaN never win (then
  * 0xffffffff, the reference's -1); equal values go to the smallest index. */
 int luc_argmax(luc_ctx* ctx, void* stream, int dtype, const void* logits, int n, uint32_t* out_idx);
+
+/* ---- Multi-sequence page allocator (host only: no GPU call, no ctx) ------
+ * Generalises KVCache's free list and prepare_for_step
+ * (src/layers/kv_cache.rs:73-76, 106-122) from one sequence to max_seqs rows
+ * of a block table over one pool of num_blocks pages of LUC_BLOCK_SIZE tokens.
+ * The free list is LIFO and starts as [num_blocks-1, ..., 0], so a fresh
+ * allocator hands out pages 0, 1, 2, ... as the reference does.  Calls on
+ * one allocator must not overlap (the caller serialises them). */
+typedef struct luc_blocks luc_blocks;
+
+int luc_blocks_create(int num_blocks, int max_seqs, int max_blocks_per_seq, luc_blocks** out);
+void luc_blocks_destroy(luc_blocks* bm);
+
+/* Give sequence `seq` pages for positions [0, num_tokens): as many pages as
+ * that needs beyond those it holds (prepare_for_step adds one per call).
+ * Never shrinks.  LUC_E_NOMEM when the free list is short (the reference
+ * panics), LUC_E_INVALID past max_blocks_per_seq; either way nothing changes. */
+int luc_blocks_reserve(luc_blocks* bm, int seq, int num_tokens);
+
+/* The same for n distinct sequences, all or nothing over the batch. */
+int luc_blocks_reserve_batch(luc_blocks* bm, int n, const int32_t* seqs, const int32_t* num_tokens);
+
+/* Return every page of `seq` to the free list, last page first (a release
+ * then a reserve with nothing in between gives back the same pages in the
+ * same order).  The reference never frees pages. */
+int luc_blocks_release(luc_blocks* bm, int seq);
+
+/* Free pages in the pool / pages held by `seq` (negative status on error). */
+int luc_blocks_num_free(const luc_blocks* bm);
+int luc_blocks_num_pages(const luc_blocks* bm, int seq);
+
+/* Rows [first_seq, first_seq + n) of the block table into host memory
+ * `table` (row stride `stride` >= max_blocks_per_seq, int32): the held pages,
+ * then 0 (the reference's block_table is zero-initialised).  The caller
+ * copies it to the device, as prepare_for_step does with memcpy_htod. */
+int luc_blocks_table(const luc_blocks* bm, int first_seq, int n, int32_t* table, int stride);
 
 #ifdef __cplusplus
 }

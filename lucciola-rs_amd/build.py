@@ -63,6 +63,7 @@ def build_host(verbose=False):
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
           "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"),
           "-I", os.path.join(ROOT, "include"), os.path.join(CSRC, "luc_attn.cpp"),
+          os.path.join(CSRC, "luc_blocks.cpp"),
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
           "-o", tmp], verbose)
     os.replace(tmp, out)

@@ -224,9 +224,14 @@ int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requeste
 }
 
 // Workspace layout (each section 256-byte aligned):
+//   [split arrivals per (b, kv head): int32 x kMaxArrivalCounters, zero between launches]
 //   [(max, sum) per (b, kv head, split, head of the group): f32 x2]
 //   [o per (b, kv head, split): f32 x group x head_dim]
-//   [split arrivals per (b, kv head): int32, zero between launches]
+// The counters come first, at a size that does not depend on the call, so
+// that no later call with other sizes finds partials where it expects zeros:
+// one zero-filled workspace serves calls of any batch and max_ctx.
+constexpr int64_t kMaxArrivalCounters = 1 << 16;  // batch x kv heads
+constexpr int64_t kCounterBytes = kMaxArrivalCounters * 4;
 int64_t align256(int64_t n) { return ceil_div(n, 256) * 256; }
 int64_t ml_bytes(int batch, int hq, int max_splits) {
   return align256((int64_t)batch * hq * max_splits * 2 * 4);
@@ -237,9 +242,10 @@ int64_t o_bytes(int batch, int hq, int head_dim, int max_splits) {
 
 size_t workspace_bytes_for(int batch, int hq, int hkv, int head_dim, int max_ctx, int split_tokens) {
   const int64_t max_splits = ceil_div(max_ctx, split_tokens);
-  if (max_splits <= 1) return 0;
-  return (size_t)(ml_bytes(batch, hq, (int)max_splits) +
-                  o_bytes(batch, hq, head_dim, (int)max_splits) + align256((int64_t)batch * hkv * 4));
+  if (max_splits <= 1 || batch <= 0) return 0;
+  (void)hkv;
+  return (size_t)(kCounterBytes + ml_bytes(batch, hq, (int)max_splits) +
+                  o_bytes(batch, hq, head_dim, (int)max_splits));
 }
 
 struct DecodeLaunch {
@@ -281,6 +287,9 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
   if (need && (!workspace || workspace_bytes < need))
     return fail(LUC_E_WORKSPACE, "workspace %zu bytes, %zu needed", workspace_bytes, need);
   if (need && !aligned(workspace, 256)) return fail(LUC_E_INVALID, "workspace must be 256-byte aligned");
+  if (need && (int64_t)batch * num_kv_heads > kMaxArrivalCounters)
+    return fail(LUC_E_UNSUPPORTED, "split-K decode of batch x kv heads %lld above %lld",
+                (long long)batch * num_kv_heads, (long long)kMaxArrivalCounters);
   const int64_t grid = (int64_t)max_splits * batch * num_kv_heads;
   if (grid > INT32_MAX) return fail(LUC_E_INVALID, "batch x kv heads x splits too large");
 
@@ -315,10 +324,9 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
   a.max_splits = max_splits;
   if (need) {
     char* ws = static_cast<char*>(workspace);
-    a.ws_ml = reinterpret_cast<float*>(ws);
-    a.ws_o = reinterpret_cast<float*>(ws + ml_bytes(batch, num_q_heads, max_splits));
-    a.ws_cnt = reinterpret_cast<int32_t*>(ws + ml_bytes(batch, num_q_heads, max_splits) +
-                                          o_bytes(batch, num_q_heads, head_dim, max_splits));
+    a.ws_cnt = reinterpret_cast<int32_t*>(ws);
+    a.ws_ml = reinterpret_cast<float*>(ws + kCounterBytes);
+    a.ws_o = reinterpret_cast<float*>(ws + kCounterBytes + ml_bytes(batch, num_q_heads, max_splits));
   }
   a.out = static_cast<uint16_t*>(out);
   a.out_stride = out_row_stride;
@@ -348,6 +356,19 @@ int launch_decode(DecodeLaunch& L, void* stream) {
 }
 
 }  // namespace
+
+namespace luc_internal {
+// Error reporting for the other translation units of the library.
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+}  // namespace luc_internal
 
 extern "C" {
 

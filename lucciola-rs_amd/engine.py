@@ -14,6 +14,8 @@ Device memory comes from torch; every launch goes through liblucattn.so.
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import torch
 
@@ -98,6 +100,94 @@ class KVCache:
             self._workspace = torch.zeros(need // 4, dtype=torch.float32,
                                           device=self.k_pool.device)
         return self._workspace
+
+
+class BlockManager:
+    """Pages of one pool for many sequences, through the native allocator
+    (luc_blocks_*): the reference's free list and prepare_for_step
+    (kv_cache.rs:73-76, 106-122) per table row, with multi-page growth, batch
+    admission (all or nothing) and release.  Host only; no GPU call."""
+
+    def __init__(self, num_blocks: int, max_seqs: int, max_blocks_per_seq: int):
+        self.cdll = library.load_cdll()
+        self.max_seqs, self.max_pages = max_seqs, max_blocks_per_seq
+        self.handle = ctypes.c_void_p()
+        self._check(self.cdll.luc_blocks_create(num_blocks, max_seqs, max_blocks_per_seq,
+                                                ctypes.byref(self.handle)))
+
+    def _check(self, rc):
+        if rc < 0:
+            raise library.LucError(rc, self.cdll.luc_last_error().decode())
+        return rc
+
+    def close(self):
+        if self.handle:
+            self.cdll.luc_blocks_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reserve(self, seq: int, num_tokens: int) -> None:
+        self._check(self.cdll.luc_blocks_reserve(self.handle, seq, num_tokens))
+
+    def reserve_batch(self, seqs, num_tokens) -> None:
+        s = np.ascontiguousarray(seqs, dtype=np.int32)
+        t = np.ascontiguousarray(num_tokens, dtype=np.int32)
+        if s.shape != t.shape:
+            raise ValueError("seqs and num_tokens differ in length")
+        self._check(self.cdll.luc_blocks_reserve_batch(self.handle, s.size, s.ctypes.data,
+                                                       t.ctypes.data))
+
+    def release(self, seq: int) -> None:
+        self._check(self.cdll.luc_blocks_release(self.handle, seq))
+
+    @property
+    def num_free(self) -> int:
+        return self._check(self.cdll.luc_blocks_num_free(self.handle))
+
+    def num_pages(self, seq: int) -> int:
+        return self._check(self.cdll.luc_blocks_num_pages(self.handle, seq))
+
+    def table(self, first_seq: int = 0, n: int | None = None) -> np.ndarray:
+        n = self.max_seqs - first_seq if n is None else n
+        out = np.empty((n, self.max_pages), np.int32)
+        self._check(self.cdll.luc_blocks_table(self.handle, first_seq, n, out.ctypes.data,
+                                               self.max_pages))
+        return out
+
+
+class PagedKVCache:
+    """K/V pools shared by up to `max_seqs` sequences, their device block table
+    [max_seqs, max_blocks_per_seq] and the native allocator behind it -- the
+    batched form of KVCache.  `reserve` / `reserve_batch` / `release` change
+    the allocation; `sync()` copies the table to the device before a launch."""
+
+    def __init__(self, num_layers, num_kv_heads, head_dim, num_physical_blocks, max_seqs,
+                 max_position_embeddings, dtype=torch.bfloat16, device="cuda"):
+        self.num_layers, self.num_kv_heads, self.head_dim = num_layers, num_kv_heads, head_dim
+        self.block_size = BLOCK_SIZE
+        max_pages = (max_position_embeddings + BLOCK_SIZE - 1) // BLOCK_SIZE
+        self.blocks = BlockManager(num_physical_blocks, max_seqs, max_pages)
+        shape = (num_physical_blocks, num_layers, num_kv_heads, BLOCK_SIZE, head_dim)
+        self.k_pool = torch.zeros(shape, dtype=dtype, device=device)
+        self.v_pool = torch.zeros(shape, dtype=dtype, device=device)
+        self.block_tables = torch.zeros((max_seqs, max_pages), dtype=torch.int32, device=device)
+
+    def reserve(self, seq, num_tokens):
+        self.blocks.reserve(seq, num_tokens)
+
+    def reserve_batch(self, seqs, num_tokens):
+        self.blocks.reserve_batch(seqs, num_tokens)
+
+    def release(self, seq):
+        self.blocks.release(seq)
+
+    def sync(self):
+        self.block_tables.copy_(torch.from_numpy(self.blocks.table()))
 
 
 def apply_rope(rope, qkv, q_start_idx, k_start_idx, q_bias, k_bias, pos_ptr, head_dim,

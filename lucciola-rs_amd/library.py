@@ -16,7 +16,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LUC_BF16 = 0
 LUC_F16 = 1
 STATUS = {0: "LUC_OK", -1: "LUC_E_INVALID", -2: "LUC_E_UNSUPPORTED", -3: "LUC_E_LOAD",
-          -4: "LUC_E_HIP", -5: "LUC_E_WORKSPACE"}
+          -4: "LUC_E_HIP", -5: "LUC_E_WORKSPACE", -6: "LUC_E_NOMEM"}
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int
@@ -51,6 +51,14 @@ SIGNATURES = {
     "luc_silu_mul": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32]),
     "luc_embedding": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32]),
     "luc_argmax": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp]),
+    "luc_blocks_create": (_i32, [_i32, _i32, _i32, ctypes.POINTER(_vp)]),
+    "luc_blocks_destroy": (None, [_vp]),
+    "luc_blocks_reserve": (_i32, [_vp, _i32, _i32]),
+    "luc_blocks_reserve_batch": (_i32, [_vp, _i32, _vp, _vp]),
+    "luc_blocks_release": (_i32, [_vp, _i32]),
+    "luc_blocks_num_free": (_i32, [_vp]),
+    "luc_blocks_num_pages": (_i32, [_vp, _i32]),
+    "luc_blocks_table": (_i32, [_vp, _i32, _i32, _vp, _i32]),
 }
 
 

@@ -45,7 +45,7 @@ def test_code_objects_built_for_gfx950():
 
 def test_abi_version_and_error_string():
     cdll = library.load_cdll()
-    assert cdll.luc_abi_version() == 2
+    assert cdll.luc_abi_version() == 3
     rc = cdll.luc_paged_decode(None, None, 0, None, 0, None, 0, None, None, None, 0, None, 1,
                                1, 0, 1, 14, 2, 64, 16, 0.125, 0, None, 0)
     assert rc == -1
@@ -93,11 +93,11 @@ def test_workspace_size_policy(cdll):
     ws = cdll.luc_paged_decode_workspace_size
 
     def expect(batch, hq, hkv, d, splits):
-        # 256-byte aligned sections: (max, sum) in f32 per (sequence, q-head,
-        # split), o[d] in f32 per (sequence, q-head, split), an int32 arrival
-        # counter per (sequence, kv head)
+        # 256-byte aligned sections: 65536 int32 arrival counters (a fixed
+        # size, so one workspace serves calls of any sizes), (max, sum) in f32
+        # per (sequence, q-head, split), o[d] in f32 per (sequence, q-head, split)
         a256 = lambda n: -(-n // 256) * 256  # noqa: E731
-        return a256(batch * hq * splits * 8) + a256(batch * hq * splits * d * 4) + a256(batch * hkv * 4)
+        return 65536 * 4 + a256(batch * hq * splits * 8) + a256(batch * hq * splits * d * 4)
 
     # one split per sequence -> no workspace
     assert ws(32, 14, 2, 64, 100, 0) == 0

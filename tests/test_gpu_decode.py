@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from lucciola_rs_amd import workloads as wl
-from gpu_util import TOL, gpu_step, max_abs, oracle_step, say
+from gpu_util import TOL, from_dev, gpu_step, max_abs, oracle_step, say
 
 pytestmark = pytest.mark.gpu
 
@@ -207,7 +207,19 @@ def test_workspace_reuse_across_launches(orc, luc):
         luc.paged_decode(out, q, kp, vp, tables, pos, 6, max_ctx, i % 2, 2, 14, 2, 64,
                          sm_scale(64), 256, ws, q_row_stride=cfg.row)
         outs.append(out)
+    # a call with another batch and max_ctx on the same workspace in between
+    # (the arrival counters keep their place), then the first call again
+    small = torch.zeros((3, 14 * 64), dtype=torch.float16, device="cuda")
+    small_ctx = int(h.ctx[:3].max())
+    say(f"  [gpu] paged_decode batch 3, max_ctx {small_ctx} on the same workspace")
+    luc.paged_decode(small, q[:3], kp, vp, tables[:3], pos[:3], 3, small_ctx, 0, 2, 14, 2, 64,
+                     sm_scale(64), 128, ws, q_row_stride=cfg.row)
+    again = torch.zeros((6, 14 * 64), dtype=torch.float16, device="cuda")
+    luc.paged_decode(again, q, kp, vp, tables, pos, 6, max_ctx, 0, 2, 14, 2, 64,
+                     sm_scale(64), 256, ws, q_row_stride=cfg.row)
     torch.cuda.synchronize()
     for i in range(2, 8):
         assert torch.equal(outs[i], outs[i % 2])
     assert not torch.equal(outs[0], outs[1])
+    assert torch.equal(again, outs[0])
+    assert max_abs(orc, from_dev(small), from_dev(outs[0][:3]), "f16") <= TOL["f16"]
