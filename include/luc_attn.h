@@ -214,6 +214,28 @@ int luc_embedding(luc_ctx* ctx, void* stream, int dtype, void* out, const void* 
  * 0xffffffff, the reference's -1); equal values go to the smallest index. */
 int luc_argmax(luc_ctx* ctx, void* stream, int dtype, const void* logits, int n, uint32_t* out_idx);
 
+/* Top-k / top-p sampling of one bf16 logits row -- CudaFunctions::
+ * apply_sort_and_sample (src/kernels.rs:346-498) with its kernels top_k_filter
+ * and fused_top_p_sample_<top_k> (src/kernels/sampling_optimized.cu:27-236):
+ *  - candidates: the largest top_k/32 logits of each of 32 partitions
+ *    [p*vocab/32, (p+1)*vocab/32), values <= -1e30 and NaN excluded (a
+ *    partition short of them pads with (start - 1, -1e30)); equal values in
+ *    the reference's order;
+ *  - sorted by the reference's bitonic network (value, descending) and written
+ *    back to sort_buffer as top_k pairs (int32 index, f32 value);
+ *  - prob = exp(v - v_max) / sum, cdf = inclusive sum; cutoff = the cdf of the
+ *    candidate whose [cdf - prob, cdf] holds top_p (1 when none does);
+ *    *out_idx = the index of the candidate whose interval holds
+ *    rand_val * cutoff, left unwritten when none does (rand_val = 0).
+ * top_k is the sampler's normalised value (src/sampler.rs:19-23): a power of
+ * two in [32, 1024], else LUC_E_UNSUPPORTED (the reference's "Unsupported
+ * candidate size").  vocab in [32, 524288].  sort_buffer is caller-owned
+ * device memory of >= 8*top_k bytes (the engine's 8 KB sort_buffer,
+ * src/models.rs:171-174), else LUC_E_WORKSPACE.  Two launches on `stream`. */
+int luc_sort_and_sample(luc_ctx* ctx, void* stream, int dtype, const void* logits, int vocab,
+                        float top_p, int top_k, float rand_val, void* sort_buffer,
+                        size_t sort_buffer_bytes, uint32_t* out_idx);
+
 /* ---- Multi-sequence page allocator (host only: no GPU call, no ctx) ------
  * Generalises KVCache's free list and prepare_for_step
  * (src/layers/kv_cache.rs:73-76, 106-122) from one sequence to max_seqs rows

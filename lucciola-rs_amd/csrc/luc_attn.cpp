@@ -54,7 +54,8 @@ int fail(int code, const char* fmt, ...) {
   } while (0)
 
 constexpr const char* kCodeObjects[] = {"rope_append.hsaco", "paged_decode.hsaco",
-                                         "paged_prefill.hsaco", "model_ops.hsaco"};
+                                         "paged_prefill.hsaco", "model_ops.hsaco",
+                                         "sampling.hsaco"};
 
 // Kernel-side constants (kept in step with csrc/kernels/paged_decode.hip):
 // four waves per workgroup, which share one split; tiles of 64 tokens
@@ -399,6 +400,8 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
   }
   std::vector<std::string> names = {"luc_rmsnorm_bf16", "luc_silu_mul_bf16", "luc_embedding_bf16",
                                     "luc_argmax_bf16"};
+  for (int npl : {1, 2, 4, 8, 16}) names.push_back("luc_topk_filter_bf16_n" + std::to_string(npl));
+  for (int k = 32; k <= 1024; k *= 2) names.push_back("luc_top_p_sample_" + std::to_string(k));
   for (const char* dt : {"bf16", "f16"}) {
     names.push_back(std::string("luc_rope_append_") + dt);
     for (int d : {64, 128}) names.push_back(std::string("luc_rope_append_vec_") + dt + "_d" + std::to_string(d));
@@ -705,6 +708,38 @@ int luc_argmax(luc_ctx* ctx, void* stream, int dtype, const void* logits, int n,
   if (int rc = get_fn(ctx, "luc_argmax_bf16", &fn)) return rc;
   void* args[] = {&logits, &n, &out_idx};
   return launch(fn, dim3(1), dim3(1024), stream, args);
+}
+
+int luc_sort_and_sample(luc_ctx* ctx, void* stream, int dtype, const void* logits, int vocab,
+                        float top_p, int top_k, float rand_val, void* sort_buffer,
+                        size_t sort_buffer_bytes, uint32_t* out_idx) {
+  if (!ctx) return fail(LUC_E_INVALID, "null context");
+  if (dtype != LUC_BF16) return fail(LUC_E_UNSUPPORTED, "sort_and_sample: bf16 logits only");
+  // the fused sort kernels exist for 32..1024 candidates (kernels.rs:403-493)
+  if (top_k < 32 || top_k > 1024 || (top_k & (top_k - 1)))
+    return fail(LUC_E_UNSUPPORTED, "Unsupported candidate size: %d (a power of two in [32, 1024])",
+                top_k);
+  // every one of the 32 filter partitions holds at least one logit; at most
+  // 16 per thread of a 1024-thread partition workgroup
+  if (vocab < 32 || vocab > 32 * 16384)
+    return fail(LUC_E_INVALID, "vocab %d outside [32, %d]", vocab, 32 * 16384);
+  if (!logits || !sort_buffer || !out_idx) return fail(LUC_E_INVALID, "null logits, sort_buffer or out_idx");
+  if (!aligned(sort_buffer, 8)) return fail(LUC_E_INVALID, "sort_buffer must be 8-byte aligned");
+  if (sort_buffer_bytes < (size_t)top_k * 8)
+    return fail(LUC_E_WORKSPACE, "sort_buffer holds %zu bytes, %d candidates need %d", sort_buffer_bytes,
+                top_k, top_k * 8);
+  if (int rc = check_device(ctx)) return rc;
+  const int per_part = (vocab + 31) / 32;  // the largest partition
+  int npl = 1;
+  while (npl * 1024 < per_part) npl *= 2;
+  hipFunction_t filter, sample;
+  if (int rc = get_fn(ctx, "luc_topk_filter_bf16_n" + std::to_string(npl), &filter)) return rc;
+  if (int rc = get_fn(ctx, "luc_top_p_sample_" + std::to_string(top_k), &sample)) return rc;
+  int kpp = top_k / 32;
+  void* fargs[] = {&logits, &vocab, &kpp, &sort_buffer};
+  if (int rc = launch(filter, dim3(32), dim3(1024), stream, fargs)) return rc;
+  void* sargs[] = {&sort_buffer, &top_p, &rand_val, &out_idx};
+  return launch(sample, dim3(1), dim3(top_k < 64 ? 64 : top_k), stream, sargs);
 }
 
 }  // extern "C"

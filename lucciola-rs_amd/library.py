@@ -51,6 +51,7 @@ SIGNATURES = {
     "luc_silu_mul": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32]),
     "luc_embedding": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32]),
     "luc_argmax": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp]),
+    "luc_sort_and_sample": (_i32, [_vp, _vp, _i32, _vp, _i32, _f32, _i32, _f32, _vp, _sz, _vp]),
     "luc_blocks_create": (_i32, [_i32, _i32, _i32, ctypes.POINTER(_vp)]),
     "luc_blocks_destroy": (None, [_vp]),
     "luc_blocks_reserve": (_i32, [_vp, _i32, _i32]),
@@ -238,6 +239,16 @@ class LucAttn:
         """luc_argmax into out_idx (a one-element device int32 tensor)."""
         self._check(self.lib.luc_argmax(self.ctx, _stream(stream), dtype_code(logits), _p(logits),
                                         logits.numel(), _p(out_idx)))
+
+    def sort_and_sample(self, logits, top_p, top_k, rand_val, sort_buffer, out_idx, stream=None):
+        """luc_sort_and_sample of one bf16 logits row into out_idx (one-element
+        device int32 tensor, left unwritten when no candidate is drawn);
+        sort_buffer (>= 8*top_k bytes of device memory) returns the sorted
+        (index, value) candidates."""
+        self._check(self.lib.luc_sort_and_sample(
+            self.ctx, _stream(stream), dtype_code(logits), _p(logits), logits.numel(), float(top_p),
+            int(top_k), float(rand_val), _p(sort_buffer),
+            sort_buffer.numel() * sort_buffer.element_size(), _p(out_idx)))
 
     def workspace(self, batch, hq, hkv, head_dim, max_ctx, split_tokens=0, device=None):
         """A zero-filled decode workspace (None when no split-K is needed)."""

@@ -139,6 +139,7 @@ class Qwen2Model:
         self.pos = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.hidden = torch.zeros(1, cfg.hidden_size, dtype=torch.bfloat16, device=self.device)
         self.idx = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._sampler = None  # device buffers of sample_token, made on first use
 
     @classmethod
     def from_checkpoint(cls, directory: str, **kw) -> "Qwen2Model":
@@ -220,6 +221,13 @@ class Qwen2Model:
     def sample_greedy(self) -> int:
         self.lib.argmax(self.logits(), self.idx)
         return int(self.idx.cpu().item())
+
+    def sample_token(self, sampler) -> int:
+        """Qwen2Model::sample_token (models.rs:385-432): greedy or GPU top-p."""
+        if self._sampler is None:
+            from .sampler import DeviceSampler
+            self._sampler = DeviceSampler(self.lib, self.device)
+        return self._sampler.sample(self.logits(), sampler)
 
     def generate(self, prompt_ids, max_new_tokens: int, stop_at_eos: bool = True) -> list[int]:
         """Greedy generation (models.rs:184-243): prefill, then one token per step."""

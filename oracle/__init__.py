@@ -83,6 +83,10 @@ class Oracle:
         lib.orc_silu_mul.argtypes = [_u16p, _int, _int]
         lib.orc_argmax.restype = _int
         lib.orc_argmax.argtypes = [_u16p, _int]
+        lib.orc_topk_filter.argtypes = [_u16p, _int, _int, _i32p, _f32p]
+        lib.orc_bitonic_desc.argtypes = [_i32p, _f32p, _int]
+        lib.orc_top_p_pick.restype = _int
+        lib.orc_top_p_pick.argtypes = [_f32p, _int, _flt, _flt, _f32p, _f32p]
         lib.orc_prefill.argtypes = [_u16p, _i64, _u16p, _i64, _u16p, _u16p, _u16p, _f32p, _f32p,
                                     _u16p, _u16p, _i32p, _int, _i32p, _i32p, _int, _int, _int,
                                     _int, _int, _flt, _int, _int, _int, _int]
@@ -106,6 +110,41 @@ class Oracle:
     def argmax(self, x):
         x = np.ascontiguousarray(x)
         return int(self.lib.orc_argmax(_ptr(x, "u16"), x.size))
+
+    # ---- top-k / top-p sampling (sampling_optimized.cu) ---------------
+    def topk_filter(self, logits, k_per_block):
+        """Candidates of top_k_filter: (keys int32, values f32), 32*k_per_block each."""
+        x = np.ascontiguousarray(logits, dtype=np.uint16)
+        keys = np.zeros(32 * k_per_block, np.int32)
+        vals = np.zeros(32 * k_per_block, np.float32)
+        self.lib.orc_topk_filter(_ptr(x, "u16"), x.size, k_per_block, _ptr(keys, "i32"),
+                                 _ptr(vals, "f32"))
+        return keys, vals
+
+    def bitonic_desc(self, keys, vals):
+        """The reference's bitonic network on copies of (keys, vals)."""
+        keys = np.array(keys, dtype=np.int32)
+        vals = np.array(vals, dtype=np.float32)
+        self.lib.orc_bitonic_desc(_ptr(keys, "i32"), _ptr(vals, "f32"), keys.size)
+        return keys, vals
+
+    def top_p_pick(self, vals_sorted, top_p, rand_val):
+        """(position or -1, prob, cdf) of the sample step on sorted values."""
+        v = np.ascontiguousarray(vals_sorted, dtype=np.float32)
+        prob = np.empty_like(v)
+        cdf = np.empty_like(v)
+        i = self.lib.orc_top_p_pick(_ptr(v, "f32"), v.size, top_p, rand_val, _ptr(prob, "f32"),
+                                    _ptr(cdf, "f32"))
+        return int(i), prob, cdf
+
+    def sort_and_sample(self, logits, top_p, top_k, rand_val):
+        """apply_sort_and_sample: dict(keys, vals) of the sorted candidates,
+        token (None when no candidate's interval holds the target), prob, cdf."""
+        keys, vals = self.topk_filter(logits, top_k // 32)
+        keys, vals = self.bitonic_desc(keys, vals)
+        i, prob, cdf = self.top_p_pick(vals, top_p, rand_val)
+        return dict(keys=keys, vals=vals, token=None if i < 0 else int(keys[i]), pos=i, prob=prob,
+                    cdf=cdf)
 
     def to_storage(self, x: np.ndarray, dtype) -> np.ndarray:
         x = np.ascontiguousarray(x, dtype=np.float32)

@@ -430,3 +430,118 @@ int orc_argmax(const uint16_t* x, int n) {
     return idx;
 }
 
+
+/* ------------------------------------------------------------------ */
+/* Top-k / top-p sampling (src/kernels/sampling_optimized.cu)          */
+/* ------------------------------------------------------------------ */
+
+/* One (key, value) pair of the reference's KeyValuePair (sampling_optimized.cu:6-9). */
+typedef struct { int key; float value; } orc_kv;
+
+/* warpReduceMax over the 32 lanes of v (sampling_optimized.cu:15-25): for
+ * offsets 16, 8, 4, 2, 1 lane l takes lane l + offset's pair when that value
+ * is strictly larger; __shfl_down_sync hands a lane past 31 its own value, so
+ * those lanes keep theirs.  Lanes are updated from the values before the
+ * step, as the shuffle reads them.  Returns lane 0's pair. */
+static orc_kv orc_warp_reduce_max(orc_kv* v) {
+    for (int off = 16; off > 0; off /= 2) {
+        orc_kv nv[32];
+        for (int l = 0; l < 32; ++l) {
+            const orc_kv o = l + off < 32 ? v[l + off] : v[l];
+            nv[l] = v[l];
+            if (ORC_MUTANT == 14 ? o.value >= v[l].value : o.value > v[l].value) nv[l] = o;
+        }
+        memcpy(v, nv, sizeof(nv));
+    }
+    return v[0];
+}
+
+void orc_topk_filter(const uint16_t* logits, int vocab, int k_per_block, int32_t* keys,
+                     float* vals) {
+    enum { NT = 256, NWARP = NT / 32 };                       /* block 256 (kernels.rs:371-375) */
+    for (int p = 0; p < 32; ++p) {                            /* filter_grid = 32 (kernels.rs:367) */
+        const int start = (int)((long long)p * vocab / 32);   /* sampling_optimized.cu:37-43 */
+        const int end = (int)((long long)(p + 1) * vocab / 32);
+        const int n = end - start;
+        if (n <= 0) continue;                                 /* :45-46 (slots left untouched) */
+        float* s = (float*)malloc(sizeof(float) * (size_t)n);
+        for (int i = 0; i < n; ++i) s[i] = orc_bf16_to_f32(logits[start + i]);   /* :51-57 */
+        for (int k = 0; k < k_per_block; ++k) {               /* :65 */
+            orc_kv warp_max[NWARP];
+            for (int w = 0; w < NWARP; ++w) {
+                orc_kv lane[32];
+                for (int l = 0; l < 32; ++l) {                /* :66-76: strided scan, strict > */
+                    const int t = w * 32 + l;
+                    orc_kv m = {-1, -1e30f};
+                    for (int i = t; i < n; i += NT)
+                        if (s[i] > m.value) { m.value = s[i]; m.key = i; }
+                    lane[l] = m;
+                }
+                warp_max[w] = orc_warp_reduce_max(lane);      /* :78-83 */
+            }
+            orc_kv lane[32];                                  /* :85-92: warp 0 over the warps */
+            for (int l = 0; l < 32; ++l) {
+                lane[l].key = -1;
+                lane[l].value = -1e30f;
+                if (l < NWARP) lane[l] = warp_max[l];
+            }
+            const orc_kv bm = orc_warp_reduce_max(lane);
+            keys[p * k_per_block + k] = start + bm.key;       /* :102-106 */
+            vals[p * k_per_block + k] = bm.value;
+            if (bm.key >= 0 && bm.key < n) s[bm.key] = -1e30f; /* :107-108 */
+        }
+        free(s);
+    }
+}
+
+void orc_bitonic_desc(int32_t* keys, float* vals, int n) {
+    /* the compare-exchange network of sampling_optimized.cu:130-152, one
+     * stage at a time (the pairs of a stage are disjoint) */
+    for (int k = 2; k <= n; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1)
+            for (int t = 0; t < n; ++t) {
+                const int x = t ^ j;
+                if (x <= t) continue;
+                const int down = ORC_MUTANT == 15 ? (t & k) != 0 : (t & k) == 0;
+                const int swap = down ? vals[t] < vals[x] : vals[t] > vals[x];
+                if (swap) {
+                    const int32_t tk = keys[t]; keys[t] = keys[x]; keys[x] = tk;
+                    const float tv = vals[t]; vals[t] = vals[x]; vals[x] = tv;
+                }
+            }
+}
+
+int orc_top_p_pick(const float* vals, int n, float top_p, float rand_val, float* prob,
+                   float* cdf) {
+    /* sampling_optimized.cu:154-187 on the sorted candidates.  The sum and the
+     * inclusive scan run in index order here (CUB's BlockReduce/BlockScan
+     * order is not in the reference's sources). */
+    const float max_val = vals[0];                            /* :154 */
+    float total = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        prob[i] = expf(vals[i] - max_val);                    /* :155 */
+        total += prob[i];                                     /* :157-163 */
+    }
+    float run = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        prob[i] = prob[i] / total;                            /* :165 */
+        run += prob[i];                                       /* :166-169 */
+        cdf[i] = run;
+    }
+    /* :171-180: the thread whose interval holds top_p sets the cutoff (the
+     * first such thread here: the reference lets equal-time writers race) */
+    float cutoff = 1.0f;
+    for (int i = 0; i < n; ++i) {
+        const float prev = cdf[i] - prob[i];                  /* :176 */
+        if (ORC_MUTANT == 16 ? (prev < top_p && cdf[i] > top_p) : (prev < top_p && cdf[i] >= top_p)) {
+            cutoff = cdf[i];
+            break;
+        }
+    }
+    const float target = rand_val * cutoff;                   /* :182 */
+    for (int i = 0; i < n; ++i) {                             /* :183-187 */
+        const float prev = cdf[i] - prob[i];
+        if (cdf[i] >= target && prev < target) return i;
+    }
+    return -1;                                                /* no winner: output not written */
+}

@@ -110,6 +110,32 @@ void orc_silu_mul(uint16_t* gate_up, int rows, int inter);
  * index. */
 int orc_argmax(const uint16_t* x, int n);
 
+/* ---- Top-k / top-p sampling (src/kernels/sampling_optimized.cu) ---- */
+
+/* top_k_filter (sampling_optimized.cu:27-112) as launched by
+ * apply_sort_and_sample (src/kernels.rs:366-386): 32 partitions
+ * [p*vocab/32, (p+1)*vocab/32), each of 256 threads; k_per_block rounds of a
+ * strided per-thread scan (strict >, from {-1, -1e30}), a shfl_down max tree
+ * over each warp's 32 lanes and one over the 8 warp results; the winner's
+ * slot is set to -1e30.  Candidate p*k_per_block + k = (start + key, value).
+ * A round with nothing above -1e30 gives (start - 1, -1e30).  Simulated
+ * thread by thread, so ties resolve as the reference's trees resolve them. */
+void orc_topk_filter(const uint16_t* logits, int vocab, int k_per_block, int32_t* keys,
+                     float* vals);
+
+/* The bitonic compare-exchange network of fused_top_p_sample_impl
+ * (sampling_optimized.cu:130-152) over n (a power of two) pairs, by value,
+ * descending; equal values keep whatever order the network leaves. */
+void orc_bitonic_desc(int32_t* keys, float* vals, int n);
+
+/* The sample step of fused_top_p_sample_impl (sampling_optimized.cu:154-187)
+ * on n sorted values: prob = exp(v - v[0]) / sum, cdf = inclusive sum of prob,
+ * cutoff = the first cdf whose interval [cdf - prob, cdf] holds top_p (1.0 if
+ * none), and the first position whose interval holds rand_val * cutoff
+ * (-1 if none: the reference then leaves the output unwritten).  prob and cdf
+ * (n floats each) are filled as intermediate results. */
+int orc_top_p_pick(const float* vals, int n, float top_p, float rand_val, float* prob, float* cdf);
+
 #ifdef __cplusplus
 }
 #endif

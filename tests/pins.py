@@ -349,6 +349,193 @@ def check_argmax(orc, seed=9):
     return fails
 
 
+# ---------------------------------------------------------------- top-k / top-p sampling
+def _bitrev5(x):
+    x = np.asarray(x, dtype=np.int64)
+    r = np.zeros_like(x)
+    for b in range(5):
+        r |= ((x >> b) & 1) << (4 - b)
+    return r
+
+
+def topk_closed_form(logits_bits, k_per_block):
+    """Candidates of top_k_filter in closed form.  In each of the 32 partitions
+    the valid items (value > -1e30, not NaN) are ordered by value, descending;
+    equal values are ordered the way the reference's trees resolve them: a
+    shfl_down max tree that keeps the lower slot's pair on ties makes lane bit 0
+    the most significant tie bit, then bit 1, ..., i.e. the smallest
+    bit-reversed lane wins, first over the 8 warps (warp = (i % 256) // 32),
+    then over the lanes ((i % 256) % 32), and a thread's own strided scan keeps
+    its smallest i.  The first k_per_block are taken; missing ones are
+    (start - 1, -1e30)."""
+    v = f32(logits_bits, "bf16").astype(np.float32)
+    n_all = v.size
+    keys, vals = [], []
+    for p in range(32):
+        start, end = p * n_all // 32, (p + 1) * n_all // 32
+        x = v[start:end]
+        i = np.arange(end - start)
+        ok = ~np.isnan(x) & (x > np.float32(-1e30))
+        t = i % 256
+        order = np.lexsort((i // 256, _bitrev5(t % 32), _bitrev5(t // 32), -x.astype(np.float64)))
+        order = order[ok[order]][:k_per_block]
+        kk = list(start + order) + [start - 1] * (k_per_block - order.size)
+        vv = list(x[order]) + [np.float32(-1e30)] * (k_per_block - order.size)
+        keys += kk
+        vals += vv
+    return np.array(keys, np.int32), np.array(vals, np.float32)
+
+
+def sampling_logits(n, seed, levels=None, specials=True):
+    """bf16 logits with many equal values (levels > 0 quantises them) and, with
+    specials, NaN, -inf, values <= -1e30 and a partition with few valid items."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(n) * 3.0
+    if levels:
+        x = np.round(x * levels) / levels
+    b = bits(x, "bf16")
+    if specials and n >= 64:
+        b[rng.integers(0, n, max(1, n // 500))] = 0x7fc0          # NaN
+        b[rng.integers(0, n, max(1, n // 500))] = 0xff80          # -inf
+        b[rng.integers(0, n, max(1, n // 500))] = bits(np.array([-1e30]), "bf16")[0]
+        b[rng.integers(0, n, max(1, n // 500))] = bits(np.array([-3e35]), "bf16")[0]
+        b[rng.integers(0, n, max(2, n // 200))] = 0x8000                 # -0 ties with +0
+        b[rng.integers(0, n, max(2, n // 200))] = 0x0000
+        e = n * 3 // 32                                            # partition 2: 5 valid items
+        b[2 * n // 32:e] = 0xff80
+        b[2 * n // 32:e][:: max(1, (e - 2 * n // 32) // 5)][:5] = bits(np.arange(5.0), "bf16")
+    return b
+
+
+def signed_zero_logits(n, seed):
+    """Negative logits with scattered +0 and -0: the zeros are the largest
+    values and tie with each other."""
+    rng = np.random.default_rng(seed)
+    b = bits(-np.abs(rng.standard_normal(n)) - 0.01, "bf16")
+    b[rng.integers(0, n, n // 40)] = 0x8000
+    b[rng.integers(0, n, n // 40)] = 0x0000
+    return b
+
+
+def sampling_cases(seed):
+    """(logits bits, k_per_block) cases of the filter checks."""
+    cases = [(sampling_logits(n, seed + n, levels), kpb)
+             for n, kpb, levels in ((151936, 32, 4), (151936, 4, None), (1000, 32, 2),
+                                    (40000, 8, 1), (33, 1, None), (8192, 16, 8))]
+    cases.append((signed_zero_logits(12000, seed), 32))
+    return cases
+
+
+def check_topk_filter(orc, seed=21):
+    """Oracle candidates vs the closed form (keys and value bits exact), on
+    vocabularies that are and are not multiples of 32, with ties.  Returns the
+    number of mismatching candidates."""
+    fails = 0
+    for b, kpb in sampling_cases(seed):
+        k1, v1 = orc.topk_filter(b, kpb)
+        k2, v2 = topk_closed_form(b, kpb)
+        fails += int(np.sum((k1 != k2) | (v1.view(np.uint32) != v2.view(np.uint32))))
+    return fails
+
+
+def _bitonic_recursive(keys, vals):
+    """Batcher's bitonic sort, recursive form: a block of size m at offset lo
+    sorts descending when (lo // m) is even (so every block at the top is
+    descending, its first half descending and its second ascending), then
+    merges by compare-exchanges at distance m/2, m/4, ... that swap only on a
+    strict inequality."""
+    keys, vals = list(keys), list(vals)
+
+    def merge(lo, m, down):
+        if m < 2:
+            return
+        h = m // 2
+        for i in range(lo, lo + h):
+            if (vals[i] < vals[i + h]) if down else (vals[i] > vals[i + h]):
+                keys[i], keys[i + h] = keys[i + h], keys[i]
+                vals[i], vals[i + h] = vals[i + h], vals[i]
+        merge(lo, h, down)
+        merge(lo + h, h, down)
+
+    def sort(lo, m):
+        if m < 2:
+            return
+        sort(lo, m // 2)
+        sort(lo + m // 2, m // 2)
+        merge(lo, m, (lo // m) % 2 == 0)
+
+    sort(0, len(vals))
+    return np.array(keys, np.int32), np.array(vals, np.float32)
+
+
+def check_bitonic(orc, seed=22):
+    """Oracle network vs the recursive form (exact, ties included), and the
+    output is a permutation sorted by value, descending.  Returns misses."""
+    rng = np.random.default_rng(seed)
+    fails = 0
+    for n in (32, 64, 256, 1024):
+        for levels in (None, 2, 0.25):
+            x = rng.standard_normal(n) * 3
+            if levels:
+                x = np.round(x * levels) / levels
+            vals = x.astype(np.float32)
+            keys = rng.permutation(100000)[:n].astype(np.int32)
+            k1, v1 = orc.bitonic_desc(keys, vals)
+            k2, v2 = _bitonic_recursive(keys, vals)
+            fails += int(np.sum(k1 != k2) + np.sum(v1 != v2))
+            fails += int(np.any(np.diff(v1) > 0))
+            fails += int(not np.array_equal(np.sort(k1), np.sort(keys)))
+    return fails
+
+
+def top_p_closed_form(vals, top_p, rand_val):
+    """Position picked from sorted values in f64, and the smallest distance of
+    top_p and of the target to an interval end (ties within it are not
+    decided by this form)."""
+    v = np.asarray(vals, np.float64)
+    e = np.exp(v - v[0])
+    prob = e / e.sum()
+    cdf = np.cumsum(prob)
+    prev = cdf - prob
+    hit = np.nonzero((prev < top_p) & (cdf >= top_p))[0]
+    cutoff = cdf[hit[0]] if hit.size else 1.0
+    target = rand_val * cutoff
+    win = np.nonzero((cdf >= target) & (prev < target))[0]
+    margin = min(np.min(np.abs(cdf - top_p)), np.min(np.abs(cdf - target)))
+    return (int(win[0]) if win.size else -1), margin
+
+
+def check_top_p(orc, seed=23):
+    """The sample step vs the f64 closed form where no interval end lies
+    within 1e-5 of top_p or the target, plus exact cases: a single
+    dominating candidate, an exact top_p boundary, rand 0 (no winner).
+    Returns misses."""
+    rng = np.random.default_rng(seed)
+    fails = 0
+    decided = 0
+    for n in (32, 128, 1024):
+        for _ in range(60):
+            vals = np.sort(rng.standard_normal(n).astype(np.float32) * rng.uniform(0.5, 4))[::-1]
+            vals = np.ascontiguousarray(vals)
+            top_p, r = float(rng.uniform(0.05, 1.0)), float(rng.uniform(0, 1))
+            want, margin = top_p_closed_form(vals, top_p, r)
+            if margin < 1e-5:
+                continue
+            decided += 1
+            fails += int(orc.top_p_pick(vals, top_p, r)[0] != want)
+    fails += int(decided < 150)
+    # two equal leaders, the rest negligible: prob (0.5, 0.5, 0 ...); top_p = 0.5
+    # is the first interval's end exactly, so the cutoff is 0.5 and any rand
+    # picks position 0 (a strict cutoff test would pick position 1 for rand 0.75)
+    vals = np.array([5.0, 5.0] + [-1e30] * 30, np.float32)
+    fails += int(orc.top_p_pick(vals, 0.5, 0.75)[0] != 0)
+    fails += int(orc.top_p_pick(vals, 0.9, 0.75)[0] != 1)
+    fails += int(orc.top_p_pick(vals, 0.9, 0.0)[0] != -1)          # rand 0: no winner
+    big = np.array([40.0] + [0.0] * 31, np.float32)                 # one candidate holds ~1
+    fails += int(orc.top_p_pick(big, 0.3, 0.999)[0] != 0)
+    return fails
+
+
 # ---------------------------------------------------------------- model composition
 def tiny_qwen_weights(cfg, seed, std=0.15):
     """Random weights in the fused layout (bf16 bits), larger than an HF init

@@ -189,3 +189,33 @@ def test_prefill_argument_checks(cdll):
     assert call(block_size=32) == -2
     assert call(max_ctx=0) == -1
     assert call(batch=0) == 0 and call(total=0) == 0
+
+
+def test_sort_and_sample_argument_checks(cdll):
+    """luc_sort_and_sample rejects on the host: top_k outside the built
+    candidate sizes (the reference's "Unsupported candidate size"), bf16 only,
+    a vocabulary the 32 partitions cannot cover, a short or misaligned
+    sort buffer and null pointers."""
+    def call(**kw):
+        args = dict(ctx=ctypes.c_void_p(1), stream=None, dtype=0, logits=ctypes.c_void_p(256),
+                    vocab=151936, top_p=0.9, top_k=1024, rand=0.5, buf=ctypes.c_void_p(4096),
+                    buf_bytes=8192, out=ctypes.c_void_p(64))
+        args.update(kw)
+        return cdll.luc_sort_and_sample(*args.values())
+    for k in (0, 16, 48, 2048):
+        assert call(top_k=k) == -2
+        assert b"Unsupported candidate size" in cdll.luc_last_error()
+    assert call(dtype=1) == -2
+    assert call(vocab=31) == -1 and call(vocab=32 * 16384 + 1) == -1
+    assert call(buf_bytes=8191) == -5
+    assert call(top_k=32, buf_bytes=255) == -5
+    assert call(buf=ctypes.c_void_p(4100)) == -1
+    assert call(logits=None) == -1 and call(buf=None) == -1 and call(out=None) == -1
+    assert call(ctx=None) == -1
+
+
+def test_sampler_top_k_rule():
+    """Sampler::new's normalisation (src/sampler.rs:19-23)."""
+    from lucciola_rs_amd.sampler import normalize_top_k
+    assert [normalize_top_k(k) for k in (0, 1, 32, 33, 50, 64, 100, 1000, 1024, 5000)] == \
+        [1024, 32, 32, 64, 64, 64, 128, 1024, 1024, 1024]

@@ -148,3 +148,18 @@ def test_argmax_first_of_equals_nan_and_floor(orc):
 
 def test_oracle_qwen2_loop_vs_f64_decoder(orc):
     assert pins.check_oracle_model(orc) <= 1
+
+
+def test_topk_filter_matches_closed_form(orc):
+    """Candidates of the 32-partition filter: keys and value bits equal the
+    closed-form order (value, then the reference's tree tie order), with NaN,
+    -inf, values <= -1e30, signed zeros and a short partition."""
+    assert pins.check_topk_filter(orc) == 0
+
+
+def test_bitonic_network_matches_recursive_form(orc):
+    assert pins.check_bitonic(orc) == 0
+
+
+def test_top_p_pick_matches_f64_closed_form(orc):
+    assert pins.check_top_p(orc) == 0

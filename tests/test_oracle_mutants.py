@@ -25,6 +25,9 @@ MUTANTS = {
     11: "RMSNorm mean over n - 1",
     12: "silu with exp(+x)",
     13: "argmax ties go to the last index",
+    14: "top-k filter: ties go to the higher lane in the warp trees",
+    15: "bitonic network: block directions swapped",
+    16: "top-p cutoff needs cdf strictly above top_p",
 }
 
 
@@ -44,6 +47,9 @@ def all_checks(o):
     res.append(("rmsnorm", pins.check_rmsnorm(o) <= 1))
     res.append(("silu_mul", pins.check_silu_mul(o) <= 1))
     res.append(("argmax", pins.check_argmax(o) == 0))
+    res.append(("topk_filter", pins.check_topk_filter(o) == 0))
+    res.append(("bitonic", pins.check_bitonic(o) == 0))
+    res.append(("top_p", pins.check_top_p(o) == 0))
     return res
 
 
