@@ -59,7 +59,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--eager", action="store_true", help="launch eagerly instead of a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the prefill and sampling measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (reference for PMC byte counters)")
     return ap.parse_args()
@@ -143,6 +144,45 @@ def prefill_bench(lib, torch, reps=50):
             "us_per_call": round(us, 2), "attention_flops": int(flops),
             "achieved_tflops": round(tflops, 1), "peak_tflops": PEAK_BF16_TFLOPS,
             "frac": round(tflops / PEAK_BF16_TFLOPS, 4)}
+
+
+def sampling_bench(lib, torch, reps=100):
+    """Microseconds per luc_sort_and_sample call (top-k filter + sort/sample
+    kernels) on one Qwen2.5 logits row (vocab 151936, bf16, seeded N(0,1)*4),
+    top_k 1024, top_p 0.9, replayed from a HIP graph."""
+    import numpy as np
+    from lucciola_rs_amd import workloads as wl
+
+    vocab, top_k = 151936, 1024
+    rng = np.random.default_rng(3)
+    logits = wl.bits_to_tensor(wl.to_bits(rng.standard_normal(vocab) * 4, "bf16"), "bf16").cuda()
+    buf = torch.zeros(2 * top_k, dtype=torch.int32, device="cuda")
+    idx = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def call():
+        lib.sort_and_sample(logits, 0.9, top_k, 0.37, buf, idx)
+
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            call()
+    g.replay()
+    torch.cuda.synchronize()
+    runs = []
+    for _ in range(5):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        runs.append(e0.elapsed_time(e1) * 1e3 / reps)
+    return {"call": "luc_sort_and_sample (top-k filter + bitonic sort / top-p draw)",
+            "vocab": vocab, "top_k": top_k, "top_p": 0.9,
+            "us_per_call": round(statistics.median(runs), 2)}
 
 
 def main():
@@ -242,6 +282,7 @@ def main():
             traffic = tr.get("hbm_bytes_per_launch")
 
     prefill = None if args.no_prefill else prefill_bench(lib, torch)
+    sampling = None if args.no_prefill else sampling_bench(lib, torch)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -283,6 +324,7 @@ def main():
                      "algorithmic_bytes_per_launch": int(dec_bytes)},
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "sampling": sampling,
     }
     print(json.dumps(res), flush=True)
 
