@@ -29,12 +29,19 @@
 //   the float compare treats them) in the top 16 bits, the complement of its
 //   14-bit tie rank below, and 0 for items that never count -- so "larger key
 //   first" is exactly the reference's order and keys of counted items are
-//   distinct.  Each lane sorts its NPL keys in registers; each wave then takes
-//   its k/32 largest by repeated DPP wave maxima (the winning lane shifts its
-//   sorted keys), and wave 0 repeats that over the 16 waves' lists from LDS.
-//   Sort and sample: one workgroup of max(k, 64) threads; the bitonic stages
-//   inside a wave need no workgroup barrier; sums and the inclusive scan by
-//   DPP within waves and a fixed-order pass over the wave totals.
+//   distinct.  Each lane sorts its NPL keys in registers and each wave takes
+//   its two largest (DPP wave maxima; the winning lane shifts its sorted
+//   keys).  The (k/32)-th largest of those 32 keys bounds the partition's k/32
+//   largest from below; the items at or above it are gathered in LDS and each
+//   is ranked by counting the larger ones.  When more than 1024 items pass the
+//   bound (the largest values crowded into few waves), each wave takes its
+//   k/32 largest in order instead and wave 0 takes the k/32 largest of the 16
+//   lists.
+//   Sort and sample: one workgroup of max(k, 64) threads, candidate t in lane
+//   t.  Bitonic stages whose pairs lie inside a wave run in registers (DPP
+//   and lane permutes); the stages across waves exchange through LDS with one
+//   barrier each.  Sums and the inclusive scan by DPP within waves and a
+//   fixed-order pass over the wave totals.
 #include "luc_common.h"
 
 namespace luc {
@@ -65,6 +72,14 @@ __device__ inline int key_index(uint32_t k) {
   const uint32_t rank = 0x3fffu - (k & 0xffffu);
   const uint32_t t = (bitrev3((rank >> 11) & 7u) << 5) | bitrev5((rank >> 6) & 31u);
   return (int)(((rank & 63u) << 8) | t);
+}
+
+// bf16 bits of a counted item from its key; a zero key value stands for
+// both +0 and -0, so those are read back from the row.
+__device__ inline uint16_t item_bits(uint32_t k, const uint16_t* row) {
+  const uint32_t ord = k >> 16;
+  if (ord == 0x8000u) return row[key_index(k)];
+  return (uint16_t)((ord & 0x8000u) ? (ord & 0x7fffu) : (~ord & 0xffffu));
 }
 
 // Wave-uniform maximum of an unsigned value over the 64 lanes (the DPP chain
@@ -112,25 +127,104 @@ __device__ __attribute__((always_inline)) inline void wave_take(uint32_t (&k)[N]
   }
 }
 
+// Index of the first lane with pred set (64 when none).
+__device__ inline int first_lane(bool pred) {
+  const uint64_t b = __builtin_amdgcn_ballot_w64(pred);
+  return b ? __builtin_ctzll(b) : 64;
+}
+
+// Inclusive integer sum over the lanes of the wave (lane l gets lanes 0..l).
+__device__ inline int wave_inclusive_sum_i(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return x;
+}
+
 template <int NPL>
 __device__ void topk_filter_impl(const uint16_t* x, int vocab, int kpp, int2* cand) {
+  constexpr int kFast = kFilterThreads;  // items the threshold path ranks at most
   __shared__ uint32_t s_list[kFilterWaves][kMaxPerPart];
   __shared__ uint32_t s_win[kMaxPerPart];
+  __shared__ uint2 s_sel[kFast];         // (key, bf16 bits) of the items >= the threshold
+  __shared__ uint32_t s_thr, s_nsel;
   const int p = blockIdx.x;
   const int start = (int)((int64_t)p * vocab / kParts);
   const int n = (int)((int64_t)(p + 1) * vocab / kParts) - start;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  // every load before any use (one memory round trip); indices past the
+  // partition re-read its last item and are dropped below
+  uint16_t h[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) h[j] = x[start + min(t + kFilterThreads * j, n - 1)];
   uint32_t k[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     const int i = t + kFilterThreads * j;
-    k[j] = i < n ? item_key(x[start + i], i) : 0u;
+    k[j] = i < n ? item_key(h[j], i) : 0u;
   }
   sort_desc<NPL>(k);
+  uint32_t kk[NPL];  // the sorted keys, kept for the general path
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) kk[j] = k[j];
+
+  // Threshold: the kpp-th largest of the 16 waves' two largest keys (32
+  // distinct items, so at least kpp items lie at or above it and the
+  // partition's kpp largest all do).
+  wave_take<NPL>(k, 2, s_list[w], lane);
+  if (t == 0) s_nsel = 0u;
+  __syncthreads();
+  if (w == 0) {
+    const uint32_t y = lane < 2 * kFilterWaves ? s_list[lane >> 1][lane & 1] : 0u;
+    int rank = 0;  // keys larger than this lane's (distinct unless 0)
+#pragma unroll
+    for (int m = 0; m < 2 * kFilterWaves; ++m)
+      rank += (uint32_t)__builtin_amdgcn_readlane((int)y, m) > y ? 1 : 0;
+    const int at = first_lane(lane < 2 * kFilterWaves && y != 0u && rank == kpp - 1);
+    const uint32_t thr = at < 64 ? (uint32_t)__builtin_amdgcn_readlane((int)y, at & 63) : 1u;
+    if (lane == 0) s_thr = thr;
+  }
+  __syncthreads();
+  const uint32_t thr = s_thr;
+  // gather the items at or above the threshold: a lane's are its first c keys
+  int c = 0;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) c += kk[j] >= thr ? 1 : 0;
+  const int incl = wave_inclusive_sum_i(c);
+  uint32_t wbase = 0;
+  if (lane == 63) wbase = atomicAdd(&s_nsel, (uint32_t)incl);
+  wbase = (uint32_t)__builtin_amdgcn_readlane((int)wbase, 63);
+  const uint32_t mine = wbase + (uint32_t)(incl - c);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    if (j < c && mine + j < (uint32_t)kFast)
+      s_sel[mine + j] = make_uint2(kk[j], (uint32_t)item_bits(kk[j], x + start));
+  }
+  __syncthreads();
+  const int nsel = (int)s_nsel;
+  if (nsel <= kFast) {
+    // rank each gathered item among the gathered ones (keys are distinct);
+    // the kpp largest land at their rank, missing ones are (start - 1, -1e30)
+    if (t < nsel) {
+      const uint2 me = s_sel[t];
+      int rank = 0;
+      for (int m = 0; m < nsel; ++m) rank += s_sel[m].x > me.x ? 1 : 0;
+      if (rank < kpp)
+        cand[p * kpp + rank] = make_int2(start + key_index(me.x), __float_as_int(St<kBF16>::load((uint16_t)me.y)));
+    }
+    if (t >= nsel && t < kpp) cand[p * kpp + t] = make_int2(start - 1, __float_as_int(-1e30f));
+    return;
+  }
+  // General path (many items at or above the threshold): each wave takes its
+  // kpp largest in order, then wave 0 the kpp largest of the 16 lists.
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) k[j] = kk[j];
   wave_take<NPL>(k, kpp, s_list[w], lane);
   __syncthreads();
   if (w != 0) return;
-  // wave 0: the partition's kpp largest of the 16 lists (16 * kpp <= 512 keys)
   uint32_t k2[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -142,12 +236,10 @@ __device__ void topk_filter_impl(const uint16_t* x, int vocab, int kpp, int2* ca
   wave_lds_sync();
   if (lane < kpp) {
     const uint32_t m = s_win[lane];
-    int2 c = make_int2(start - 1, __float_as_int(-1e30f));
-    if (m != 0u) {  // the value itself (a -0 keeps its sign)
-      const int i = key_index(m);
-      c = make_int2(start + i, __float_as_int(St<kBF16>::load(x[start + i])));
-    }
-    cand[p * kpp + lane] = c;
+    int2 cv = make_int2(start - 1, __float_as_int(-1e30f));
+    if (m != 0u)  // the value itself (a -0 keeps its sign)
+      cv = make_int2(start + key_index(m), __float_as_int(St<kBF16>::load(item_bits(m, x + start))));
+    cand[p * kpp + lane] = cv;
   }
 }
 
@@ -162,49 +254,92 @@ __device__ inline float wave_inclusive_sum(float x) {
   return x;
 }
 
-// Index of the first lane with pred set (64 when none).
-__device__ inline int first_lane(bool pred) {
-  const uint64_t b = __builtin_amdgcn_ballot_w64(pred);
-  return b ? __builtin_ctzll(b) : 64;
+// Value of lane (this lane ^ J), J < 64: DPP within a row for J <= 8 (quad
+// permutes, or a row shift in the direction of the partner), a lane permute
+// through the LDS crossbar for 16 and 32.
+template <int J>
+__device__ inline int xor_lane(int v, int lane) {
+  if constexpr (J == 1) {
+    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (J == 2) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (J == 4 || J == 8) {
+    const int up = __builtin_amdgcn_update_dpp(0, v, 0x100 + J, 0xF, 0xF, false);  // row_shl:J
+    const int dn = __builtin_amdgcn_update_dpp(0, v, 0x110 + J, 0xF, 0xF, false);  // row_shr:J
+    return (lane & J) ? dn : up;
+  } else {
+    return __shfl_xor(v, J, 64);
+  }
+}
+
+// One compare-exchange stage of the reference's bitonic network (block k,
+// distance j): element t and its partner t ^ j; the block sorts descending
+// when (t & k) == 0; the pair swaps only on a strict inequality.  This lane
+// holds element t as (key, value bits) and keeps its side of the outcome.
+__device__ inline void bitonic_pick(int t, int k, int j, int& key, int& val, int pkey, int pval) {
+  const bool lower = (t & j) == 0;
+  const float mine = __int_as_float(val), other = __int_as_float(pval);
+  const float a = lower ? mine : other, b = lower ? other : mine;  // elements (lo, hi)
+  const bool swap = (t & k) == 0 ? a < b : a > b;
+  key = swap ? pkey : key;
+  val = swap ? pval : val;
+}
+
+template <int J>
+__device__ __attribute__((always_inline)) inline void stage_in_wave(int t, int k, int lane, int& key,
+                                                                    int& val) {
+  const int pk = xor_lane<J>(key, lane), pv = xor_lane<J>(val, lane);
+  bitonic_pick(t, k, J, key, val, pk, pv);
 }
 
 template <int N>
 __device__ void top_p_sample_impl(int2* cand, float top_p, float rand_val, uint32_t* out) {
   constexpr int NT = N < 64 ? 64 : N;
   constexpr int NW = NT / 64;
-  __shared__ int2 s[N];
-  __shared__ float s_wsum[NW], s_wtot[NW], s_wcut[NW];
+  __shared__ int2 s_x[2][N > 64 ? N : 1];  // cross-wave stages, double-buffered
+  __shared__ float s_wsum[NW], s_wtot[NW], s_wcut[NW], s_max;
   __shared__ int s_wcut_at[NW], s_wwin_at[NW];
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const bool act = t < N;
-  if (act) s[t] = cand[t];
-  __syncthreads();
-  // the reference's network (sampling_optimized.cu:130-152); a stage whose
-  // pairs cross waves (j >= 64), or that precedes one, ends in a workgroup
-  // barrier, the others only order the wave's own LDS accesses
+  int key = 0, val = 0;
+  if (act) {
+    const int2 c = cand[t];
+    key = c.x;
+    val = c.y;
+  }
+  // the reference's network (sampling_optimized.cu:130-152), element t in
+  // lane t: stages with j < 64 stay inside the wave, the others exchange
+  // through LDS with one barrier each
+  int buf = 0;
 #pragma unroll
   for (int k = 2; k <= N; k <<= 1) {
 #pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
-      const int x = t ^ j;
-      if (act && x > t) {
-        const int2 a = s[t], b = s[x];
-        const float av = __int_as_float(a.y), bv = __int_as_float(b.y);
-        if ((t & k) == 0 ? av < bv : av > bv) {
-          s[t] = b;
-          s[x] = a;
+      if constexpr (N > 64) {
+        if (j >= 64) {
+          if (act) s_x[buf][t] = make_int2(key, val);
+          __syncthreads();
+          const int2 o = act ? s_x[buf][t ^ j] : make_int2(0, 0);
+          buf ^= 1;
+          bitonic_pick(t, k, j, key, val, o.x, o.y);
+          continue;
         }
       }
-      const int jn = j > 1 ? j >> 1 : k;  // the next stage's distance
-      if (j >= 64 || jn >= 64) __syncthreads();
-      else wave_lds_sync();
+      switch (j) {
+        case 1: stage_in_wave<1>(t, k, lane, key, val); break;
+        case 2: stage_in_wave<2>(t, k, lane, key, val); break;
+        case 4: stage_in_wave<4>(t, k, lane, key, val); break;
+        case 8: stage_in_wave<8>(t, k, lane, key, val); break;
+        case 16: stage_in_wave<16>(t, k, lane, key, val); break;
+        default: stage_in_wave<32>(t, k, lane, key, val); break;
+      }
     }
   }
-  if constexpr (N <= 64) __syncthreads();
-  const int2 me = act ? s[t] : make_int2(0, 0);
-  if (act) cand[t] = me;  // the sorted candidates go back to the buffer
-  const float maxv = __int_as_float(s[0].y);
-  const float e = act ? expf(__int_as_float(me.y) - maxv) : 0.0f;
+  if (act) cand[t] = make_int2(key, val);  // the sorted candidates go back to the buffer
+  if (t == 0) s_max = __int_as_float(val);
+  __syncthreads();
+  const float maxv = s_max;
+  const float e = act ? expf(__int_as_float(val) - maxv) : 0.0f;
   const float ws = wave_sum(e);
   if (lane == 0) s_wsum[w] = ws;
   __syncthreads();
@@ -238,7 +373,7 @@ __device__ void top_p_sample_impl(int2* cand, float top_p, float rand_val, uint3
   int first_w = NW;
 #pragma unroll
   for (int v = NW - 1; v >= 0; --v) first_w = s_wwin_at[v] < 64 ? v : first_w;
-  if (w == first_w && lane == fw) out[0] = (uint32_t)me.x;
+  if (w == first_w && lane == fw) out[0] = (uint32_t)key;
 }
 
 }  // namespace luc

@@ -423,6 +423,16 @@ def sampling_cases(seed):
              for n, kpb, levels in ((151936, 32, 4), (151936, 4, None), (1000, 32, 2),
                                     (40000, 8, 1), (33, 1, None), (8192, 16, 8))]
     cases.append((signed_zero_logits(12000, seed), 32))
+    # every logit equal: the order is the tie order alone, and with 32 per
+    # partition more than 1024 items of a partition tie with the 32nd
+    cases.append((bits(np.ones(32 * 4748), "bf16"), 32))
+    # the largest values of every partition crowded into the items whose
+    # partition-local index is below 64 modulo 1024
+    rng = np.random.default_rng(seed + 1)
+    x = rng.standard_normal(32 * 4748) - 5.0
+    loc = np.arange(32 * 4748) % 4748
+    x[loc % 1024 < 64] += 15.0
+    cases.append((bits(x, "bf16"), 32))
     return cases
 
 
