@@ -66,13 +66,15 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(cfg, seed, budget_s=10.0):
-    """Time the oracle's decode step (one layer, the whole batch) on the host."""
+def cpu_baseline(cfg, seed, budget_s=10.0, threads=None):
+    """Time the oracle's decode step (one layer, the whole batch) on the host
+    with `threads` OpenMP threads (default: OMP_NUM_THREADS, else up to 16)."""
     import oracle
     from lucciola_rs_amd import workloads as wl
     from lucciola_rs_amd.engine import sm_scale
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+    if threads is None:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
     h = wl.host_decode_inputs(cfg, seed, num_layers=1, poison=False)
     orc = oracle.get()
     cos, sin = orc.rope_table(cfg.ctx_hi + 1, cfg.head_dim, cfg.rope_theta)
@@ -293,6 +295,12 @@ def main():
                "sample": (f"one full layer step of {cfg.name} (B={cfg.batch}, RoPE + append + "
                           f"attention of every sequence), oracle C restatement with OpenMP, "
                           f"median of {cb['reps']} runs, {cb['t'] * 1e3:.1f} ms/step")}
+        if cb["threads"] > 1:
+            c1 = cpu_baseline(cfg, args.seed, budget_s=8.0, threads=1)
+            cpu["single_core"] = {"value": round(cpu_bytes / c1["t"] / 1e9, 3), "unit": "GB/s",
+                                  "cores": 1, "sample": (f"the same step on one thread, median of "
+                                                         f"{c1['reps']} runs, "
+                                                         f"{c1['t'] * 1e3:.1f} ms/step")}
 
     res = {
         "metric": "paged decode attn: µs/step + achieved HBM GB/s (% peak) at B=32, 1 MI355X",
