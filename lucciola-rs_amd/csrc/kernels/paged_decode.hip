@@ -30,10 +30,11 @@
 //   one tile (a split of 4 tiles); the _t2 kernels walk two tiles at a time,
 //   tile i computed while tile i+1 lands.
 //   Prologue: the wave's block-table entries come through the scalar cache;
-//   in the single-tile kernels q (or, in the step variant, q, k, v, their
-//   biases and the cos/sin rows) arrive by direct-to-LDS loads issued between
-//   the tile's K and V loads, so no vector-memory round trip precedes the KV
-//   stream.  q is then held in 2G registers, spread so that DPP row_newbcast
+//   in the single-tile kernels q arrives by direct-to-LDS loads issued between
+//   the tile's K and V loads, and the step variant's operands (q, k, v, their
+//   biases and the cos/sin rows: one block per workgroup, loaded by wave 0)
+//   by direct-to-LDS loads issued just before wave 0's K tile, so no
+//   vector-memory round trip precedes the KV stream.  q is then held in 2G registers, spread so that DPP row_newbcast
 //   hands every lane the q word it needs as an operand of v_dot2c.
 //   Per tile:
 //     1. K goes straight from HBM into LDS (global_load_lds_dwordx4; one
@@ -423,11 +424,12 @@ __device__ void decode_impl(const DecodeArgs& A) {
   constexpr int WS = W * S::TILE;  // tokens between two tiles of one wave
   // Single-tile kernels (T1): no vector-memory round trip before the KV
   // stream.  The wave's page numbers come through the scalar cache, and q
-  // (FASTQ), or the step variant's operands (FASTA: q, k, v, their biases,
-  // the cos/sin rows), by 4-byte direct-to-LDS loads issued between the
-  // tile's K and V loads (behind the same K wait), instead of vector loads
-  // that would queue behind the KV streams other waves of the CU have
-  // already issued.
+  // (FASTQ) by 4-byte direct-to-LDS loads issued between the tile's K and V
+  // loads (behind the same K wait), or the step variant's operands (FASTA:
+  // q, k, v, their biases, the cos/sin rows) by such loads issued by wave 0
+  // just before its K tile (so its RoPE, which every wave waits for, does
+  // not wait for the tile), instead of vector loads that would queue behind
+  // the KV streams other waves of the CU have already issued.
   constexpr bool T1 = NB == 1;
   constexpr bool FASTQ = T1 && !APPEND;
   constexpr bool FASTA = T1 && APPEND;
@@ -608,19 +610,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
   };
   auto issue_k = [&](int t0, int buf) __attribute__((always_inline)) {
     lds_char* kdma = (lds_char*)s_k[w][buf];
-#pragma unroll
-    for (int r = 0; r < S::LOADS; ++r) {
-      const int64_t phys = phys_of(t0, r);
-      // wave-uniform slab base (scalar registers) + 32-bit lane offsets
-      const char* kslab = (const char*)(A.k_pool + phys * page_stride + head_off);
-      dma16(kslab + ((r & 1) ? koff1 : koff0), kdma + (r - r % S::LPP) * 1024,
-            (r % S::LPP) * 1024);
-    }
-    if constexpr (FASTQ) {
-#pragma unroll
-      for (int i = 0; i < NQ; ++i)
-        dma4((const char*)qrow + min(i * 256 + lane * 4, GD * 2 - 4), (lds_char*)s_qr[w] + i * 256);
-    }
+    // wave 0's operand block goes out first, so that the RoPE which every
+    // wave waits for needs only these loads, not the wave's K tile behind them
     if (FASTA && w == 0) {
       // the workgroup's operand block (wave 0 only); a missing bias reads the
       // operand itself (ignored)
@@ -648,6 +639,19 @@ __device__ void decode_impl(const DecodeArgs& A) {
         for (int k = 1; k < 6; ++k) src = reg == k ? small[k] : src;
         dma4(src + (o - reg * SR), pa + PA_SM + i * 256);
       }
+    }
+#pragma unroll
+    for (int r = 0; r < S::LOADS; ++r) {
+      const int64_t phys = phys_of(t0, r);
+      // wave-uniform slab base (scalar registers) + 32-bit lane offsets
+      const char* kslab = (const char*)(A.k_pool + phys * page_stride + head_off);
+      dma16(kslab + ((r & 1) ? koff1 : koff0), kdma + (r - r % S::LPP) * 1024,
+            (r % S::LPP) * 1024);
+    }
+    if constexpr (FASTQ) {
+#pragma unroll
+      for (int i = 0; i < NQ; ++i)
+        dma4((const char*)qrow + min(i * 256 + lane * 4, GD * 2 - 4), (lds_char*)s_qr[w] + i * 256);
     }
   };
   auto issue_v = [&](int t0, uint4(&vr)[S::LOADS]) __attribute__((always_inline)) {
@@ -875,7 +879,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       // j + 1 and j + D/2, j + D/2 + 1) from the operand block; v + v_bias.
       // Every wave, with or without a tile, meets it at the barrier.
       if (w == 0) {
-        LUC_WAIT_VM(8);  // K and the operand block
+        LUC_WAIT_VM(16);  // the operand block (the tile's K and V may be in flight)
         const uint32_t pa = lds_addr(s_pa[0]);
         constexpr int NP2 = (G + 1) * HD / 2;
         const bool hqb = A.q_bias != nullptr, hkb = A.k_bias != nullptr, hvb = A.v_bias != nullptr;
