@@ -149,7 +149,10 @@ __device__ void topk_filter_impl(const uint16_t* x, int vocab, int kpp, int2* ca
   constexpr int kFast = kFilterThreads;  // items the threshold path ranks at most
   __shared__ uint32_t s_list[kFilterWaves][kMaxPerPart];
   __shared__ uint32_t s_win[kMaxPerPart];
-  __shared__ uint2 s_sel[kFast];         // (key, bf16 bits) of the items >= the threshold
+  // keys and bf16 bits of the items at or above the threshold; unused keys
+  // stay 0, below every counted key, so the ranking reads whole 16-byte rows
+  __shared__ __attribute__((aligned(16))) uint32_t s_selk[kFast];
+  __shared__ uint16_t s_selb[kFast];
   __shared__ uint32_t s_thr, s_nsel;
   const int p = blockIdx.x;
   const int start = (int)((int64_t)p * vocab / kParts);
@@ -176,6 +179,7 @@ __device__ void topk_filter_impl(const uint16_t* x, int vocab, int kpp, int2* ca
   // partition's kpp largest all do).
   wave_take<NPL>(k, 2, s_list[w], lane);
   if (t == 0) s_nsel = 0u;
+  s_selk[t] = 0u;
   __syncthreads();
   if (w == 0) {
     const uint32_t y = lane < 2 * kFilterWaves ? s_list[lane >> 1][lane & 1] : 0u;
@@ -200,8 +204,10 @@ __device__ void topk_filter_impl(const uint16_t* x, int vocab, int kpp, int2* ca
   const uint32_t mine = wbase + (uint32_t)(incl - c);
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    if (j < c && mine + j < (uint32_t)kFast)
-      s_sel[mine + j] = make_uint2(kk[j], (uint32_t)item_bits(kk[j], x + start));
+    if (j < c && mine + j < (uint32_t)kFast) {
+      s_selk[mine + j] = kk[j];
+      s_selb[mine + j] = item_bits(kk[j], x + start);
+    }
   }
   __syncthreads();
   const int nsel = (int)s_nsel;
@@ -209,11 +215,16 @@ __device__ void topk_filter_impl(const uint16_t* x, int vocab, int kpp, int2* ca
     // rank each gathered item among the gathered ones (keys are distinct);
     // the kpp largest land at their rank, missing ones are (start - 1, -1e30)
     if (t < nsel) {
-      const uint2 me = s_sel[t];
+      const uint32_t me = s_selk[t];
+      const uint4* rows = (const uint4*)s_selk;
       int rank = 0;
-      for (int m = 0; m < nsel; ++m) rank += s_sel[m].x > me.x ? 1 : 0;
+#pragma unroll 4
+      for (int m = 0; m < (nsel + 3) >> 2; ++m) {
+        const uint4 r = rows[m];
+        rank += (r.x > me) + (r.y > me) + (r.z > me) + (r.w > me);
+      }
       if (rank < kpp)
-        cand[p * kpp + rank] = make_int2(start + key_index(me.x), __float_as_int(St<kBF16>::load((uint16_t)me.y)));
+        cand[p * kpp + rank] = make_int2(start + key_index(me), __float_as_int(St<kBF16>::load(s_selb[t])));
     }
     if (t >= nsel && t < kpp) cand[p * kpp + t] = make_int2(start - 1, __float_as_int(-1e30f));
     return;
