@@ -207,3 +207,29 @@ def test_greedy_from_checkpoint_second_shape(orc, tmp_path):
         ids = [g]
     say(f"  identical for {len(tokens)} of 49 tokens; distinct: {len(set(tokens))}")
     assert len(tokens) >= 24
+
+
+def test_sample_token_dispatch(orc, qwen):
+    """Qwen2Model.sample_token (models.rs:385-432) on the model's own logits:
+    temperature 0 is luc_argmax; top_p < 1 draws, with the sampler's first
+    random value, the token the oracle's apply_sort_and_sample draws from the
+    same logits (checked where no interval end lies within 1e-5 of top_p or
+    the target; always among the oracle's candidates)."""
+    import pins
+    from lucciola_rs_amd.sampler import Sampler
+    cfg, gpu, _ = qwen
+    rng = np.random.default_rng(23)
+    gpu.forward(rng.integers(0, cfg.vocab_size, 5).tolist(), 0)
+    bits = from_dev(gpu.logits())[0]
+    say("  [gpu] sample_token: greedy and top-p on the model's logits")
+    assert gpu.sample_token(Sampler(temperature=0.0)) == gpu.sample_greedy()
+    decided = 0
+    for seed in range(12):
+        rand = Sampler(seed=seed).next_rand()
+        tok = gpu.sample_token(Sampler(seed=seed, temperature=0.7, top_p=0.9, top_k=50))
+        want = orc.sort_and_sample(bits, 0.9, 64, rand)
+        assert tok in set(want["keys"].tolist())
+        if pins.top_p_closed_form(want["vals"], 0.9, rand)[1] > 1e-5:
+            decided += 1
+            assert tok == want["token"]
+    assert decided >= 6
