@@ -46,6 +46,7 @@ sys.path.insert(0, ROOT)
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_batch32_mixed_traffic.json")
+MFMA_FILE = os.path.join(ROOT, "profiles", "prefill_4x2048_mfma.json")
 
 
 def parse():
@@ -145,7 +146,16 @@ def prefill_bench(lib, torch, reps=50):
             "call": "luc_paged_prefill (RoPE + append kernel, causal attention kernel)",
             "us_per_call": round(us, 2), "attention_flops": int(flops),
             "achieved_tflops": round(tflops, 1), "peak_tflops": PEAK_BF16_TFLOPS,
-            "frac": round(tflops / PEAK_BF16_TFLOPS, 4)}
+            "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "mfma_busy_frac": mfma_busy()}
+
+
+def mfma_busy():
+    """Fraction of SIMD cycles with the matrix cores busy during the prefill
+    attention kernel, from the committed rocprofv3 PMC summary (or None)."""
+    if not os.path.exists(MFMA_FILE):
+        return None
+    with open(MFMA_FILE) as f:
+        return json.load(f).get("mfma_busy_frac")
 
 
 def sampling_bench(lib, torch, reps=100):
