@@ -874,18 +874,23 @@ __device__ void decode_impl(const DecodeArgs& A) {
   if constexpr (NB == 1) {
     // at most one tile per wave (the split is W tiles)
     if constexpr (FASTA) {
-      // wave 0 (it always has a tile) ropes the workgroup's operands: bias +
-      // RoPE of q (G heads) and k of the new token, in dword pairs (dims j,
-      // j + 1 and j + D/2, j + D/2 + 1) from the operand block; v + v_bias.
-      // Every wave, with or without a tile, meets it at the barrier.
-      if (w == 0) {
-        LUC_WAIT_VM(16);  // the operand block (the tile's K and V may be in flight)
+      // The workgroup's operands are roped by all its waves.  Wave 0 (it
+      // always has a tile) waits for the operand block it loaded and a barrier
+      // hands the block to every wave; thread t then ropes the dword pairs t,
+      // t + 64W, ... (bias + RoPE of q (G heads) and k of the new token: dims
+      // j, j + 1 and j + D/2, j + D/2 + 1), the last D/2 threads also
+      // v + v_bias, and a second barrier hands the results to every wave.
+      // Every wave, with or without a tile, meets both barriers.
+      if (w == 0) LUC_WAIT_VM(16);  // the operand block (the tile's K and V may be in flight)
+      __builtin_amdgcn_s_barrier();
+      {
         const uint32_t pa = lds_addr(s_pa[0]);
         constexpr int NP2 = (G + 1) * HD / 2;
+        constexpr int NT = 64 * W;
         const bool hqb = A.q_bias != nullptr, hkb = A.k_bias != nullptr, hvb = A.v_bias != nullptr;
 #pragma unroll
-        for (int i = 0; i < (NP2 + 63) / 64; ++i) {
-          const int idx = lane + 64 * i;
+        for (int i = 0; i < (NP2 + NT - 1) / NT; ++i) {
+          const int idx = (int)threadIdx.x + NT * i;
           if (idx < NP2) {
             const int g = idx / (HD / 2), j = (idx % (HD / 2)) * 2;
             const uint32_t xb = pa + (g < G ? PA_XQ + g * D * 2 : PA_K);
@@ -911,15 +916,16 @@ __device__ void decode_impl(const DecodeArgs& A) {
             }
           }
         }
-        if (lane < D / 2) {
+        const int vt = (int)threadIdx.x - (NT - D / 2);  // v word of the last D/2 threads
+        if (vt >= 0) {
           uint32_t vv, vbv;
-          lds_read2(pa + PA_V + lane * 4, pa + PA_VB + lane * 4, vv, vbv);
+          lds_read2(pa + PA_V + vt * 4, pa + PA_VB + vt * 4, vv, vbv);
           if (!hvb) vbv = 0u;
           const uint16_t lo = St<DT>::store(St<DT>::load(vv & 0xffff) + St<DT>::load(vbv & 0xffff));
           const uint16_t hi = St<DT>::store(St<DT>::load(vv >> 16) + St<DT>::load(vbv >> 16));
-          *(uint32_t*)(s_vnew[qi] + 2 * lane) = (uint32_t)lo | ((uint32_t)hi << 16);
+          *(uint32_t*)(s_vnew[qi] + 2 * vt) = (uint32_t)lo | ((uint32_t)hi << 16);
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // its LDS writes are done
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this thread's LDS writes are done
       }
       __builtin_amdgcn_s_barrier();
     }
