@@ -23,13 +23,17 @@ Also reported:
                 `traffic` is the HBM bytes per launch read from the committed
                 rocprofv3 PMC summary, if present;
   cpu_baseline  the oracle (C restatement of the reference's attention, OpenMP)
-                on one full layer step of the same workload on the host;
+                on one full layer step of the same workload on the host, on up to
+                16 threads and (single_core) on one;
   prefill       luc_paged_prefill on prefill_4x2048 (4 prompts x 2048 rows from
                 an empty cache, 14q/2kv, d=64, bf16): RoPE + cache append
                 kernel, then the causal attention kernel on bf16 MFMA; time per
                 call (HIP events over a graph of back-to-back calls) and the
                 attention's algorithmic FLOP rate against the 2.5 PFLOP/s dense
-                bf16 peak.
+                bf16 peak; mfma_busy_frac is the share of SIMD cycles with the
+                matrix cores busy, from the committed rocprofv3 PMC summary;
+  sampling      luc_sort_and_sample on one logits row (vocab 151936, top_k
+                1024): time per call.
 """
 from __future__ import annotations
 
