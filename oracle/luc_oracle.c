@@ -8,8 +8,10 @@
  * Where the reference's CUDA source has a multiply-add that NVRTC contracts by
  * default (build.rs:32-40 uses default CompileOptions, i.e. --fmad=true), the
  * restatement writes fmaf() explicitly; where the contraction is ambiguous the
- * choice is noted.  Those choices, and CUDA's expf versus glibc's expf, are
- * the parts no available reference output pins.
+ * choice is noted.  Those choices, CUDA's expf versus glibc's expf, and the
+ * summation order of CUB's BlockReduce/BlockScan in the top-p draw (CUB is not
+ * in the reference's sources; orc_top_p_pick sums in index order) are the
+ * parts no available reference output pins: parity unpinned.
  *
  * ORC_MUTANT (compile-time, 0 = off) plants one known mistake; the test suite
  * builds each mutant and checks that its pinning checks reject it.
