@@ -3,6 +3,7 @@ rejected by at least one of the pinning checks in tests/pins.py.  This shows
 the checks pin the oracle rather than restate it."""
 import os
 import subprocess
+import sys
 
 import pytest
 
@@ -58,11 +59,30 @@ def test_unmutated_oracle_passes_all(orc):
     assert not failed, failed
 
 
+# The checks of one mutant run in a child process: a planted indexing mistake
+# can write outside the oracle's buffers and crash the process that runs it,
+# which counts as caught (the unmutated oracle runs in-process above).
+_CHILD = """
+import sys
+sys.path[:0] = {paths!r}
+import oracle
+import test_oracle_mutants as t
+failed = [n for n, ok in t.all_checks(oracle.Oracle({so!r})) if not ok]
+print("FAILED_CHECKS", ",".join(failed))
+"""
+
+
 @pytest.mark.parametrize("mutant", sorted(MUTANTS))
 def test_mutant_is_caught(mutant, tmp_path):
     so = tmp_path / f"mutant{mutant}.so"
     subprocess.run(["gcc", "-O2", "-std=c11", "-fPIC", "-fopenmp", "-ffp-contract=off",
                     f"-DORC_MUTANT={mutant}", "-shared", "-o", str(so), SRC, "-lm"], check=True)
-    o = oracle.Oracle(str(so))
-    failed = [n for n, ok in all_checks(o) if not ok]
+    here = os.path.dirname(os.path.abspath(__file__))
+    code = _CHILD.format(paths=[here, os.path.dirname(here)], so=str(so))
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=600)
+    if res.returncode < 0:
+        return  # killed by a signal (an out-of-bounds write crashed the checks): caught
+    assert res.returncode == 0, res.stderr[-3000:]
+    line = [l for l in res.stdout.splitlines() if l.startswith("FAILED_CHECKS")][-1]
+    failed = [n for n in line.split(" ", 1)[1].split(",") if n]
     assert failed, f"mutant {mutant} ({MUTANTS[mutant]}) passed every check"
