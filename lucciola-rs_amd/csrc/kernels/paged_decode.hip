@@ -608,13 +608,14 @@ __device__ void decode_impl(const DecodeArgs& A) {
     if constexpr (T1) return tpage[r / S::LPP];  // (t0 is the wave's only tile)
     else return page_of(min((t0 - s_begin) / kPage + r / S::LPP, jend));
   };
-  auto issue_k = [&](int t0, int buf) __attribute__((always_inline)) {
-    lds_char* kdma = (lds_char*)s_k[w][buf];
-    // wave 0's operand block goes out first, so that the RoPE which every
-    // wave waits for needs only these loads, not the wave's K tile behind them
-    if (FASTA && w == 0) {
-      // the workgroup's operand block (wave 0 only); a missing bias reads the
-      // operand itself (ignored)
+  // Issued by every wave, with or without a tile, before its K tile.
+  auto issue_operands = [&]() __attribute__((always_inline)) {
+    // The workgroup's operand block goes out first, so that the RoPE which
+    // every wave waits for needs only these loads, not the K tiles behind
+    // them; its 4-byte loads are dealt round robin over the waves (load i by
+    // wave i % W), so no wave's K tile waits behind all of them.
+    if constexpr (FASTA) {
+      // a missing bias reads the operand itself (ignored)
       const char* krow = (const char*)(A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D);
       const char* vrow = (const char*)(A.v_new + (int64_t)b * A.q_stride + (int64_t)h * D);
       const char* qb = A.q_bias ? (const char*)(A.q_bias + (int64_t)h * GD) : (const char*)qrow;
@@ -626,8 +627,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
         const int off = min(i * 256 + lane * 4, GD * 2 - 4);
-        dma4((const char*)qrow + off, pa + PA_XQ + i * 256);
-        dma4(qb + off, pa + PA_BQ + i * 256);
+        if ((2 * i) % W == w) dma4((const char*)qrow + off, pa + PA_XQ + i * 256);
+        if ((2 * i + 1) % W == w) dma4(qb + off, pa + PA_BQ + i * 256);
       }
       const char* small[6] = {krow, kb, cr, sr, vrow, vb};
 #pragma unroll
@@ -637,9 +638,12 @@ __device__ void decode_impl(const DecodeArgs& A) {
         const char* src = small[0];
 #pragma unroll
         for (int k = 1; k < 6; ++k) src = reg == k ? small[k] : src;
-        dma4(src + (o - reg * SR), pa + PA_SM + i * 256);
+        if ((2 * NQ + i) % W == w) dma4(src + (o - reg * SR), pa + PA_SM + i * 256);
       }
     }
+  };
+  auto issue_k = [&](int t0, int buf) __attribute__((always_inline)) {
+    lds_char* kdma = (lds_char*)s_k[w][buf];
 #pragma unroll
     for (int r = 0; r < S::LOADS; ++r) {
       const int64_t phys = phys_of(t0, r);
@@ -687,6 +691,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
     // every wave's K (and q) goes out before any wave's V: the CU's memory
     // pipeline returns them roughly in that order, so the scores of all the
     // waves overlap the V stream and only PV is left once the last V lands
+    issue_operands();
     if (ntw > 0) issue_k(t_first, 0);
     __builtin_amdgcn_s_barrier();
     if (ntw > 0) issue_v(t_first, vr0);
@@ -874,14 +879,16 @@ __device__ void decode_impl(const DecodeArgs& A) {
   if constexpr (NB == 1) {
     // at most one tile per wave (the split is W tiles)
     if constexpr (FASTA) {
-      // The workgroup's operands are roped by all its waves.  Wave 0 (it
-      // always has a tile) waits for the operand block it loaded and a barrier
-      // hands the block to every wave; thread t then ropes the dword pairs t,
+      // The workgroup's operands are roped by all its waves.  Each wave waits
+      // for its share of the operand block (behind it only its own K and V,
+      // when it has a tile) and a barrier hands the block to every wave;
+      // thread t then ropes the dword pairs t,
       // t + 64W, ... (bias + RoPE of q (G heads) and k of the new token: dims
       // j, j + 1 and j + D/2, j + D/2 + 1), the last D/2 threads also
       // v + v_bias, and a second barrier hands the results to every wave.
       // Every wave, with or without a tile, meets both barriers.
-      if (w == 0) LUC_WAIT_VM(16);  // the operand block (the tile's K and V may be in flight)
+      if (ntw > 0) LUC_WAIT_VM(16);  // its operand loads (its K and V may be in flight)
+      else LUC_WAIT_VM(0);           // (no tile: only operand loads were issued)
       __builtin_amdgcn_s_barrier();
       {
         const uint32_t pa = lds_addr(s_pa[0]);
