@@ -157,6 +157,29 @@ int luc_decode_step(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qk
                     int split_tokens, void* out, int64_t out_row_stride, void* workspace,
                     size_t workspace_bytes);
 
+/* luc_decode_step for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * It has no counterpart in the reference (whose attention needs no
+ * workspace).  The same launch and results as luc_decode_step with the same
+ * arguments, except that the split-K workspace is the library's own fixed
+ * scratch: a device array of LUC_SCRATCH_BYTES per GPU, resolved and
+ * zero-filled by luc_init, held until the process ends.  Calls whose
+ * workspace (luc_paged_decode_workspace_size of the same sizes) exceeds
+ * LUC_SCRATCH_BYTES fail with LUC_E_WORKSPACE before any launch.  The entry
+ * point itself calls no allocator.  Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (other streams, other threads, other
+ * contexts on the same device) race and give undefined results; the caller
+ * serialises them (one stream, in order). */
+#define LUC_SCRATCH_BYTES (16u << 20)
+int luc_decode_step_noalloc(luc_ctx* ctx, void* stream, int dtype, void* qkv,
+                            int64_t qkv_row_stride, const void* q_bias, const void* k_bias,
+                            const void* v_bias, const float* cos_table, const float* sin_table,
+                            void* k_pool, void* v_pool, const int32_t* block_tables,
+                            int table_stride, const int32_t* positions, int batch, int max_ctx,
+                            int layer, int num_layers, int num_q_heads, int num_kv_heads,
+                            int head_dim, int block_size, float sm_scale, int split_tokens,
+                            void* out, int64_t out_row_stride);
+
 /* Causal prefill of packed prompts: the engine's per-token prefill loop
  * (Qwen2Model::forward_layer, src/models.rs:485-550 -- rope
  * (src/kernels/rope.cu), the cache write (src/kernels/kv_cache.cu) and

@@ -57,13 +57,27 @@ def build_kernel(name, verbose=False):
     return out
 
 
+def build_scratch_object(verbose=False):
+    """luc_scratch.hip: the library's fixed device scratch (a __device__ array
+    registered with the HIP runtime) and its set-up, as a relocatable object."""
+    out = os.path.join(LIB, "luc_scratch.o")
+    tmp = out + ".tmp"
+    _run([os.path.join(ROCM, "bin", "hipcc"), f"--offload-arch={ARCH}", "-O2", "-std=c++17",
+          "-fPIC", "-c", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-I", os.path.join(ROOT, "include"), os.path.join(CSRC, "luc_scratch.hip"), "-o", tmp],
+         verbose)
+    os.replace(tmp, out)
+    return out
+
+
 def build_host(verbose=False):
+    scratch = build_scratch_object(verbose)
     out = os.path.join(LIB, "liblucattn.so")
     tmp = out + ".tmp"
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
           "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"),
           "-I", os.path.join(ROOT, "include"), os.path.join(CSRC, "luc_attn.cpp"),
-          os.path.join(CSRC, "luc_blocks.cpp"),
+          os.path.join(CSRC, "luc_blocks.cpp"), scratch,
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
           "-o", tmp], verbose)
     os.replace(tmp, out)

@@ -29,9 +29,14 @@
 struct luc_ctx {
   int device = 0;
   int num_cus = 0;
+  void* scratch = nullptr;  // this device's copy of the library scratch (luc_scratch.hip)
   std::vector<hipModule_t> modules;
   std::unordered_map<std::string, hipFunction_t> fns;
 };
+
+namespace luc_internal {
+int scratch_setup(int device, void** out);
+}
 
 namespace {
 
@@ -433,6 +438,10 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
       ctx->num_cus < 1)
     ctx->num_cus = 256;
   (void)hipGetLastError();  // clear the misses from probing several modules
+  if (int rc = luc_internal::scratch_setup(device, &ctx->scratch)) {
+    luc_destroy(ctx);
+    return rc;
+  }
   *out_ctx = ctx;
   return LUC_OK;
 }
@@ -579,6 +588,33 @@ int luc_decode_step(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qk
   L.a.cos_t = cos_table;
   L.a.sin_t = sin_table;
   return launch_decode(L, stream);
+}
+
+int luc_decode_step_noalloc(luc_ctx* ctx, void* stream, int dtype, void* qkv,
+                            int64_t qkv_row_stride, const void* q_bias, const void* k_bias,
+                            const void* v_bias, const float* cos_table, const float* sin_table,
+                            void* k_pool, void* v_pool, const int32_t* block_tables,
+                            int table_stride, const int32_t* positions, int batch, int max_ctx,
+                            int layer, int num_layers, int num_q_heads, int num_kv_heads,
+                            int head_dim, int block_size, float sm_scale, int split_tokens,
+                            void* out, int64_t out_row_stride) {
+  if (!ctx) return fail(LUC_E_INVALID, "null context");
+  if (!ctx->scratch) return fail(LUC_E_WORKSPACE, "the context has no scratch (luc_init failed?)");
+  const size_t need = luc_paged_decode_workspace_size(batch, num_q_heads, num_kv_heads, head_dim,
+                                                      max_ctx, split_tokens);
+  if (need > LUC_SCRATCH_BYTES)
+    return fail(LUC_E_WORKSPACE,
+                "luc_decode_step_noalloc: these sizes need %zu bytes of split-K workspace, more "
+                "than the library's fixed scratch of %u bytes (use luc_decode_step with a "
+                "caller workspace)",
+                need, (unsigned)LUC_SCRATCH_BYTES);
+  // the scratch is this device's copy (ctx->scratch, from hipGetSymbolAddress
+  // at luc_init), already zero-filled; every launch leaves its counters at zero
+  return luc_decode_step(ctx, stream, dtype, qkv, qkv_row_stride, q_bias, k_bias, v_bias,
+                         cos_table, sin_table, k_pool, v_pool, block_tables, table_stride,
+                         positions, batch, max_ctx, layer, num_layers, num_q_heads, num_kv_heads,
+                         head_dim, block_size, sm_scale, split_tokens, out, out_row_stride,
+                         ctx->scratch, LUC_SCRATCH_BYTES);
 }
 
 int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qkv_row_stride,

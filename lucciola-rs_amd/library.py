@@ -44,6 +44,9 @@ SIGNATURES = {
     "luc_decode_step": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                _i32, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                _i32, _vp, _i64, _vp, _sz]),
+    "luc_decode_step_noalloc": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
+                                       _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
+                                       _i32, _i32, _f32, _i32, _vp, _i64]),
     "luc_paged_prefill": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                  _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                  _i32, _i32, _f32, _vp, _i64]),
@@ -201,6 +204,20 @@ class LucAttn:
             head_dim, block_size, sm_scale, split_tokens, _p(out),
             out_row_stride if out_row_stride is not None else hq * head_dim, _p(workspace),
             ws_bytes))
+
+    def decode_step_noalloc(self, qkv, q_bias, k_bias, v_bias, cos, sin, k_pool, v_pool, tables,
+                            positions, batch, max_ctx, layer, num_layers, hq, hkv, head_dim,
+                            sm_scale, out, split_tokens=0, qkv_row_stride=None,
+                            out_row_stride=None, block_size=16, stream=None):
+        """luc_decode_step_noalloc: luc_decode_step with the library's fixed
+        per-device scratch as its split-K workspace (no workspace argument)."""
+        self._check(self.lib.luc_decode_step_noalloc(
+            self.ctx, _stream(stream), dtype_code(k_pool), _p(qkv),
+            qkv_row_stride if qkv_row_stride is not None else (hq + 2 * hkv) * head_dim,
+            _p(q_bias), _p(k_bias), _p(v_bias), _p(cos), _p(sin), _p(k_pool), _p(v_pool),
+            _p(tables), tables.shape[-1], _p(positions), batch, max_ctx, layer, num_layers, hq, hkv,
+            head_dim, block_size, sm_scale, split_tokens, _p(out),
+            out_row_stride if out_row_stride is not None else hq * head_dim))
 
     def paged_prefill(self, qkv, q_bias, k_bias, v_bias, cos, sin, k_pool, v_pool, tables,
                       cu_seqlens, start_pos, total_rows, max_ctx, layer, num_layers, hq, hkv,
