@@ -413,6 +413,136 @@ __device__ void qk_writeback(const DecodeArgs& A, int b, int h, const uint16_t* 
   }
 }
 
+// The end of a split, shared by the decode kernels.  On entry each wave holds
+// its running state over its own tokens in the load layout (lane = token row
+// pv_tok x 16-byte chunk pv_ch of a 1 KB load): o[g][e] for head g and dim
+// pv_ch * 8 + e, the wave-uniform reference point m_run[g] and the per-lane
+// sums l_lane[g].  The wave's token rows are reduced with permlane swaps
+// (reduce-scatter), the W waves merge their (m, l, o) records through LDS
+// (wave v's record at recs + v * rec_stride floats; recs also serves as the
+// cross-split merge's weight table, at least G * 257 floats), and the
+// workgroup writes its output (one split) or its partial, whose arrival is
+// counted; the last split of (b, h) to arrive merges the partials.  s_last is
+// one word of LDS; sq / sk are the step variant's roped q and k of the new
+// token, written back into the qkv row by the workgroup that finishes last.
+template <int DT, int D, int G, bool APPEND, int W>
+__device__ __attribute__((always_inline)) inline void finish_split(
+    const DecodeArgs& A, float (&o)[G][8], const float (&m_run)[G], const float (&l_lane)[G],
+    float* recs, int rec_stride, uint32_t* s_last, const uint16_t* sq, const uint16_t* sk, int split,
+    int bh, int b, int h, int nsplit, uint16_t* out_row) {
+  constexpr int GD = G * D;
+  constexpr int NV = 8 * G;  // o values per lane: 8 dims x G heads
+  constexpr int CH = D / 8;  // 16-byte chunks per token row
+  constexpr int NVP = (NV / 4 + 3) / 4 * 4;
+  constexpr int REC_ML = 4 * CH * NVP;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pv_ch = lane % CH;
+  // ---- reduce the wave's token groups (lanes sharing pv_ch): reduce-scatter ----
+  float lsum[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) lsum[g] = l_lane[g];
+  wave_sum_n<G>(lsum);
+  float u[NV / 2], y[NV / 4];
+#pragma unroll
+  for (int k = 0; k < NV / 2; ++k) {
+    const int k2 = k + NV / 2;
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(o[k / 8][k % 8]),
+                                                    __float_as_uint(o[k2 / 8][k2 % 8]), false, false);
+    u[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int k = 0; k < NV / 4; ++k) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(u[k]),
+                                                    __float_as_uint(u[k + NV / 4]), false, false);
+    y[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (D == 64) {  // token groups also differ in lane bit 3
+#pragma unroll
+    for (int k = 0; k < NV / 4; ++k) y[k] += dpp_mov<0x128>(y[k]);  // row_ror:8
+  }
+
+  // ---- merge the W waves through LDS: each wave's record (o, m, l) ----
+  // the lane holds o values base + k (value v: head v / 8, dim pv_ch * 8 + v % 8)
+  const int base = ((lane >> 5) & 1) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);
+  const bool writer = D == 128 || (lane & 8) == 0;
+  float* const recw = recs + w * rec_stride;
+  if (writer) {
+    float* const slot = recw + ((lane >> 4) * CH + pv_ch) * NVP;
+#pragma unroll
+    for (int k = 0; k < NVP; k += 4)
+      *(float4*)(slot + k) = make_float4(y[k], k + 1 < NV / 4 ? y[k + 1] : 0.0f,
+                                         k + 2 < NV / 4 ? y[k + 2] : 0.0f,
+                                         k + 3 < NV / 4 ? y[k + 3] : 0.0f);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      recw[REC_ML + g] = m_run[g];
+      recw[REC_ML + G + g] = lsum[g];
+    }
+  }
+  __syncthreads();
+  const int64_t prec = (int64_t)bh * A.max_splits + split;  // this split's partial
+  for (int e = threadIdx.x; e < GD; e += 64 * W) {
+    const int g = e / D, d = e % D;
+    const int val = g * 8 + d % 8;  // the value's index in the reduce-scatter
+    const int idx = ((val / (NV / 4)) * CH + d / 8) * NVP + val % (NV / 4);
+    float mw[W], M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < W; ++v) {
+      mw[v] = recs[v * rec_stride + REC_ML + g];
+      M = fmaxf(M, mw[v]);
+    }
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int v = 0; v < W; ++v) {  // waves without tiles: m = -inf, weight 0
+      const float* rv2 = recs + v * rec_stride;
+      const float wt = __builtin_amdgcn_exp2f(mw[v] - M);
+      O = fmaf(wt, rv2[idx], O);
+      L = fmaf(wt, rv2[REC_ML + G + g], L);
+    }
+    if (nsplit == 1) {
+      out_row[e] = St<DT>::store(O / L);
+    } else {
+      // partials by agent-scope stores (coherent across the XCDs' L2s), read
+      // back the same way by the split that merges
+      ws_store(A.ws_o + prec * GD + e, O);
+      if (e % D == 0) {
+        ws_store(A.ws_ml + (prec * G + g) * 2, M);
+        ws_store(A.ws_ml + (prec * G + g) * 2 + 1, L);
+      }
+    }
+  }
+
+  // ---- the last split of (b, h) to finish merges the partials ----
+  if (nsplit > 1) {
+    // this wave's partial stores have completed (at agent scope) before the
+    // workgroup's arrival is counted
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    // whether this workgroup is the last split of (b, h) to finish, passed
+    // through s_last
+    if (threadIdx.x == 0) {
+      const int old = __hip_atomic_fetch_add(A.ws_cnt + bh, 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+      *s_last = old == nsplit - 1;
+      // the counter goes back to zero for the next launch
+      if (old == nsplit - 1)
+        __hip_atomic_store(A.ws_cnt + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!*s_last) return;
+    if constexpr (APPEND) qk_writeback<D, G, 64 * W>(A, b, h, sq, sk);
+    // every other split's partial is complete: the agent-scope loads of
+    // lse_merge see them
+    float* const s_w = recs;  // the records were read above
+    lse_merge<DT, D, G, 64 * W>(A, bh, nsplit, out_row, s_w, s_w + G * 256);
+  } else if constexpr (APPEND) {
+    qk_writeback<D, G, 64 * W>(A, b, h, sq, sk);
+  }
+}
+
 template <int DT, int D, int G, bool APPEND, int W, int NB>
 __device__ void decode_impl(const DecodeArgs& A) {
   using S = DecodeGeo<D>;
@@ -1007,111 +1137,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
     }
   }
 
-  // ---- reduce the wave's token groups (lanes sharing pv_ch): reduce-scatter ----
-  float lsum[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) lsum[g] = l_lane[g];
-  wave_sum_n<G>(lsum);
-  float u[NV / 2], y[NV / 4];
-#pragma unroll
-  for (int k = 0; k < NV / 2; ++k) {
-    const int k2 = k + NV / 2;
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(o[k / 8][k % 8]),
-                                                    __float_as_uint(o[k2 / 8][k2 % 8]), false, false);
-    u[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-#pragma unroll
-  for (int k = 0; k < NV / 4; ++k) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(u[k]),
-                                                    __float_as_uint(u[k + NV / 4]), false, false);
-    y[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-  if constexpr (D == 64) {  // token groups also differ in lane bit 3
-#pragma unroll
-    for (int k = 0; k < NV / 4; ++k) y[k] += dpp_mov<0x128>(y[k]);  // row_ror:8
-  }
-
-  // ---- merge the W waves through LDS: each wave's record (o, m, l) in its
-  // first K buffer (no loads into it are outstanding any more) ----
-  // the lane holds o values base + k (value v: head v / 8, dim pv_ch * 8 + v % 8)
-  const int base = ((lane >> 5) & 1) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);
-  const bool writer = D == 128 || (lane & 8) == 0;
-  float* const recw = (float*)s_k[w][0];
-  if (writer) {
-    float* const slot = recw + ((lane >> 4) * S::CH + pv_ch) * NVP;
-#pragma unroll
-    for (int k = 0; k < NVP; k += 4)
-      *(float4*)(slot + k) = make_float4(y[k], k + 1 < NV / 4 ? y[k + 1] : 0.0f,
-                                         k + 2 < NV / 4 ? y[k + 2] : 0.0f,
-                                         k + 3 < NV / 4 ? y[k + 3] : 0.0f);
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      recw[REC_ML + g] = m_run[g];
-      recw[REC_ML + G + g] = lsum[g];
-    }
-  }
-  __syncthreads();
-  const int64_t rec = (int64_t)bh * A.max_splits + split;
-  for (int e = threadIdx.x; e < GD; e += 64 * W) {
-    const int g = e / D, d = e % D;
-    const int val = g * 8 + d % 8;  // the value's index in the reduce-scatter
-    const int idx = ((val / (NV / 4)) * S::CH + d / 8) * NVP + val % (NV / 4);
-    float mw[W], M = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < W; ++v) {
-      mw[v] = ((const float*)s_k[v][0])[REC_ML + g];
-      M = fmaxf(M, mw[v]);
-    }
-    float O = 0.0f, L = 0.0f;
-#pragma unroll
-    for (int v = 0; v < W; ++v) {  // waves without tiles: m = -inf, weight 0
-      const float* rv2 = (const float*)s_k[v][0];
-      const float wt = __builtin_amdgcn_exp2f(mw[v] - M);
-      O = fmaf(wt, rv2[idx], O);
-      L = fmaf(wt, rv2[REC_ML + G + g], L);
-    }
-    if (nsplit == 1) {
-      out_row[e] = St<DT>::store(O / L);
-    } else {
-      // partials by agent-scope stores (coherent across the XCDs' L2s), read
-      // back the same way by the split that merges
-      ws_store(A.ws_o + rec * GD + e, O);
-      if (e % D == 0) {
-        ws_store(A.ws_ml + (rec * G + g) * 2, M);
-        ws_store(A.ws_ml + (rec * G + g) * 2 + 1, L);
-      }
-    }
-  }
-
-  // ---- the last split of (b, h) to finish merges the partials ----
-  if (nsplit > 1) {
-    // this wave's partial stores have completed (at agent scope) before the
-    // workgroup's arrival is counted
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    // whether this workgroup is the last split of (b, h) to finish, passed
-    // through the p exchange buffer (unused from here on)
-    uint32_t* const s_last = &s_p[0][0];
-    if (threadIdx.x == 0) {
-      const int old = __hip_atomic_fetch_add(A.ws_cnt + bh, 1, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-      *s_last = old == nsplit - 1;
-      // the counter goes back to zero for the next launch
-      if (old == nsplit - 1)
-        __hip_atomic_store(A.ws_cnt + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!*s_last) return;
-    if constexpr (APPEND) qk_writeback<D, G, 64 * W>(A, b, h, s_q[0], s_knew[0]);
-    // every other split's partial is complete: the agent-scope loads of
-    // lse_merge see them
-    float* const s_w = (float*)&s_k[0][0][0];  // the records were read above
-    lse_merge<DT, D, G, 64 * W>(A, bh, nsplit, out_row, s_w, s_w + G * 256);
-  } else if constexpr (APPEND) {
-    qk_writeback<D, G, 64 * W>(A, b, h, s_q[0], s_knew[0]);
-  }
+  finish_split<DT, D, G, APPEND, W>(A, o, m_run, l_lane, (float*)s_k[0][0], NB * S::KBYTES / 4,
+                                    &s_p[0][0], s_q[0], s_knew[0], split, bh, b, h, nsplit, out_row);
 }
 
 }  // namespace luc
