@@ -12,15 +12,20 @@ from gpu_util import TOL, from_dev, gpu_step, max_abs, oracle_step, say
 pytestmark = pytest.mark.gpu
 
 
-def assert_step_matches(orc, got, want, dtype):
+def assert_step_matches(orc, got, want, dtype, gate=None):
+    """Bit-exact cache and roped q/k; attention output within the north-star
+    tolerance and, where given, within `gate`: a regression bound at about
+    ten times the error measured on the same inputs."""
     assert np.array_equal(got["qkv"], want["qkv"]), "RoPE'd q/k differ"
     assert np.array_equal(got["k_pool"], want["k_pool"]), "K pool differs"
     assert np.array_equal(got["v_pool"], want["v_pool"]), "V pool differs"
     o = orc.to_f32(got["out"], dtype)
     assert np.all(np.isfinite(o)), "non-finite attention output"
     err = max_abs(orc, got["out"], want["out"], dtype)
-    say(f"  max|hip - oracle| = {err:.3e} (tol {TOL[dtype]})")
+    say(f"  max|hip - oracle| = {err:.3e} (tol {TOL[dtype]}, gate {gate})")
     assert err <= TOL[dtype]
+    if gate is not None:
+        assert err <= gate
 
 
 SMALL = [
@@ -82,36 +87,55 @@ def test_batch32_mixed_full(orc, luc, fused):
     """B=32, ctx U{128..4096}, pool 16384 pages, fp16 -- full size, one layer."""
     cfg = wl.CONFIGS["batch32_mixed"]
     h = wl.host_decode_inputs(cfg, seed=1)
-    assert_step_matches(orc, gpu_step(luc, h, fused=fused), oracle_step(orc, luc, h), "f16")
+    assert_step_matches(orc, gpu_step(luc, h, fused=fused), oracle_step(orc, luc, h), "f16",
+                        gate=2e-4)  # measured 6.1e-5: one fp16 unit at these magnitudes
 
 
 def test_batch8_32k_full(orc, luc):
     """B=8, ctx 32768 each, 12q/2kv d=128 bf16, 1% x8 outliers -- full size."""
     cfg = wl.CONFIGS["batch8_32k"]
     h = wl.host_decode_inputs(cfg, seed=8)
-    assert_step_matches(orc, gpu_step(luc, h), oracle_step(orc, luc, h), "bf16")
+    assert_step_matches(orc, gpu_step(luc, h), oracle_step(orc, luc, h), "bf16",
+                        gate=1e-4)  # measured 1.5e-5
 
 
-def test_batch64_long_full(orc, luc):
-    """B=64, ctx U{1024..16384}, 28q/4kv d=128 bf16 -- full size, one layer."""
+@pytest.mark.parametrize("split", [0, 512], ids=["auto", "split512"])
+def test_batch64_long_full(orc, luc, split):
+    """B=64, ctx U{1024..16384}, 28q/4kv d=128 bf16 -- full size, one layer;
+    automatic splits, and 512-token splits (2 to 32 per sequence, the
+    configuration's split-K regime)."""
     cfg = wl.CONFIGS["batch64_long"]
     h = wl.host_decode_inputs(cfg, seed=64, poison=False)
-    assert_step_matches(orc, gpu_step(luc, h), oracle_step(orc, luc, h), "bf16")
+    assert_step_matches(orc, gpu_step(luc, h, split_tokens=split), oracle_step(orc, luc, h), "bf16",
+                        gate=2e-4)  # measured 3.1e-5
+
+
+def bf16_units(a, b):
+    """Distance in bf16 units in the last place between two bit arrays."""
+    def key(x):
+        x = x.astype(np.int32)
+        return np.where(x & 0x8000, -(x & 0x7fff), x & 0x7fff)
+    return np.abs(key(a) - key(b))
 
 
 def test_split_count_independence(orc, luc):
-    """The output does not depend on how the context is split (within f32
-    rounding), and one split equals the unsplit path."""
-    cfg = wl.scaled(wl.CONFIGS["batch8_32k"], batch=3, ctx_lo=3000, ctx_hi=5000,
-                    pool_pages=3 * 313 + 1)
+    """The output does not depend on how the context is split: with every
+    context at most 2048 tokens, 2048-token splits are one split per
+    sequence (no merge); 128..1024-token splits (2 to 16 per sequence) give
+    the same bf16 output to within one unit in the last place, on at most 1%
+    of the outputs (f32 merge rounding crossing a bf16 rounding boundary)."""
+    cfg = wl.scaled(wl.CONFIGS["batch8_32k"], batch=3, ctx_lo=1500, ctx_hi=2048,
+                    pool_pages=3 * 128 + 1)
     h = wl.host_decode_inputs(cfg, seed=17)
-    outs = {s: orc.to_f32(gpu_step(luc, h, split_tokens=s)["out"], "bf16")
-            for s in (32, 96, 512, 2048, 5024)}
-    ref = outs[5024]  # one split
+    outs = {s: gpu_step(luc, h, split_tokens=s)["out"] for s in (128, 256, 512, 1024, 2048)}
+    ref = outs[2048]  # one split per sequence
+    want = oracle_step(orc, luc, h)["out"]
+    say(f"  one split vs oracle: {max_abs(orc, ref, want, 'bf16'):.3e}")
+    assert max_abs(orc, ref, want, "bf16") <= 2e-4
     for s, o in outs.items():
-        d = float(np.max(np.abs(o - ref)))
-        say(f"  split {s}: max diff vs single split {d:.3e}")
-        assert d <= 2 * 2.0 ** -8  # two bf16 ulps at |x| < 1
+        u = bf16_units(o, ref)
+        say(f"  split {s}: max {u.max()} bf16 units from one split, {np.count_nonzero(u)} of {u.size} differ")
+        assert u.max() <= 1 and np.count_nonzero(u) <= u.size // 100
 
 
 @pytest.mark.parametrize("split", [64, 128, 192, 256, 512, 1024, 2048])
