@@ -23,8 +23,21 @@ Also reported:
                 `traffic` is the HBM bytes per launch read from the committed
                 rocprofv3 PMC summary, if present;
   cpu_baseline  the oracle (C restatement of the reference's attention, OpenMP)
-                on one full layer step of the same workload on the host, on up to
-                16 threads and (single_core) on one;
+                on one full layer step of the same workload on the host, on the
+                process's CPU share (the cores it may run on, at most the
+                OMP_NUM_THREADS the box sets for one GPU) and (single_core) on
+                one, with nproc and the affinity count stated; `single_512`
+                is the same for the single-sequence workload (B=1, ctx 512,
+                14q/2kv, fp16), the one the reference's own path serves;
+  long_context  the paged decode operation (luc_paged_decode) on
+                batch64_long (B=64, 28q/4kv, d=128, bf16, ctx U{1024..16384})
+                and batch8_32k (B=8, 12q/2kv, d=128, bf16, ctx 32768), 4
+                layers rotated, per launch: us, algorithmic GB/s, fraction
+                of 8 TB/s;
+  floors        (in roofline) luc_gather_floor: the same K/V page slabs as
+                the decode kernel reads, with its work split and no
+                arithmetic, and luc_stream_read: the same bytes read
+                contiguously -- the memory floors under the kernel;
   prefill       luc_paged_prefill on prefill_4x2048 (4 prompts x 2048 rows from
                 an empty cache, 14q/2kv, d=64, bf16): RoPE + cache append
                 kernel, then the causal attention kernel on bf16 MFMA; time per
@@ -64,6 +77,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--eager", action="store_true", help="launch eagerly instead of a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-long-context", action="store_true",
+                    help="skip the batch64_long / batch8_32k decode measurements")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the prefill and sampling measurements")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -71,15 +86,25 @@ def parse():
     return ap.parse_args()
 
 
+def cpu_share():
+    """(threads, nproc, affinity): the cores this process may run on
+    (sched_getaffinity), capped by OMP_NUM_THREADS where the box sets it (its
+    CPU share per GPU), and the machine's nproc."""
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(affinity, omp) if omp > 0 else affinity
+    return max(threads, 1), os.cpu_count(), affinity
+
+
 def cpu_baseline(cfg, seed, budget_s=10.0, threads=None):
     """Time the oracle's decode step (one layer, the whole batch) on the host
-    with `threads` OpenMP threads (default: OMP_NUM_THREADS, else up to 16)."""
+    with `threads` OpenMP threads (default: the process's CPU share)."""
     import oracle
     from lucciola_rs_amd import workloads as wl
     from lucciola_rs_amd.engine import sm_scale
 
     if threads is None:
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+        threads = cpu_share()[0]
     h = wl.host_decode_inputs(cfg, seed, num_layers=1, poison=False)
     orc = oracle.get()
     cos, sin = orc.rope_table(cfg.ctx_hi + 1, cfg.head_dim, cfg.rope_theta)
@@ -201,6 +226,94 @@ def sampling_bench(lib, torch, reps=100):
             "us_per_call": round(statistics.median(runs), 2)}
 
 
+def graph_us(torch, fn, n, reps=3):
+    """Median microseconds per call of fn(i), i < n, replayed from a HIP graph."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    runs = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        runs.append(e0.elapsed_time(e1) * 1e3 / n)
+    return statistics.median(runs)
+
+
+def long_context_bench(lib, torch, name, seed, layers=4, launches=40):
+    """luc_paged_decode on a long-context workload: us per launch (graph of
+    back-to-back launches over `layers` rotated layers), algorithmic GB/s
+    and fraction of the 8 TB/s peak."""
+    import numpy as np
+    from lucciola_rs_amd import workloads as wl
+    from lucciola_rs_amd.engine import sm_scale
+
+    cfg = wl.CONFIGS[name]
+    dev = torch.device("cuda:0")
+    inp = wl.device_decode_inputs(cfg, seed, layers, device=dev)
+    ctx = inp["ctx"]
+    max_ctx = int(ctx.max())
+    out = torch.empty((cfg.batch, cfg.hq * cfg.head_dim), dtype=cfg.torch_dtype, device=dev)
+    ws = lib.workspace(cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, max_ctx, 0)
+
+    def call(i):
+        lib.paged_decode(out, inp["qkv"], inp["k_pool"], inp["v_pool"], inp["tables"],
+                         inp["positions"], cfg.batch, max_ctx, i % layers, layers, cfg.hq, cfg.hkv,
+                         cfg.head_dim, sm_scale(cfg.head_dim), 0, ws,
+                         out_row_stride=out.shape[-1], q_row_stride=cfg.row)
+
+    for i in range(layers):
+        call(i)
+    torch.cuda.synchronize()
+    us = graph_us(torch, call, launches)
+    nbytes = wl.decode_bytes(cfg, ctx) - cfg.batch * cfg.hkv * cfg.head_dim * 2 * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    res = {"workload": name, "batch": cfg.batch, "q_heads": cfg.hq, "kv_heads": cfg.hkv,
+           "head_dim": cfg.head_dim, "dtype": cfg.dtype, "mean_ctx": float(np.mean(ctx)),
+           "layers_rotated": layers, "us_per_launch": round(us, 2),
+           "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbs": round(gbs, 1),
+           "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    del inp
+    torch.cuda.empty_cache()
+    return res
+
+
+def floors(lib, torch, cfg, inp, max_ctx, layers, nbytes, launches=240):
+    """Memory floors under the decode kernel at this workload: the page-slab
+    gather with the decode kernel's split and no arithmetic, and the same
+    number of bytes read contiguously (from the K pool, offsets rotated so
+    successive reads do not hit the same 256 MB)."""
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def gather(i):
+        lib.gather_floor(inp["k_pool"], inp["v_pool"], inp["tables"], inp["positions"], cfg.batch,
+                         max_ctx, i % layers, layers, cfg.hkv, cfg.head_dim, sink)
+
+    flat = inp["k_pool"].view(-1)
+    n = (nbytes // 2 // 8) * 8  # elements, a multiple of 16 bytes
+    span = flat.numel() - n
+
+    def contiguous(i):
+        off = ((i % layers) * (span // max(layers, 1))) // 8 * 8
+        lib.stream_read(flat[off:off + n], sink)
+
+    for i in range(layers):
+        gather(i)
+        contiguous(i)
+    torch.cuda.synchronize()
+    g = graph_us(torch, gather, launches)
+    c = graph_us(torch, contiguous, launches)
+    return {"gather_floor_us": round(g, 3), "gather_floor_gbs": round(nbytes / (g * 1e-6) / 1e9, 1),
+            "contiguous_read_us": round(c, 3),
+            "contiguous_read_gbs": round(nbytes / (c * 1e-6) / 1e9, 1)}
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -297,24 +410,46 @@ def main():
         if tr.get("workload") == args.workload and tr.get("split_tokens", 0) == args.split_tokens:
             traffic = tr.get("hbm_bytes_per_launch")
 
+    fl = floors(lib, torch, cfg, inp, max_ctx, L, dec_bytes)
+    del inp, qkv, kp, vp
+    torch.cuda.empty_cache()
+
     prefill = None if args.no_prefill else prefill_bench(lib, torch)
     sampling = None if args.no_prefill else sampling_bench(lib, torch)
+    long_ctx = None
+    if not args.no_long_context:
+        long_ctx = [long_context_bench(lib, torch, n, args.seed) for n in ("batch64_long", "batch8_32k")]
 
     cpu = None
     if not args.no_cpu_baseline:
-        cb = cpu_baseline(cfg, args.seed)
+        threads, nproc, affinity = cpu_share()
+        cb = cpu_baseline(cfg, args.seed, threads=threads)
         cpu_bytes = wl.decode_bytes(cfg, cb["ctx"])
         cpu = {"value": round(cpu_bytes / cb["t"] / 1e9, 3), "unit": "GB/s",
-               "cores": cb["threads"], "kind": "port",
+               "cores": cb["threads"], "kind": "port", "nproc": nproc, "affinity_cpus": affinity,
                "sample": (f"one full layer step of {cfg.name} (B={cfg.batch}, RoPE + append + "
-                          f"attention of every sequence), oracle C restatement with OpenMP, "
-                          f"median of {cb['reps']} runs, {cb['t'] * 1e3:.1f} ms/step")}
+                          f"attention of every sequence), oracle C restatement with OpenMP on "
+                          f"{cb['threads']} threads (the process's CPU share: {affinity} CPUs in "
+                          f"its affinity mask of {nproc}, OMP_NUM_THREADS "
+                          f"{os.environ.get('OMP_NUM_THREADS', 'unset')}), median of {cb['reps']} "
+                          f"runs, {cb['t'] * 1e3:.1f} ms/step")}
         if cb["threads"] > 1:
             c1 = cpu_baseline(cfg, args.seed, budget_s=8.0, threads=1)
             cpu["single_core"] = {"value": round(cpu_bytes / c1["t"] / 1e9, 3), "unit": "GB/s",
                                   "cores": 1, "sample": (f"the same step on one thread, median of "
                                                          f"{c1['reps']} runs, "
                                                          f"{c1['t'] * 1e3:.1f} ms/step")}
+        c1cfg = wl.CONFIGS["single_512"]
+        s_all = cpu_baseline(c1cfg, args.seed, budget_s=3.0, threads=threads)
+        s_one = cpu_baseline(c1cfg, args.seed, budget_s=3.0, threads=1)
+        s_bytes = wl.decode_bytes(c1cfg, s_all["ctx"])
+        cpu["single_512"] = {
+            "workload": "single_512 (B=1, 14q/2kv, d=64, fp16, ctx 512, permuted table)",
+            "us_per_step": round(s_all["t"] * 1e6, 1), "value": round(s_bytes / s_all["t"] / 1e9, 3),
+            "unit": "GB/s", "cores": s_all["threads"],
+            "single_core_us_per_step": round(s_one["t"] * 1e6, 1),
+            "single_core_value": round(s_bytes / s_one["t"] / 1e9, 3),
+            "sample": f"median of {s_all['reps']} / {s_one['reps']} runs"}
 
     res = {
         "metric": "paged decode attn: µs/step + achieved HBM GB/s (% peak) at B=32, 1 MI355X",
@@ -343,8 +478,9 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": traffic, "kernel": "luc_paged_decode (luc_decode_*, merge in the last split)",
                      "us_per_launch": round(dec_ms * 1e3, 3),
-                     "algorithmic_bytes_per_launch": int(dec_bytes)},
+                     "algorithmic_bytes_per_launch": int(dec_bytes), **fl},
         "cpu_baseline": cpu,
+        "long_context": long_ctx,
         "prefill": prefill,
         "sampling": sampling,
     }

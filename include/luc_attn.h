@@ -180,6 +180,21 @@ int luc_decode_step_noalloc(luc_ctx* ctx, void* stream, int dtype, void* qkv,
                             int head_dim, int block_size, float sm_scale, int split_tokens,
                             void* out, int64_t out_row_stride);
 
+/* Measurement entry points; they have no counterpart in the reference and
+ * compute nothing the engine uses.  luc_gather_floor reads exactly the K and V
+ * page slabs a decode step over the same arguments reads (pages 0 ..
+ * positions[b] / 16 of table row b, layer `layer`, every kv head), with
+ * luc_paged_decode's work split and no arithmetic: its duration is the floor
+ * of the decode kernel's KV stream with this cache layout.  luc_stream_read
+ * reads `bytes` (a multiple of 16) contiguously from `src`.  Both write
+ * `sink` (one device uint32) only if the XOR of what they read equals a fixed
+ * pattern, so no load is dead. */
+int luc_gather_floor(luc_ctx* ctx, void* stream, const void* k_pool, const void* v_pool,
+                     const int32_t* block_tables, int table_stride, const int32_t* positions,
+                     int batch, int max_ctx, int layer, int num_layers, int num_kv_heads,
+                     int head_dim, uint32_t* sink);
+int luc_stream_read(luc_ctx* ctx, void* stream, const void* src, size_t bytes, uint32_t* sink);
+
 /* Causal prefill of packed prompts: the engine's per-token prefill loop
  * (Qwen2Model::forward_layer, src/models.rs:485-550 -- rope
  * (src/kernels/rope.cu), the cache write (src/kernels/kv_cache.cu) and

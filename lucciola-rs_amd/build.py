@@ -24,7 +24,7 @@ LIB = os.path.join(HERE, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-KERNELS = ["rope_append", "paged_decode", "paged_prefill", "model_ops", "sampling"]
+KERNELS = ["rope_append", "paged_decode", "paged_prefill", "model_ops", "sampling", "probe_gather"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "--genco", "--no-gpu-bundle-output",

@@ -8,9 +8,15 @@
 //   RMSNorm: thread t of 256 sums x*x over its 16-byte chunks c = t, t + 256,
 //   ... (elements in order, one fma each); the 256 partials add as a halving
 //   tree (a[i] += a[i + s] for s = 128, 64, ..., 1); inv = 1 / sqrt(sum / n +
-//   eps) with IEEE division and square root; y = round((x * inv) * w).
-//   argmax: the largest value wins; equal values go to the smallest index
-//   (the reference's block reduction leaves that order to its library).
+//   eps) with IEEE division and square root; y = round((x * inv) * w).  The
+//   formula is rmsnorm.cu's (:40, :63-64); its summation order is not: the
+//   reference adds per-thread x*x + y*y pairs (:19-29) with a 1024-thread CUB
+//   block reduction (:32-35) and takes rsqrtf (:40).
+//   argmax: the largest value wins; among equal values the one with the
+//   smallest i mod 1024, then the smallest i -- the order of the reference's
+//   1024-thread kernel (sampling.cu:16-46): each thread keeps the first of its
+//   equal values (i = tid, tid + 1024, ...) and the block reduction keeps the
+//   lower thread's pair on ties (ArgMaxOp returns a unless b is larger).
 #include "luc_common.h"
 
 namespace luc {
@@ -119,8 +125,9 @@ __device__ void argmax_impl(const uint16_t* x, int n, uint32_t* out) {
     if (t < h) {
       const float bv = sv[t + h];
       const int bi = si[t + h];
-      // larger value, or an equal one at a smaller index (-1 = none)
-      if (bv > sv[t] || (bv == sv[t] && bi >= 0 && (si[t] < 0 || bi < si[t]))) {
+      // larger value, or an equal one from a lower thread (i mod 1024; -1 = none)
+      if (bv > sv[t] || (bv == sv[t] && bi >= 0 &&
+                         (si[t] < 0 || (bi % kArgmaxThreads) < (si[t] % kArgmaxThreads)))) {
         sv[t] = bv;
         si[t] = bi;
       }

@@ -1,0 +1,93 @@
+// Measurement kernels: the memory floor under the paged decode kernel.
+//
+// luc_gather_floor_d{64,128}: reads exactly the K and V page slabs a decode
+// step reads -- every (sequence, kv head) unit's pages 0 .. positions[b] / 16
+// through its block-table row, layer `layer` -- with the decode kernel's own
+// work split (workgroup = 4 waves = (split of 4 tiles, sequence, kv head),
+// split-major; a tile is 8 KB of K: 64 tokens at head_dim 64, 32 at 128;
+// page numbers and the position by scalar loads in one round trip) and
+// nothing else: no q, no scores, no merge.  Every lane keeps an XOR of what
+// it read, so no load is dead; the sink is written only if that XOR equals a
+// fixed pattern.  Its duration is the time the decode kernel's KV stream
+// cannot beat with this layout and split.
+//
+// luc_stream_read: the same number of bytes read contiguously (16-byte
+// non-temporal loads, grid-stride), the floor without the page gather.
+#include "luc_common.h"
+
+namespace luc {
+
+struct GatherArgs {
+  const uint16_t* k_pool;
+  const uint16_t* v_pool;
+  const int32_t* tables;
+  int64_t table_stride;
+  const int32_t* positions;
+  int32_t batch, layer, num_layers, hkv, max_ctx;
+  uint32_t* sink;
+};
+
+constexpr uint32_t kSinkPattern = 0x9e3779b9u;
+
+template <int D>
+__device__ void gather_floor_impl(const GatherArgs& A) {
+  constexpr int TILE = D == 64 ? 64 : 32;       // tokens of 8 KB of K
+  constexpr int PAGES = TILE / kPage;           // pages per tile
+  constexpr int LPP = 8 / PAGES;                // 1 KB loads per page slab
+  constexpr int W = 4;                          // waves per workgroup, one tile each
+  typedef __attribute__((address_space(4))) const int const_i32;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pairs = A.batch * A.hkv;
+  const int split = blockIdx.x / pairs;
+  const int bh = blockIdx.x - split * pairs;
+  const int b = bh / A.hkv, h = bh - b * A.hkv;
+  const int* trow = A.tables + (int64_t)b * A.table_stride;
+  const int tmax = (int)A.table_stride - 1;
+  const int p0 = (split * W + w) * PAGES;       // first page of this wave's tile
+  int tab[PAGES];
+#pragma unroll
+  for (int i = 0; i < PAGES; ++i) tab[i] = ((const const_i32*)trow)[min(p0 + i, tmax)];
+  int pos = __builtin_amdgcn_readfirstlane(((const const_i32*)A.positions)[b]);
+#pragma unroll
+  for (int i = 0; i < PAGES; ++i) asm volatile("" : "+s"(pos) : "s"(__builtin_amdgcn_readfirstlane(tab[i])));
+  const int ctx = pos + 1;
+  if (ctx < 1 || ctx > A.max_ctx || p0 * kPage >= ctx) return;
+  const int last = pos / kPage;                 // pages past it re-read the last one
+  const int64_t page_stride = (int64_t)A.num_layers * A.hkv * kPage * D;
+  const int64_t head_off = ((int64_t)A.layer * A.hkv + h) * kPage * D;
+  uint4 x[16];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int e = min(p0 + r / LPP, last) - p0;
+    int phys = tab[0];
+#pragma unroll
+    for (int i = 1; i < PAGES; ++i) phys = e == i ? tab[i] : phys;
+    const int64_t off = (int64_t)phys * page_stride + head_off + (r % LPP) * 512 + lane * 8;
+    x[r] = ld_nt16(A.k_pool + off);
+    x[8 + r] = ld_nt16(A.v_pool + off);
+  }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc ^= x[r].x ^ x[r].y ^ x[r].z ^ x[r].w;
+  if (acc == kSinkPattern) A.sink[0] = acc;
+}
+
+}  // namespace luc
+
+extern "C" __global__ __launch_bounds__(256) void luc_gather_floor_d64(luc::GatherArgs a) {
+  luc::gather_floor_impl<64>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void luc_gather_floor_d128(luc::GatherArgs a) {
+  luc::gather_floor_impl<128>(a);
+}
+
+extern "C" __global__ __launch_bounds__(256) void luc_stream_read(const uint4* src, int64_t n16,
+                                                                  uint32_t* sink) {
+  uint32_t acc = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256) {
+    const uint4 v = luc::ld_nt16((const uint16_t*)(src + i));
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == luc::kSinkPattern) sink[0] = acc;
+}

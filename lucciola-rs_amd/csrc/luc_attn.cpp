@@ -60,7 +60,7 @@ int fail(int code, const char* fmt, ...) {
 
 constexpr const char* kCodeObjects[] = {"rope_append.hsaco", "paged_decode.hsaco",
                                          "paged_prefill.hsaco", "model_ops.hsaco",
-                                         "sampling.hsaco"};
+                                         "sampling.hsaco", "probe_gather.hsaco"};
 
 // Kernel-side constants (kept in step with csrc/kernels/paged_decode.hip):
 // four waves per workgroup, which share one split; tiles of 64 tokens
@@ -404,7 +404,8 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
     ctx->modules.push_back(mod);
   }
   std::vector<std::string> names = {"luc_rmsnorm_bf16", "luc_silu_mul_bf16", "luc_embedding_bf16",
-                                    "luc_argmax_bf16"};
+                                    "luc_argmax_bf16", "luc_gather_floor_d64",
+                                    "luc_gather_floor_d128", "luc_stream_read"};
   for (int npl : {1, 2, 4, 8, 16}) names.push_back("luc_topk_filter_bf16_n" + std::to_string(npl));
   for (int k = 32; k <= 1024; k *= 2) names.push_back("luc_top_p_sample_" + std::to_string(k));
   for (const char* dt : {"bf16", "f16"}) {
@@ -776,6 +777,57 @@ int luc_sort_and_sample(luc_ctx* ctx, void* stream, int dtype, const void* logit
   if (int rc = launch(filter, dim3(32), dim3(1024), stream, fargs)) return rc;
   void* sargs[] = {&sort_buffer, &top_p, &rand_val, &out_idx};
   return launch(sample, dim3(1), dim3(top_k < 64 ? 64 : top_k), stream, sargs);
+}
+
+// ---- measurement kernels (probe_gather.hip) ----
+
+int luc_gather_floor(luc_ctx* ctx, void* stream, const void* k_pool, const void* v_pool,
+                     const int32_t* block_tables, int table_stride, const int32_t* positions,
+                     int batch, int max_ctx, int layer, int num_layers, int num_kv_heads,
+                     int head_dim, uint32_t* sink) {
+  if (int rc = check_common(ctx, LUC_BF16, head_dim)) return rc;
+  if (num_kv_heads <= 0) return fail(LUC_E_INVALID, "num_kv_heads %d <= 0", num_kv_heads);
+  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers,
+                           LUC_BLOCK_SIZE))
+    return rc;
+  if (batch < 0 || max_ctx <= 0) return fail(LUC_E_INVALID, "batch %d / max_ctx %d", batch, max_ctx);
+  if (!positions || !sink) return fail(LUC_E_INVALID, "null positions or sink");
+  if ((int64_t)table_stride * LUC_BLOCK_SIZE < max_ctx)
+    return fail(LUC_E_INVALID, "table_stride %d pages cannot hold max_ctx %d", table_stride, max_ctx);
+  if (batch == 0) return LUC_OK;
+  if (int rc = check_device(ctx)) return rc;
+  hipFunction_t fn;
+  if (int rc = get_fn(ctx, "luc_gather_floor_d" + std::to_string(head_dim), &fn)) return rc;
+  // the decode kernel's split: 4 waves, one 8 KB K tile each
+  const int split = kDecodeWaves * decode_tile(head_dim);
+  const int64_t grid = ceil_div(max_ctx, split) * batch * num_kv_heads;
+  if (grid > INT32_MAX) return fail(LUC_E_INVALID, "grid too large");
+  struct {
+    const void* k;
+    const void* v;
+    const int32_t* tables;
+    int64_t table_stride;
+    const int32_t* positions;
+    int32_t batch, layer, num_layers, hkv, max_ctx;
+    uint32_t* sink;
+  } a{k_pool, v_pool, block_tables, table_stride, positions, batch, layer, num_layers,
+      num_kv_heads, max_ctx, sink};
+  void* args[] = {&a};
+  return launch(fn, dim3((unsigned)grid), dim3(kDecodeWaves * 64), stream, args);
+}
+
+int luc_stream_read(luc_ctx* ctx, void* stream, const void* src, size_t bytes, uint32_t* sink) {
+  if (!ctx) return fail(LUC_E_INVALID, "null context");
+  if (!src || !sink) return fail(LUC_E_INVALID, "null src or sink");
+  if (bytes % 16 || !aligned(src, 16)) return fail(LUC_E_INVALID, "src / bytes must be 16-byte multiples");
+  if (bytes == 0) return LUC_OK;
+  if (int rc = check_device(ctx)) return rc;
+  hipFunction_t fn;
+  if (int rc = get_fn(ctx, "luc_stream_read", &fn)) return rc;
+  int64_t n16 = (int64_t)(bytes / 16);
+  const int64_t grid = std::min<int64_t>(ceil_div(n16, 256), 2048);
+  void* args[] = {&src, &n16, &sink};
+  return launch(fn, dim3((unsigned)grid), dim3(256), stream, args);
 }
 
 }  // extern "C"

@@ -55,6 +55,9 @@ SIGNATURES = {
     "luc_embedding": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32]),
     "luc_argmax": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp]),
     "luc_sort_and_sample": (_i32, [_vp, _vp, _i32, _vp, _i32, _f32, _i32, _f32, _vp, _sz, _vp]),
+    "luc_gather_floor": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32,
+                                _i32, _vp]),
+    "luc_stream_read": (_i32, [_vp, _vp, _vp, _sz, _vp]),
     "luc_blocks_create": (_i32, [_i32, _i32, _i32, ctypes.POINTER(_vp)]),
     "luc_blocks_destroy": (None, [_vp]),
     "luc_blocks_reserve": (_i32, [_vp, _i32, _i32]),
@@ -251,6 +254,19 @@ class LucAttn:
         self._check(self.lib.luc_embedding(self.ctx, _stream(stream), dtype_code(table), _p(out),
                                            _p(table), _p(ids), ids.numel(), table.shape[0],
                                            table.shape[1]))
+
+    def gather_floor(self, k_pool, v_pool, tables, positions, batch, max_ctx, layer, num_layers,
+                     hkv, head_dim, sink, stream=None):
+        """luc_gather_floor: the decode step's K/V page slabs read with its work
+        split and no arithmetic (sink: a one-element device int32 tensor)."""
+        self._check(self.lib.luc_gather_floor(
+            self.ctx, _stream(stream), _p(k_pool), _p(v_pool), _p(tables), tables.shape[-1],
+            _p(positions), batch, max_ctx, layer, num_layers, hkv, head_dim, _p(sink)))
+
+    def stream_read(self, src, sink, stream=None):
+        """luc_stream_read of the whole of src (a contiguous device tensor)."""
+        self._check(self.lib.luc_stream_read(self.ctx, _stream(stream), _p(src),
+                                             src.numel() * src.element_size(), _p(sink)))
 
     def argmax(self, logits, out_idx, stream=None):
         """luc_argmax into out_idx (a one-element device int32 tensor)."""

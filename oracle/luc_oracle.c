@@ -382,6 +382,14 @@ void orc_prefill(uint16_t* out, int64_t out_stride, uint16_t* qkv, int64_t qkv_s
 /* ------------------------------------------------------------------ */
 /* Model loop operations: src/kernels/{rmsnorm,activation,sampling}.cu */
 /* ------------------------------------------------------------------ */
+/* RMSNorm in the fixed order of this library's kernel (model_ops.hip luc_rmsnorm_bf16:
+ * 256 threads, fma over each thread's 16-byte chunks, halving tree, 1/sqrtf), so that
+ * the GPU result can be compared bit for bit; the formula is rmsnorm.cu's
+ * (y = round((x * inv) * w), inv = 1/sqrt(mean(x^2) + eps), rmsnorm.cu:40, :63-64).
+ * The reference's own order is not this one: per-thread x*x + y*y pair sums
+ * (rmsnorm.cu:19-29), cub::BlockReduce<float, 1024> (:32-35) and rsqrtf (:40) --
+ * parity unpinned; tests/pins.py holds this function to the f64 formula within half
+ * a bf16 unit. */
 void orc_rmsnorm(uint16_t* out, const uint16_t* in, const uint16_t* weight, float eps, int rows,
                  int cols) {
     enum { T = 256 };
@@ -399,9 +407,9 @@ void orc_rmsnorm(uint16_t* out, const uint16_t* in, const uint16_t* weight, floa
             part[t] = s;
         }
         for (int h = T / 2; h > 0; h >>= 1)
-            for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];   /* rmsnorm.cu:33-35 */
+            for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];   /* halving tree */
         const float ms = part[0] / (float)(ORC_MUTANT == 11 ? cols - 1 : cols);
-        const float inv = 1.0f / sqrtf(ms + eps);                          /* rmsnorm.cu:40 */
+        const float inv = 1.0f / sqrtf(ms + eps);           /* rmsnorm.cu:40 has rsqrtf */
         uint16_t* y = out + (int64_t)r * cols;
         for (int i = 0; i < cols; ++i) {
             const float f = orc_bf16_to_f32(x[i]) * inv;                   /* rmsnorm.cu:63-64 */
@@ -422,12 +430,24 @@ void orc_silu_mul(uint16_t* gate_up, int rows, int inter) {
     }
 }
 
+/* argmax_kernel (sampling.cu:16-46) as launched by apply_argmax (kernels.rs:322-344,
+ * one block of 1024 threads): thread t keeps the first largest of x[t], x[t + 1024],
+ * ... above -1e30 (strict >, sampling.cu:28-34); the block reduction with ArgMaxOp
+ * (b if b.value > a.value, else a: sampling.cu:9-14) keeps the lower thread's pair on
+ * ties -- CUB's BlockReduce combines warp lanes and then warps in increasing order
+ * (cub/block/block_reduce.cuh, not vendored; see the parity notes). */
 int orc_argmax(const uint16_t* x, int n) {
+    enum { THREADS = 1024 };
     float best = -1e30f;                                                   /* sampling.cu:24-25 */
     int idx = -1;
-    for (int i = 0; i < n; ++i) {
-        const float v = orc_bf16_to_f32(x[i]);
-        if (ORC_MUTANT == 13 ? v >= best : v > best) { best = v; idx = i; }
+    for (int t = 0; t < THREADS; ++t) {
+        float tb = -1e30f;
+        int ti = -1;
+        for (int i = t; i < n; i += THREADS) {                             /* sampling.cu:28-34 */
+            const float v = orc_bf16_to_f32(x[i]);
+            if (v > tb) { tb = v; ti = i; }
+        }
+        if (ORC_MUTANT == 13 ? tb >= best && ti >= 0 : tb > best) { best = tb; idx = ti; }
     }
     return idx;
 }

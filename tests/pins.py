@@ -326,27 +326,48 @@ def check_silu_mul(orc, seed=8):
     return float(np.max(np.abs(f32(got[:, :inter], "bf16") - want) / tol))
 
 
-def check_argmax(orc, seed=9):
-    """Greedy index vs numpy's argmax (first of equal maxima), NaN never
-    chosen, -1 when no value exceeds -1e30.  Returns the number of misses."""
-    rng = np.random.default_rng(seed)
-    fails = 0
-    for n in (1, 7, 1000, 151936):
+def argmax_tie_order(v):
+    """The reference kernel's greedy index (sampling.cu:16-46, 1024 threads):
+    among the largest values above -1e30 (NaN never), the smallest i mod 1024,
+    then the smallest i; -1 if none.  Stated from the maxima directly, not by
+    simulating threads."""
+    v = np.where(np.isnan(v), -np.inf, np.asarray(v, np.float64))
+    if v.size == 0 or v.max() <= -1e30:
+        return -1
+    tied = np.flatnonzero(v == v.max())
+    return int(tied[np.lexsort((tied, tied % 1024))][0])
+
+
+def argmax_cases(rng):
+    """Logit rows for the greedy index: random rows, three equal maxima, a NaN
+    in front, equal maxima at 600 and 1500 (1500 mod 1024 = 476 < 600, so
+    1500 wins), at 1024 and 2048 (thread 0 both: 1024 wins), and a row with
+    nothing above -1e30."""
+    out = []
+    for n in (1, 7, 1000, 2100, 151936):
         x = bits(rng.standard_normal(n), "bf16")
-        cases = [x]
+        out.append(x)
         if n > 3:
             y = x.copy()
             y[[1, n // 2, n - 1]] = bits(np.array([9.0, 9.0, 9.0]), "bf16")  # ties
             z = y.copy()
             z[0] = 0x7fc0                                                     # NaN first
-            cases += [y, z]
-        cases.append(bits(np.full(n, -1e31), "bf16"))
-        for c in cases:
-            v = f32(c, "bf16").astype(np.float64)
-            v = np.where(np.isnan(v), -np.inf, v)
-            want = int(np.argmax(v)) if v.max() > -1e30 else -1
-            fails += int(orc.argmax(c) != want)
-    return fails
+            out += [y, z]
+        if n > 2048:
+            w = x.copy()
+            w[[600, 1500]] = bits(np.array([9.0, 9.0]), "bf16")
+            out.append(w)
+            u = x.copy()
+            u[[1024, 2048]] = bits(np.array([9.0, 9.0]), "bf16")
+            out.append(u)
+        out.append(bits(np.full(n, -1e31), "bf16"))
+    return out
+
+
+def check_argmax(orc, seed=9):
+    """Greedy index vs argmax_tie_order.  Returns the number of misses."""
+    rng = np.random.default_rng(seed)
+    return sum(int(orc.argmax(c) != argmax_tie_order(f32(c, "bf16"))) for c in argmax_cases(rng))
 
 
 # ---------------------------------------------------------------- top-k / top-p sampling

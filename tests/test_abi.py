@@ -6,6 +6,7 @@ import os
 import re
 
 import pytest
+import numpy as np
 import torch
 
 from lucciola_rs_amd import library
@@ -122,14 +123,27 @@ def test_workspace_size_policy(cdll):
     assert ws(1, 4, 1, 64, 256 * 2048 + 1, 0) == 0
 
 
-def test_rope_table_entry_point_matches_oracle(orc, cdll):
-    cos = torch.empty(512, 32)
-    sin = torch.empty(512, 32)
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("scale", [0.0, 2.0, 4.0])
+def test_rope_table_entry_point_matches_oracle(orc, cdll, head_dim, scale):
+    """luc_rope_table (RopeCache::new, src/layers/rope.rs:21-29) over the whole
+    Qwen2.5 position range: bit-equal to the oracle's table, and within the
+    f64 closed form's f32 bound (theta = (pos / scale) / base^(2i/d))."""
+    import pins
+    max_pos = 32768
+    cos = torch.empty(max_pos, head_dim // 2)
+    sin = torch.empty(max_pos, head_dim // 2)
     assert cdll.luc_rope_table(ctypes.c_void_p(cos.data_ptr()), ctypes.c_void_p(sin.data_ptr()),
-                               512, 64, 1e6, 0.0) == 0
-    oc, os_ = orc.rope_table(512, 64, 1e6)
+                               max_pos, head_dim, 1e6, scale) == 0
+    oc, os_ = orc.rope_table(max_pos, head_dim, 1e6, scale or None)
     assert torch.equal(cos, torch.from_numpy(oc)) and torch.equal(sin, torch.from_numpy(os_))
-    assert cdll.luc_rope_table(None, None, 512, 64, 1e6, 0.0) == -1
+    pos = np.arange(max_pos, dtype=np.float64)[:, None]
+    i = np.arange(head_dim // 2, dtype=np.float64)[None, :]
+    theta = (pos / (scale or 1.0)) / np.power(1e6, 2 * i / head_dim)
+    tol = np.abs(theta) * 2.0 ** -21 + 2.0 ** -23
+    err = np.maximum(np.abs(cos.numpy() - np.cos(theta)), np.abs(sin.numpy() - np.sin(theta)))
+    assert float(np.max(err / tol)) <= 1.0
+    assert cdll.luc_rope_table(None, None, 512, head_dim, 1e6, 0.0) == -1
 
 
 def test_init_without_device_fails_cleanly(cdll):

@@ -79,22 +79,19 @@ def test_embedding_gather_and_out_of_range(luc):
 
 
 def test_argmax_ties_nan_and_floor(orc, luc):
+    """luc_argmax against the oracle and the stated tie order of the
+    reference's kernel (smallest i mod 1024, then smallest i): random rows,
+    equal maxima (600 and 1500: 1500 wins), a NaN, nothing above -1e30."""
+    import pins
     rng = np.random.default_rng(4)
     idx = torch.zeros(1, dtype=torch.int32, device="cuda")
-    cases = []
-    x = to_bf16_bits(rng.standard_normal(151936))
-    cases.append(x)
-    y = x.copy(); y[[7, 90000, 151935]] = to_bf16_bits(np.array([50.0, 50.0, 50.0]))
-    cases.append(y)                                   # ties: smallest index
-    z = y.copy(); z[3] = 0x7fc0                       # a NaN never wins
-    cases.append(z)
-    cases.append(to_bf16_bits(np.full(4096, -1e31)))  # nothing above -1e30: -1
-    for c in cases:
+    for c in pins.argmax_cases(rng):
         say(f"  [gpu] argmax n={c.size}")
         luc.argmax(to_dev(c, "bf16"), idx)
         torch.cuda.synchronize()
-        want = orc.argmax(c)
-        assert int(idx.cpu().item()) == (want if want >= 0 else -1)
+        want = pins.argmax_tie_order(orc.to_f32(c, "bf16"))
+        assert orc.argmax(c) == want
+        assert int(idx.cpu().item()) == want
 
 
 @pytest.fixture(scope="module")

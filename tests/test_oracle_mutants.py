@@ -25,7 +25,7 @@ MUTANTS = {
     10: "fp16 rounding truncates",
     11: "RMSNorm mean over n - 1",
     12: "silu with exp(+x)",
-    13: "argmax ties go to the last index",
+    13: "argmax ties go to the higher thread",
     14: "top-k filter: ties go to the higher lane in the warp trees",
     15: "bitonic network: block directions swapped",
     16: "top-p cutoff needs cdf strictly above top_p",
