@@ -23,6 +23,14 @@
  *  - Positions are device int32 arrays: the position of the current token, so a
  *    sequence attends to positions 0..pos (ctx = pos + 1), as the reference's
  *    device-resident pos_ptr (src/models.rs:489-493, :715).
+ *  - Entry points that address pages through block tables take num_blocks,
+ *    the number of pages in each pool (the reference's num_physical_blocks,
+ *    kv_cache.rs:57-59; its kernels read table entries unchecked,
+ *    kv_cache.cu:28, attention.cu:82).  A table entry outside [0, num_blocks)
+ *    is never used as an address: the cache write that would go through it is
+ *    skipped (the row is left untouched, as for a position outside its table
+ *    row) and every attention output whose context reaches that page is NaN.
+ *    num_blocks < 1 is LUC_E_INVALID.
  *  - Only block_size 16 (kv_cache.rs:35) and head_dim 64/128
  *    (kernels.rs:37-46) are supported; Hq must be a multiple of Hkv with
  *    Hq/Hkv <= 8.
@@ -37,7 +45,7 @@
 extern "C" {
 #endif
 
-#define LUC_ABI_VERSION 3
+#define LUC_ABI_VERSION 4
 #define LUC_BLOCK_SIZE 16
 
 typedef struct luc_ctx luc_ctx;
@@ -89,7 +97,7 @@ int luc_rope(luc_ctx* ctx, void* stream, int dtype, void* q, const void* q_bias,
  * at slot positions[r] of table row r.  v_bias may be NULL. */
 int luc_kv_cache_update(luc_ctx* ctx, void* stream, int dtype, void* k_pool, void* v_pool,
                         const void* k, const void* v, const void* v_bias, int64_t row_stride,
-                        const int32_t* block_tables, int table_stride,
+                        const int32_t* block_tables, int table_stride, int num_blocks,
                         const int32_t* positions, int num_tokens, int layer, int num_layers,
                         int num_kv_heads, int head_dim, int block_size);
 
@@ -101,7 +109,7 @@ int luc_rope_append(luc_ctx* ctx, void* stream, int dtype, void* q, const void* 
                     void* k, const void* k_bias, const void* v, const void* v_bias,
                     int64_t row_stride, const float* cos_table, const float* sin_table,
                     const int32_t* positions, const int32_t* block_tables, int table_stride,
-                    void* k_pool, void* v_pool, int num_tokens, int layer, int num_layers,
+                    int num_blocks, void* k_pool, void* v_pool, int num_tokens, int layer, int num_layers,
                     int num_q_heads, int num_kv_heads, int head_dim, int block_size);
 
 /* Bytes of split-K workspace luc_paged_decode / luc_decode_step need for these
@@ -132,7 +140,8 @@ size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_he
  * launch. */
 int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t out_row_stride,
                      const void* q, int64_t q_row_stride, const void* k_pool, const void* v_pool,
-                     const int32_t* block_tables, int table_stride, const int32_t* positions,
+                     const int32_t* block_tables, int table_stride, int num_blocks,
+                     const int32_t* positions,
                      int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
                      int num_kv_heads, int head_dim, int block_size, float sm_scale,
                      int split_tokens, void* workspace, size_t workspace_bytes);
@@ -151,7 +160,8 @@ int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t o
 int luc_decode_step(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qkv_row_stride,
                     const void* q_bias, const void* k_bias, const void* v_bias,
                     const float* cos_table, const float* sin_table, void* k_pool, void* v_pool,
-                    const int32_t* block_tables, int table_stride, const int32_t* positions,
+                    const int32_t* block_tables, int table_stride, int num_blocks,
+                     const int32_t* positions,
                     int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
                     int num_kv_heads, int head_dim, int block_size, float sm_scale,
                     int split_tokens, void* out, int64_t out_row_stride, void* workspace,
@@ -175,7 +185,7 @@ int luc_decode_step_noalloc(luc_ctx* ctx, void* stream, int dtype, void* qkv,
                             int64_t qkv_row_stride, const void* q_bias, const void* k_bias,
                             const void* v_bias, const float* cos_table, const float* sin_table,
                             void* k_pool, void* v_pool, const int32_t* block_tables,
-                            int table_stride, const int32_t* positions, int batch, int max_ctx,
+                            int table_stride, int num_blocks, const int32_t* positions, int batch, int max_ctx,
                             int layer, int num_layers, int num_q_heads, int num_kv_heads,
                             int head_dim, int block_size, float sm_scale, int split_tokens,
                             void* out, int64_t out_row_stride);
@@ -190,7 +200,8 @@ int luc_decode_step_noalloc(luc_ctx* ctx, void* stream, int dtype, void* qkv,
  * `sink` (one device uint32) only if the XOR of what they read equals a fixed
  * pattern, so no load is dead. */
 int luc_gather_floor(luc_ctx* ctx, void* stream, const void* k_pool, const void* v_pool,
-                     const int32_t* block_tables, int table_stride, const int32_t* positions,
+                     const int32_t* block_tables, int table_stride, int num_blocks,
+                     const int32_t* positions,
                      int batch, int max_ctx, int layer, int num_layers, int num_kv_heads,
                      int head_dim, uint32_t* sink);
 int luc_stream_read(luc_ctx* ctx, void* stream, const void* src, size_t bytes, uint32_t* sink);
@@ -216,7 +227,8 @@ int luc_stream_read(luc_ctx* ctx, void* stream, const void* src, size_t bytes, u
 int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qkv_row_stride,
                       const void* q_bias, const void* k_bias, const void* v_bias,
                       const float* cos_table, const float* sin_table, void* k_pool, void* v_pool,
-                      const int32_t* block_tables, int table_stride, const int32_t* cu_seqlens,
+                      const int32_t* block_tables, int table_stride, int num_blocks,
+                      const int32_t* cu_seqlens,
                       const int32_t* start_pos, int batch, int total_rows, int max_ctx, int layer,
                       int num_layers, int num_q_heads, int num_kv_heads, int head_dim,
                       int block_size, float sm_scale, void* out, int64_t out_row_stride);

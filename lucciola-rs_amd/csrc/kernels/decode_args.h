@@ -20,6 +20,7 @@ struct luc_decode_args {
   int64_t table_stride;
   const int32_t* positions; // [batch]
   int32_t batch, layer, num_layers, hkv;
+  int32_t num_blocks;       // pages per pool: table entries outside [0, num_blocks) are never used
   float qk_scale_log2;      // sm_scale * log2(e)
   int32_t max_ctx, split_tokens, max_splits;
   float* ws_ml;             // [batch*Hkv][max_splits][G][2]  (max, sum) per split

@@ -663,8 +663,21 @@ __device__ void decode_impl(const DecodeArgs& A) {
   const int ntw = t_first < s_end ? (s_end - t_first + WS - 1) / WS : 0;
   // the wave whose tiles hold the new token (in the last split)
   const bool owns = APPEND && pos >= s_begin && pos < s_end && ((pos - s_begin) / S::TILE) % W == w;
-  auto page_of = [&](int j) -> int64_t {     // physical page j of the split (uniform j)
+  // Page numbers outside the pool are never used as addresses: such a page
+  // reads page 0 instead and the wave's result is poisoned with NaN below
+  // (bad_page is wave-uniform).
+  const int nb = A.num_blocks;
+  bool bad_page = false;
+  auto page_raw = [&](int j) -> int {  // table entry of page j of the split (uniform j)
     return j < 64 ? __builtin_amdgcn_readlane(tab0, j) : __builtin_amdgcn_readlane(tab1, j - 64);
+  };
+  auto page_of = [&](int j) -> int64_t {  // physical page j of the split, inside the pool
+    const int p = page_raw(j);
+    if (p < 0 || p >= nb) {
+      bad_page = true;
+      return 0;
+    }
+    return p;
   };
   const int jend = (s_end - 1 - s_begin) / kPage;  // last page of the split
   // single-tile kernel: the pages of this wave's tile (clamped to the split)
@@ -678,9 +691,25 @@ __device__ void decode_impl(const DecodeArgs& A) {
       int t = traw[0];
 #pragma unroll
       for (int k = 1; k < S::PAGES; ++k) t = e == k ? traw[k] : t;
-      tpage[i] = t;
+      const bool ok = t >= 0 && t < nb;
+      if (!ok && ntw > 0) bad_page = true;
+      tpage[i] = ok ? t : 0;
     }
   }
+
+  // table entry of the new token's page (the owner wave's cache write)
+  auto page_raw_of_new = [&]() __attribute__((always_inline)) -> int {
+    if constexpr (T1) {  // in the owner's only tile: one of its pages
+      const int jt = (pos - t_first) / kPage;
+      const int e = min(max(min(p0 + j0 + jt, p0 + jend) - tstart, 0), S::PAGES - 1);
+      int t = traw[0];
+#pragma unroll
+      for (int k = 1; k < S::PAGES; ++k) t = e == k ? traw[k] : t;
+      return t;
+    } else {
+      return page_raw((pos - s_begin) / kPage);
+    }
+  };
 
   // The step variant's prologue operands (q and k of the new token with their
   // biases, the cos/sin row, v + v_bias) are loaded before the KV stream is
@@ -1120,21 +1149,17 @@ __device__ void decode_impl(const DecodeArgs& A) {
   }
 
   if constexpr (APPEND) {
-    if (owns && lane < S::CH) {  // the cache write of the new token
-      int64_t phys;
-      if constexpr (T1) {  // in the owner's only tile: one of its pages
-        const int jt = (pos - t_first) / kPage;
-        int t = tpage[0];
-#pragma unroll
-        for (int k = 1; k < S::PAGES; ++k) t = jt == k ? tpage[k] : t;
-        phys = t;
-      } else {
-        phys = page_of((pos - s_begin) / kPage);
-      }
-      const int64_t slot = phys * page_stride + head_off + (int64_t)(pos % kPage) * D + lane * 8;
+    // the cache write of the new token (none through a page outside the pool)
+    const int new_page = page_raw_of_new();
+    if (owns && lane < S::CH && new_page >= 0 && new_page < nb) {
+      const int64_t slot = (int64_t)new_page * page_stride + head_off + (int64_t)(pos % kPage) * D + lane * 8;
       *(uint4*)(A.k_pool + slot) = *(const uint4*)(s_knew[qi] + lane * 8);
       *(uint4*)(A.v_pool + slot) = *(const uint4*)(s_vnew[qi] + lane * 8);
     }
+  }
+  if (bad_page) {  // a page of this wave's tiles lies outside the pool
+#pragma unroll
+    for (int g = 0; g < G; ++g) l_lane[g] = __builtin_nanf("");
   }
 
   finish_split<DT, D, G, APPEND, W>(A, o, m_run, l_lane, (float*)s_k[0][0], NB * S::KBYTES / 4,

@@ -69,6 +69,7 @@ struct PrefillArgs {
   uint16_t* out;              // row r at out + r*out_stride, [Hq*D]
   int64_t out_stride;
   int32_t batch, layer, num_layers, hkv, max_ctx, pairs;  // pairs: tile pairs per sequence
+  int32_t num_blocks;  // pages per pool: table entries outside [0, num_blocks) are never used
   float qk_scale_log2;  // sm_scale * log2(e)
 };
 
@@ -153,6 +154,9 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   constexpr int LPW = 2 * LOADS / W;  // loads per wave per stage
   static_assert(LOADS % W == 0, "every wave issues the same number of K (and V) loads");
   __shared__ __attribute__((aligned(16))) char s_kv[NS][2][KS];
+  // first token of a page outside the pool among those the tile reads (the
+  // minimum over the waves; INT_MAX if none)
+  __shared__ int s_bad_tok;
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -227,11 +231,18 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   // one iteration before the loads they address, so no wait on them
   // precedes a load.
   constexpr int NPG = LOADS / W;
+  // A page outside the pool is never used as an address: it reads page 0
+  // instead, and the rows whose context reaches it get NaN (bad_tok).
+  int bad_tok = 0x7fffffff;
   auto load_pages = [&](int sb, int* pg) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NPG; ++i) {
       const int tb = sb * SB * BT + (i * W + w) * TPL;
-      pg[i] = ((const const_i32_p*)trow)[min(tb, nkv - 1) / kPage];
+      const int lp = min(tb, nkv - 1) / kPage;
+      const int p = ((const const_i32_p*)trow)[lp];
+      const bool ok = p >= 0 && p < A.num_blocks;
+      if (!ok) bad_tok = min(bad_tok, lp * kPage);
+      pg[i] = ok ? p : 0;
     }
   };
   int pgn[NPG];  // pages of the next block to issue
@@ -416,6 +427,7 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 
   // every wave is done with the previous tile's last stage before it is refilled
   if (k) __builtin_amdgcn_s_barrier();
+  if (threadIdx.x == 0) s_bad_tok = 0x7fffffff;  // (read by every wave only after a barrier below)
 #pragma unroll
   for (int j = 0; j < NS - 1; ++j)
     if (j < nsb) {
@@ -433,9 +445,13 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   }
 
   // ---- normalise and store: lane holds dims 32db + 8i + 4g + j of row my_i ----
+  // rows whose context reaches a page outside the pool: NaN
+  if (lane == 0 && bad_tok != 0x7fffffff) atomicMin(&s_bad_tok, bad_tok);
+  __syncthreads();
+  const int first_bad = s_bad_tok;
   if (!active) continue;
   if (row_ok) {
-    const float inv = 1.0f / osum[0];
+    const float inv = my_pos >= first_bad ? __builtin_nanf("") : 1.0f / osum[0];
 #pragma unroll
     for (int db = 0; db < ND; ++db)
 #pragma unroll

@@ -23,7 +23,7 @@ struct GatherArgs {
   const int32_t* tables;
   int64_t table_stride;
   const int32_t* positions;
-  int32_t batch, layer, num_layers, hkv, max_ctx;
+  int32_t batch, layer, num_layers, hkv, max_ctx, num_blocks;
   uint32_t* sink;
 };
 
@@ -63,6 +63,7 @@ __device__ void gather_floor_impl(const GatherArgs& A) {
     int phys = tab[0];
 #pragma unroll
     for (int i = 1; i < PAGES; ++i) phys = e == i ? tab[i] : phys;
+    phys = phys >= 0 && phys < A.num_blocks ? phys : 0;  // never outside the pool
     const int64_t off = (int64_t)phys * page_stride + head_off + (r % LPP) * 512 + lane * 8;
     x[r] = ld_nt16(A.k_pool + off);
     x[8 + r] = ld_nt16(A.v_pool + off);

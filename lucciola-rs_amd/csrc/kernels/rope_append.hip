@@ -69,8 +69,9 @@ __device__ void rope_append_impl(uint16_t* q, const uint16_t* q_bias, uint16_t* 
                                  const uint16_t* v_bias, int64_t row_stride, const float* cos_t,
                                  const float* sin_t, const int* positions, const int* cu_seqlens,
                                  const int* start_pos, int batch, const int* tables,
-                                 int table_stride, uint16_t* k_pool, uint16_t* v_pool, int layer,
-                                 int num_layers, int hq, int hkv, int head_dim, int flags) {
+                                 int table_stride, int num_blocks, uint16_t* k_pool,
+                                 uint16_t* v_pool, int layer, int num_layers, int hq, int hkv,
+                                 int head_dim, int flags) {
   const int row = blockIdx.x;
   int seq, pos;
   row_position(row, positions, cu_seqlens, start_pos, batch, seq, pos);
@@ -86,6 +87,10 @@ __device__ void rope_append_impl(uint16_t* q, const uint16_t* q_bias, uint16_t* 
   int64_t slot0 = 0;  // pool offset of (pos, head 0, dim 0)
   if (flags & kWriteKV) {
     const int64_t phys = tables[(int64_t)seq * table_stride + pos / kPage];
+    // a page outside the pool: the row is left untouched, as for a position
+    // outside the table row (the reference reads the entry unchecked,
+    // kv_cache.cu:28)
+    if (phys < 0 || phys >= num_blocks) return;
     const int64_t page_elems = (int64_t)kPage * head_dim;
     slot0 = ((phys * num_layers + layer) * hkv) * page_elems + (int64_t)(pos % kPage) * head_dim;
   }
@@ -138,9 +143,9 @@ __device__ void rope_append_vec_impl(uint16_t* q, const uint16_t* q_bias, uint16
                                      const uint16_t* v_bias, int64_t row_stride,
                                      const float* cos_t, const float* sin_t, const int* positions,
                                      const int* cu_seqlens, const int* start_pos, int batch,
-                                     const int* tables, int table_stride, uint16_t* k_pool,
-                                     uint16_t* v_pool, int layer, int num_layers, int hq, int hkv,
-                                     int flags, int rows) {
+                                     const int* tables, int table_stride, int num_blocks,
+                                     uint16_t* k_pool, uint16_t* v_pool, int layer,
+                                     int num_layers, int hq, int hkv, int flags, int rows) {
 #pragma clang fp contract(off)
   constexpr int C = D / 16;  // 8-element chunks per half head
   constexpr int HALF = D / 2;
@@ -208,6 +213,7 @@ __device__ void rope_append_vec_impl(uint16_t* q, const uint16_t* q_bias, uint16
   int64_t slot0 = 0;  // pool offset of (pos, head 0, dim 0)
   if (flags & kWriteKV) {
     const int64_t phys = tables[(int64_t)seq * table_stride + pos / kPage];
+    if (phys < 0 || phys >= num_blocks) return;  // outside the pool: the row is left untouched
     slot0 = ((phys * num_layers + layer) * hkv) * head_stride + (int64_t)(pos % kPage) * D;
   }
   if (rot) {
@@ -237,12 +243,13 @@ __device__ void rope_append_vec_impl(uint16_t* q, const uint16_t* q_bias, uint16
       uint16_t* q, const uint16_t* q_bias, uint16_t* k, const uint16_t* k_bias,                   \
       const uint16_t* v, const uint16_t* v_bias, int64_t row_stride, const float* cos_t,          \
       const float* sin_t, const int* positions, const int* cu_seqlens, const int* start_pos,      \
-      int batch, const int* tables, int table_stride, uint16_t* k_pool, uint16_t* v_pool,         \
-      int layer, int num_layers, int hq, int hkv, int head_dim, int flags, int rows) {            \
+      int batch, const int* tables, int table_stride, int num_blocks, uint16_t* k_pool,           \
+      uint16_t* v_pool, int layer, int num_layers, int hq, int hkv, int head_dim, int flags,      \
+      int rows) {                                                                                 \
     luc::rope_append_vec_impl<DT, D>(q, q_bias, k, k_bias, v, v_bias, row_stride, cos_t, sin_t,   \
                                      positions, cu_seqlens, start_pos, batch, tables,             \
-                                     table_stride, k_pool, v_pool, layer, num_layers, hq, hkv,    \
-                                     flags, rows);                                                \
+                                     table_stride, num_blocks, k_pool, v_pool, layer, num_layers, \
+                                     hq, hkv, flags, rows);                                       \
   }
 
 LUC_ROPE_APPEND_VEC(luc_rope_append_vec_bf16_d64, luc::kBF16, 64)
@@ -255,11 +262,12 @@ LUC_ROPE_APPEND_VEC(luc_rope_append_vec_f16_d128, luc::kF16, 128)
       uint16_t* q, const uint16_t* q_bias, uint16_t* k, const uint16_t* k_bias,                   \
       const uint16_t* v, const uint16_t* v_bias, int64_t row_stride, const float* cos_t,          \
       const float* sin_t, const int* positions, const int* cu_seqlens, const int* start_pos,      \
-      int batch, const int* tables, int table_stride, uint16_t* k_pool, uint16_t* v_pool,         \
-      int layer, int num_layers, int hq, int hkv, int head_dim, int flags) {                      \
+      int batch, const int* tables, int table_stride, int num_blocks, uint16_t* k_pool,           \
+      uint16_t* v_pool, int layer, int num_layers, int hq, int hkv, int head_dim, int flags) {    \
     luc::rope_append_impl<DT>(q, q_bias, k, k_bias, v, v_bias, row_stride, cos_t, sin_t,          \
                               positions, cu_seqlens, start_pos, batch, tables, table_stride,      \
-                              k_pool, v_pool, layer, num_layers, hq, hkv, head_dim, flags);       \
+                              num_blocks, k_pool, v_pool, layer, num_layers, hq, hkv, head_dim,   \
+                              flags);                                                             \
   }
 
 LUC_ROPE_APPEND(luc_rope_append_bf16, luc::kBF16)

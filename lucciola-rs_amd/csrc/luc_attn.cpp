@@ -144,6 +144,7 @@ struct AppendArgs {
   int batch = 0;
   const int32_t* tables = nullptr;
   int table_stride = 0;
+  int num_blocks = 1;
   void* k_pool = nullptr;
   void* v_pool = nullptr;
   int layer = 0, num_layers = 1, hq = 0, hkv = 0, head_dim = 0, flags = 0;
@@ -153,7 +154,7 @@ int launch_append(const luc_ctx* ctx, void* stream, int dtype, int rows, AppendA
   void* args[] = {&a.q,         &a.q_bias,    &a.k,          &a.k_bias,   &a.v,
                   &a.v_bias,    &a.row_stride, &a.cos_t,     &a.sin_t,    &a.positions,
                   &a.cu_seqlens, &a.start_pos, &a.batch,     &a.tables,   &a.table_stride,
-                  &a.k_pool,    &a.v_pool,    &a.layer,      &a.num_layers, &a.hq,
+                  &a.num_blocks, &a.k_pool,    &a.v_pool,    &a.layer,      &a.num_layers, &a.hq,
                   &a.hkv,       &a.head_dim,  &a.flags,      &rows};
   // 16-byte chunk kernel when every row and bias starts on 16 bytes (the
   // pools always do), else the element-wise kernel (same values)
@@ -190,7 +191,7 @@ int check_rows(int num_tokens, int64_t row_stride, int min_row) {
 }
 
 int check_cache(const void* k_pool, const void* v_pool, const int32_t* tables, int table_stride,
-                int layer, int num_layers, int block_size) {
+                int num_blocks, int layer, int num_layers, int block_size) {
   if (block_size != LUC_BLOCK_SIZE)
     return fail(LUC_E_UNSUPPORTED, "block_size %d (only %d)", block_size, LUC_BLOCK_SIZE);
   if (!k_pool || !v_pool || !tables) return fail(LUC_E_INVALID, "null pool or block table");
@@ -199,6 +200,7 @@ int check_cache(const void* k_pool, const void* v_pool, const int32_t* tables, i
   if (num_layers <= 0 || layer < 0 || layer >= num_layers)
     return fail(LUC_E_INVALID, "layer %d outside [0, %d)", layer, num_layers);
   if (table_stride <= 0) return fail(LUC_E_INVALID, "table_stride %d <= 0", table_stride);
+  if (num_blocks < 1) return fail(LUC_E_INVALID, "num_blocks %d < 1", num_blocks);
   return LUC_OK;
 }
 
@@ -263,13 +265,15 @@ struct DecodeLaunch {
 // Shared argument checks and argument block of the two decode entry points.
 int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t out_row_stride,
                    const void* q, int64_t q_row_stride, const void* k_pool, const void* v_pool,
-                   const int32_t* block_tables, int table_stride, const int32_t* positions,
-                   int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
-                   int num_kv_heads, int head_dim, int block_size, float sm_scale,
-                   int split_tokens, void* workspace, size_t workspace_bytes, DecodeLaunch* L) {
+                   const int32_t* block_tables, int table_stride, int num_blocks,
+                   const int32_t* positions, int batch, int max_ctx, int layer, int num_layers,
+                   int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                   float sm_scale, int split_tokens, void* workspace, size_t workspace_bytes,
+                   DecodeLaunch* L) {
   if (int rc = check_common(ctx, dtype, head_dim)) return rc;
   if (int rc = check_heads(num_q_heads, num_kv_heads)) return rc;
-  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers, block_size))
+  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, num_blocks, layer,
+                           num_layers, block_size))
     return rc;
   if (batch < 0) return fail(LUC_E_INVALID, "batch %d < 0", batch);
   if (max_ctx <= 0) return fail(LUC_E_INVALID, "max_ctx %d <= 0", max_ctx);
@@ -324,6 +328,7 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
   a.layer = layer;
   a.num_layers = num_layers;
   a.hkv = num_kv_heads;
+  a.num_blocks = num_blocks;
   a.qk_scale_log2 = sm_scale * 1.4426950408889634f;
   a.max_ctx = max_ctx;
   a.split_tokens = st;
@@ -352,7 +357,7 @@ struct PrefillArgs {
   const int32_t* start_pos;
   void* out;
   int64_t out_stride;
-  int32_t batch, layer, num_layers, hkv, max_ctx, pairs;
+  int32_t batch, layer, num_layers, hkv, max_ctx, pairs, num_blocks;
   float qk_scale_log2;
 };
 
@@ -493,13 +498,14 @@ int luc_rope(luc_ctx* ctx, void* stream, int dtype, void* q, const void* q_bias,
 
 int luc_kv_cache_update(luc_ctx* ctx, void* stream, int dtype, void* k_pool, void* v_pool,
                         const void* k, const void* v, const void* v_bias, int64_t row_stride,
-                        const int32_t* block_tables, int table_stride,
+                        const int32_t* block_tables, int table_stride, int num_blocks,
                         const int32_t* positions, int num_tokens, int layer, int num_layers,
                         int num_kv_heads, int head_dim, int block_size) {
   if (int rc = check_common(ctx, dtype, head_dim)) return rc;
   if (num_kv_heads <= 0) return fail(LUC_E_INVALID, "num_kv_heads %d <= 0", num_kv_heads);
   if (int rc = check_rows(num_tokens, row_stride, num_kv_heads * head_dim)) return rc;
-  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers, block_size))
+  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, num_blocks, layer,
+                           num_layers, block_size))
     return rc;
   if (num_tokens == 0) return LUC_OK;
   if (!k || !v || !positions) return fail(LUC_E_INVALID, "null k, v or positions");
@@ -507,6 +513,7 @@ int luc_kv_cache_update(luc_ctx* ctx, void* stream, int dtype, void* k_pool, voi
   AppendArgs a;
   a.k = const_cast<void*>(k); a.v = v; a.v_bias = v_bias; a.row_stride = row_stride;
   a.positions = positions; a.tables = block_tables; a.table_stride = table_stride;
+  a.num_blocks = num_blocks;
   a.k_pool = k_pool; a.v_pool = v_pool; a.layer = layer; a.num_layers = num_layers;
   a.hq = num_kv_heads; a.hkv = num_kv_heads; a.head_dim = head_dim;
   a.flags = kWriteKV;
@@ -517,12 +524,14 @@ int luc_rope_append(luc_ctx* ctx, void* stream, int dtype, void* q, const void* 
                     void* k, const void* k_bias, const void* v, const void* v_bias,
                     int64_t row_stride, const float* cos_table, const float* sin_table,
                     const int32_t* positions, const int32_t* block_tables, int table_stride,
-                    void* k_pool, void* v_pool, int num_tokens, int layer, int num_layers,
-                    int num_q_heads, int num_kv_heads, int head_dim, int block_size) {
+                    int num_blocks, void* k_pool, void* v_pool, int num_tokens, int layer,
+                    int num_layers, int num_q_heads, int num_kv_heads, int head_dim,
+                    int block_size) {
   if (int rc = check_common(ctx, dtype, head_dim)) return rc;
   if (int rc = check_heads(num_q_heads, num_kv_heads)) return rc;
   if (int rc = check_rows(num_tokens, row_stride, num_q_heads * head_dim)) return rc;
-  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers, block_size))
+  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, num_blocks, layer,
+                           num_layers, block_size))
     return rc;
   if (num_tokens == 0) return LUC_OK;
   if (!q || !k || !v || !cos_table || !sin_table || !positions)
@@ -531,7 +540,8 @@ int luc_rope_append(luc_ctx* ctx, void* stream, int dtype, void* q, const void* 
   AppendArgs a;
   a.q = q; a.q_bias = q_bias; a.k = k; a.k_bias = k_bias; a.v = v; a.v_bias = v_bias;
   a.row_stride = row_stride; a.cos_t = cos_table; a.sin_t = sin_table; a.positions = positions;
-  a.tables = block_tables; a.table_stride = table_stride; a.k_pool = k_pool; a.v_pool = v_pool;
+  a.tables = block_tables; a.table_stride = table_stride; a.num_blocks = num_blocks;
+  a.k_pool = k_pool; a.v_pool = v_pool;
   a.layer = layer; a.num_layers = num_layers; a.hq = num_q_heads; a.hkv = num_kv_heads;
   a.head_dim = head_dim; a.flags = kRopeQ | kRopeK | kWriteKV;
   return launch_append(ctx, stream, dtype, num_tokens, a);
@@ -548,13 +558,14 @@ size_t luc_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_he
 
 int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t out_row_stride,
                      const void* q, int64_t q_row_stride, const void* k_pool, const void* v_pool,
-                     const int32_t* block_tables, int table_stride, const int32_t* positions,
-                     int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
-                     int num_kv_heads, int head_dim, int block_size, float sm_scale,
-                     int split_tokens, void* workspace, size_t workspace_bytes) {
+                     const int32_t* block_tables, int table_stride, int num_blocks,
+                     const int32_t* positions, int batch, int max_ctx, int layer, int num_layers,
+                     int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                     float sm_scale, int split_tokens, void* workspace, size_t workspace_bytes) {
   DecodeLaunch L;
   if (int rc = prepare_decode(ctx, dtype, false, out, out_row_stride, q, q_row_stride, k_pool,
-                              v_pool, block_tables, table_stride, positions, batch, max_ctx, layer,
+                              v_pool, block_tables, table_stride, num_blocks, positions, batch,
+                              max_ctx, layer,
                               num_layers, num_q_heads, num_kv_heads, head_dim, block_size, sm_scale,
                               split_tokens, workspace, workspace_bytes, &L))
     return rc;
@@ -566,15 +577,16 @@ int luc_paged_decode(luc_ctx* ctx, void* stream, int dtype, void* out, int64_t o
 int luc_decode_step(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qkv_row_stride,
                     const void* q_bias, const void* k_bias, const void* v_bias,
                     const float* cos_table, const float* sin_table, void* k_pool, void* v_pool,
-                    const int32_t* block_tables, int table_stride, const int32_t* positions,
-                    int batch, int max_ctx, int layer, int num_layers, int num_q_heads,
-                    int num_kv_heads, int head_dim, int block_size, float sm_scale,
-                    int split_tokens, void* out, int64_t out_row_stride, void* workspace,
-                    size_t workspace_bytes) {
+                    const int32_t* block_tables, int table_stride, int num_blocks,
+                    const int32_t* positions, int batch, int max_ctx, int layer, int num_layers,
+                    int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                    float sm_scale, int split_tokens, void* out, int64_t out_row_stride,
+                    void* workspace, size_t workspace_bytes) {
   if (!cos_table || !sin_table) return fail(LUC_E_INVALID, "null rope table");
   DecodeLaunch L;
   if (int rc = prepare_decode(ctx, dtype, true, out, out_row_stride, qkv, qkv_row_stride, k_pool,
-                              v_pool, block_tables, table_stride, positions, batch, max_ctx, layer,
+                              v_pool, block_tables, table_stride, num_blocks, positions, batch,
+                              max_ctx, layer,
                               num_layers, num_q_heads, num_kv_heads, head_dim, block_size, sm_scale,
                               split_tokens, workspace, workspace_bytes, &L))
     return rc;
@@ -595,7 +607,8 @@ int luc_decode_step_noalloc(luc_ctx* ctx, void* stream, int dtype, void* qkv,
                             int64_t qkv_row_stride, const void* q_bias, const void* k_bias,
                             const void* v_bias, const float* cos_table, const float* sin_table,
                             void* k_pool, void* v_pool, const int32_t* block_tables,
-                            int table_stride, const int32_t* positions, int batch, int max_ctx,
+                            int table_stride, int num_blocks, const int32_t* positions, int batch,
+                            int max_ctx,
                             int layer, int num_layers, int num_q_heads, int num_kv_heads,
                             int head_dim, int block_size, float sm_scale, int split_tokens,
                             void* out, int64_t out_row_stride) {
@@ -613,7 +626,7 @@ int luc_decode_step_noalloc(luc_ctx* ctx, void* stream, int dtype, void* qkv,
   // at luc_init), already zero-filled; every launch leaves its counters at zero
   return luc_decode_step(ctx, stream, dtype, qkv, qkv_row_stride, q_bias, k_bias, v_bias,
                          cos_table, sin_table, k_pool, v_pool, block_tables, table_stride,
-                         positions, batch, max_ctx, layer, num_layers, num_q_heads, num_kv_heads,
+                         num_blocks, positions, batch, max_ctx, layer, num_layers, num_q_heads, num_kv_heads,
                          head_dim, block_size, sm_scale, split_tokens, out, out_row_stride,
                          ctx->scratch, LUC_SCRATCH_BYTES);
 }
@@ -621,13 +634,15 @@ int luc_decode_step_noalloc(luc_ctx* ctx, void* stream, int dtype, void* qkv,
 int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qkv_row_stride,
                       const void* q_bias, const void* k_bias, const void* v_bias,
                       const float* cos_table, const float* sin_table, void* k_pool, void* v_pool,
-                      const int32_t* block_tables, int table_stride, const int32_t* cu_seqlens,
+                      const int32_t* block_tables, int table_stride, int num_blocks,
+                      const int32_t* cu_seqlens,
                       const int32_t* start_pos, int batch, int total_rows, int max_ctx, int layer,
                       int num_layers, int num_q_heads, int num_kv_heads, int head_dim,
                       int block_size, float sm_scale, void* out, int64_t out_row_stride) {
   if (int rc = check_common(ctx, dtype, head_dim)) return rc;
   if (int rc = check_heads(num_q_heads, num_kv_heads)) return rc;
-  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers, block_size))
+  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, num_blocks, layer,
+                           num_layers, block_size))
     return rc;
   if (batch < 0 || total_rows < 0) return fail(LUC_E_INVALID, "batch %d / total_rows %d < 0", batch, total_rows);
   if (max_ctx <= 0) return fail(LUC_E_INVALID, "max_ctx %d <= 0", max_ctx);
@@ -668,7 +683,8 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
   a.v = base + (int64_t)(num_q_heads + num_kv_heads) * head_dim; a.v_bias = v_bias;
   a.row_stride = qkv_row_stride; a.cos_t = cos_table; a.sin_t = sin_table;
   a.cu_seqlens = cu_seqlens; a.start_pos = start_pos; a.batch = batch;
-  a.tables = block_tables; a.table_stride = table_stride; a.k_pool = k_pool; a.v_pool = v_pool;
+  a.tables = block_tables; a.table_stride = table_stride; a.num_blocks = num_blocks;
+  a.k_pool = k_pool; a.v_pool = v_pool;
   a.layer = layer; a.num_layers = num_layers; a.hq = num_q_heads; a.hkv = num_kv_heads;
   a.head_dim = head_dim; a.flags = kRopeQ | kRopeK | kWriteKV;
   if (int rc = launch_append(ctx, stream, dtype, total_rows, a)) return rc;
@@ -679,7 +695,7 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
   p.tables = block_tables; p.table_stride = table_stride; p.cu_seqlens = cu_seqlens;
   p.start_pos = start_pos; p.out = out; p.out_stride = out_row_stride; p.batch = batch;
   p.layer = layer; p.num_layers = num_layers; p.hkv = num_kv_heads; p.max_ctx = max_ctx;
-  p.pairs = pairs; p.qk_scale_log2 = sm_scale * 1.4426950408889634f;
+  p.pairs = pairs; p.num_blocks = num_blocks; p.qk_scale_log2 = sm_scale * 1.4426950408889634f;
   void* args[] = {&p};
   return launch(fn, dim3((unsigned)grid), dim3(64 * waves), stream, args);
 }
@@ -782,13 +798,13 @@ int luc_sort_and_sample(luc_ctx* ctx, void* stream, int dtype, const void* logit
 // ---- measurement kernels (probe_gather.hip) ----
 
 int luc_gather_floor(luc_ctx* ctx, void* stream, const void* k_pool, const void* v_pool,
-                     const int32_t* block_tables, int table_stride, const int32_t* positions,
-                     int batch, int max_ctx, int layer, int num_layers, int num_kv_heads,
-                     int head_dim, uint32_t* sink) {
+                     const int32_t* block_tables, int table_stride, int num_blocks,
+                     const int32_t* positions, int batch, int max_ctx, int layer, int num_layers,
+                     int num_kv_heads, int head_dim, uint32_t* sink) {
   if (int rc = check_common(ctx, LUC_BF16, head_dim)) return rc;
   if (num_kv_heads <= 0) return fail(LUC_E_INVALID, "num_kv_heads %d <= 0", num_kv_heads);
-  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, layer, num_layers,
-                           LUC_BLOCK_SIZE))
+  if (int rc = check_cache(k_pool, v_pool, block_tables, table_stride, num_blocks, layer,
+                           num_layers, LUC_BLOCK_SIZE))
     return rc;
   if (batch < 0 || max_ctx <= 0) return fail(LUC_E_INVALID, "batch %d / max_ctx %d", batch, max_ctx);
   if (!positions || !sink) return fail(LUC_E_INVALID, "null positions or sink");
@@ -808,10 +824,10 @@ int luc_gather_floor(luc_ctx* ctx, void* stream, const void* k_pool, const void*
     const int32_t* tables;
     int64_t table_stride;
     const int32_t* positions;
-    int32_t batch, layer, num_layers, hkv, max_ctx;
+    int32_t batch, layer, num_layers, hkv, max_ctx, num_blocks;
     uint32_t* sink;
   } a{k_pool, v_pool, block_tables, table_stride, positions, batch, layer, num_layers,
-      num_kv_heads, max_ctx, sink};
+      num_kv_heads, max_ctx, num_blocks, sink};
   void* args[] = {&a};
   return launch(fn, dim3((unsigned)grid), dim3(kDecodeWaves * 64), stream, args);
 }

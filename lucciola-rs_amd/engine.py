@@ -44,10 +44,45 @@ class RopeCache:
         self.sin = sin.to(device)
 
 
+def pool_blocks(free: int, total: int, memory_fraction: float, num_layers: int,
+                num_kv_heads: int, head_dim: int, max_position_embeddings: int) -> int:
+    """Pages of a KV pool sized from a VRAM budget, as KVCache::new does
+    (src/layers/kv_cache.rs:37-59): the budget is total * memory_fraction (an
+    f32 product, truncated) less the memory already used (total - free); a
+    page holds K and V of 16 tokens for every layer and kv head in bf16; the
+    pool holds at most the pages of max_position_embeddings.  Raises
+    RuntimeError with the reference's message when the budget is below the
+    memory already used (kv_cache.rs:40-48)."""
+    used = total - free
+    available_total = int(np.float32(total) * np.float32(memory_fraction))
+    allocatable = available_total - used
+    gb = 1024.0 ** 3
+    if allocatable < 0:
+        raise RuntimeError(
+            "Not enough available GPU memory for KV Cache allocation, "
+            f"free: {free / gb} GB, used: {used / gb} GB, total: {total / gb} GB, "
+            f"requested fraction: {memory_fraction}")
+    bytes_per_block = 2 * num_layers * num_kv_heads * BLOCK_SIZE * head_dim * 2
+    return min(allocatable // bytes_per_block, (max_position_embeddings + BLOCK_SIZE - 1) // BLOCK_SIZE)
+
+
 class KVCache:
     """Paged K/V pools [num_blocks][num_layers][Hkv][16][head_dim] and one block
-    table -- src/layers/kv_cache.rs:12-104.  The pool size is given directly
-    (the reference derives it from free VRAM, kv_cache.rs:37-59)."""
+    table -- src/layers/kv_cache.rs:12-104.  The pool size is given directly,
+    or by `from_budget` from the free VRAM as the reference does
+    (kv_cache.rs:37-59)."""
+
+    @classmethod
+    def from_budget(cls, num_layers, num_kv_heads, head_dim, max_position_embeddings,
+                    memory_fraction, dtype=torch.bfloat16, device="cuda", lib=None,
+                    mem_info=None):
+        """KVCache::new: the pool sized by pool_blocks from (free, total) of the
+        device (torch.cuda.mem_get_info) or `mem_info`."""
+        free, total = mem_info if mem_info is not None else torch.cuda.mem_get_info(device)
+        blocks = pool_blocks(free, total, memory_fraction, num_layers, num_kv_heads, head_dim,
+                             max_position_embeddings)
+        return cls(num_layers, num_kv_heads, head_dim, blocks, max_position_embeddings, dtype,
+                   device, lib)
 
     def __init__(self, num_layers, num_kv_heads, head_dim, num_physical_blocks,
                  max_position_embeddings, dtype=torch.bfloat16, device="cuda", lib=None):

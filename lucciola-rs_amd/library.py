@@ -33,30 +33,31 @@ SIGNATURES = {
     "luc_rope_table": (_i32, [_vp, _vp, _i32, _i32, _f32, _f32]),
     "luc_rope": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32,
                         _i32]),
-    "luc_kv_cache_update": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i32, _vp,
-                                   _i32, _i32, _i32, _i32, _i32, _i32]),
+    "luc_kv_cache_update": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i32, _i32,
+                                   _vp, _i32, _i32, _i32, _i32, _i32, _i32]),
     "luc_rope_append": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
-                               _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+                               _vp, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
+                               _i32]),
     "luc_paged_decode_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
-    "luc_paged_decode": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i32, _vp,
-                                _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp,
-                                _sz]),
+    "luc_paged_decode": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i32, _i32,
+                                _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32,
+                                _vp, _sz]),
     "luc_decode_step": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                               _i32, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
-                               _i32, _vp, _i64, _vp, _sz]),
+                               _i32, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                               _f32, _i32, _vp, _i64, _vp, _sz]),
     "luc_decode_step_noalloc": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
-                                       _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
-                                       _i32, _i32, _f32, _i32, _vp, _i64]),
+                                       _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _i32, _i32,
+                                       _i32, _i32, _i32, _f32, _i32, _vp, _i64]),
     "luc_paged_prefill": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                                 _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-                                 _i32, _i32, _f32, _vp, _i64]),
+                                 _vp, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
+                                 _i32, _i32, _i32, _f32, _vp, _i64]),
     "luc_rmsnorm": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _f32, _i32, _i32]),
     "luc_silu_mul": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32]),
     "luc_embedding": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32]),
     "luc_argmax": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp]),
     "luc_sort_and_sample": (_i32, [_vp, _vp, _i32, _vp, _i32, _f32, _i32, _f32, _vp, _sz, _vp]),
-    "luc_gather_floor": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32,
-                                _i32, _vp]),
+    "luc_gather_floor": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _i32,
+                                _i32, _i32, _vp]),
     "luc_stream_read": (_i32, [_vp, _vp, _vp, _sz, _vp]),
     "luc_blocks_create": (_i32, [_i32, _i32, _i32, ctypes.POINTER(_vp)]),
     "luc_blocks_destroy": (None, [_vp]),
@@ -114,6 +115,14 @@ def _p(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def pool_pages(pool, num_layers, num_kv_heads, head_dim) -> int:
+    """Pages in a K/V pool tensor ([pages][layers][kv heads][16][head_dim], or
+    the same elements flat)."""
+    if pool.dim() == 5:
+        return int(pool.shape[0])
+    return int(pool.numel() // (num_layers * num_kv_heads * 16 * head_dim))
+
+
 def _stream(stream):
     if stream is None:
         stream = torch.cuda.current_stream()
@@ -167,43 +176,48 @@ class LucAttn:
 
     def kv_cache_update(self, k_pool, v_pool, k, v, v_bias, row_stride, tables, positions,
                         num_tokens, layer, num_layers, hkv, head_dim, block_size=16,
-                        stream=None):
+                        stream=None, num_blocks=None):
+        nb = num_blocks if num_blocks is not None else pool_pages(k_pool, num_layers, hkv, head_dim)
         self._check(self.lib.luc_kv_cache_update(
             self.ctx, _stream(stream), dtype_code(k_pool), _p(k_pool), _p(v_pool), _p(k), _p(v),
-            _p(v_bias), row_stride, _p(tables), tables.shape[-1], _p(positions), num_tokens,
+            _p(v_bias), row_stride, _p(tables), tables.shape[-1], nb, _p(positions), num_tokens,
             layer, num_layers, hkv, head_dim, block_size))
 
     def rope_append(self, q, q_bias, k, k_bias, v, v_bias, row_stride, cos, sin, positions,
                     tables, k_pool, v_pool, num_tokens, layer, num_layers, hq, hkv, head_dim,
-                    block_size=16, stream=None):
+                    block_size=16, stream=None, num_blocks=None):
+        nb = num_blocks if num_blocks is not None else pool_pages(k_pool, num_layers, hkv, head_dim)
         self._check(self.lib.luc_rope_append(
             self.ctx, _stream(stream), dtype_code(k_pool), _p(q), _p(q_bias), _p(k), _p(k_bias),
             _p(v), _p(v_bias), row_stride, _p(cos), _p(sin), _p(positions), _p(tables),
-            tables.shape[-1], _p(k_pool), _p(v_pool), num_tokens, layer, num_layers, hq, hkv,
+            tables.shape[-1], nb, _p(k_pool), _p(v_pool), num_tokens, layer, num_layers, hq, hkv,
             head_dim, block_size))
 
     def paged_decode(self, out, q, k_pool, v_pool, tables, positions, batch, max_ctx, layer,
                      num_layers, hq, hkv, head_dim, sm_scale, split_tokens=0, workspace=None,
-                     out_row_stride=None, q_row_stride=None, block_size=16, stream=None):
+                     out_row_stride=None, q_row_stride=None, block_size=16, stream=None,
+                     num_blocks=None):
         ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        nb = num_blocks if num_blocks is not None else pool_pages(k_pool, num_layers, hkv, head_dim)
         self._check(self.lib.luc_paged_decode(
             self.ctx, _stream(stream), dtype_code(k_pool), _p(out),
             out_row_stride if out_row_stride is not None else hq * head_dim, _p(q),
             q_row_stride if q_row_stride is not None else hq * head_dim, _p(k_pool), _p(v_pool),
-            _p(tables), tables.shape[-1], _p(positions), batch, max_ctx, layer, num_layers, hq,
+            _p(tables), tables.shape[-1], nb, _p(positions), batch, max_ctx, layer, num_layers, hq,
             hkv, head_dim, block_size, sm_scale, split_tokens, _p(workspace), ws_bytes))
 
 
     def decode_step(self, qkv, q_bias, k_bias, v_bias, cos, sin, k_pool, v_pool, tables,
                     positions, batch, max_ctx, layer, num_layers, hq, hkv, head_dim, sm_scale,
                     out, workspace=None, split_tokens=0, qkv_row_stride=None,
-                    out_row_stride=None, block_size=16, stream=None):
+                    out_row_stride=None, block_size=16, stream=None, num_blocks=None):
         ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        nb = num_blocks if num_blocks is not None else pool_pages(k_pool, num_layers, hkv, head_dim)
         self._check(self.lib.luc_decode_step(
             self.ctx, _stream(stream), dtype_code(k_pool), _p(qkv),
             qkv_row_stride if qkv_row_stride is not None else (hq + 2 * hkv) * head_dim,
             _p(q_bias), _p(k_bias), _p(v_bias), _p(cos), _p(sin), _p(k_pool), _p(v_pool),
-            _p(tables), tables.shape[-1], _p(positions), batch, max_ctx, layer, num_layers, hq, hkv,
+            _p(tables), tables.shape[-1], nb, _p(positions), batch, max_ctx, layer, num_layers, hq, hkv,
             head_dim, block_size, sm_scale, split_tokens, _p(out),
             out_row_stride if out_row_stride is not None else hq * head_dim, _p(workspace),
             ws_bytes))
@@ -211,28 +225,30 @@ class LucAttn:
     def decode_step_noalloc(self, qkv, q_bias, k_bias, v_bias, cos, sin, k_pool, v_pool, tables,
                             positions, batch, max_ctx, layer, num_layers, hq, hkv, head_dim,
                             sm_scale, out, split_tokens=0, qkv_row_stride=None,
-                            out_row_stride=None, block_size=16, stream=None):
+                            out_row_stride=None, block_size=16, stream=None, num_blocks=None):
         """luc_decode_step_noalloc: luc_decode_step with the library's fixed
         per-device scratch as its split-K workspace (no workspace argument)."""
+        nb = num_blocks if num_blocks is not None else pool_pages(k_pool, num_layers, hkv, head_dim)
         self._check(self.lib.luc_decode_step_noalloc(
             self.ctx, _stream(stream), dtype_code(k_pool), _p(qkv),
             qkv_row_stride if qkv_row_stride is not None else (hq + 2 * hkv) * head_dim,
             _p(q_bias), _p(k_bias), _p(v_bias), _p(cos), _p(sin), _p(k_pool), _p(v_pool),
-            _p(tables), tables.shape[-1], _p(positions), batch, max_ctx, layer, num_layers, hq, hkv,
+            _p(tables), tables.shape[-1], nb, _p(positions), batch, max_ctx, layer, num_layers, hq, hkv,
             head_dim, block_size, sm_scale, split_tokens, _p(out),
             out_row_stride if out_row_stride is not None else hq * head_dim))
 
     def paged_prefill(self, qkv, q_bias, k_bias, v_bias, cos, sin, k_pool, v_pool, tables,
                       cu_seqlens, start_pos, total_rows, max_ctx, layer, num_layers, hq, hkv,
                       head_dim, sm_scale, out, qkv_row_stride=None, out_row_stride=None,
-                      block_size=16, stream=None):
+                      block_size=16, stream=None, num_blocks=None):
         """luc_paged_prefill: rope + cache write + causal attention of packed
         prompts (cu_seqlens [B+1], start_pos [B] device int32)."""
+        nb = num_blocks if num_blocks is not None else pool_pages(k_pool, num_layers, hkv, head_dim)
         self._check(self.lib.luc_paged_prefill(
             self.ctx, _stream(stream), dtype_code(k_pool), _p(qkv),
             qkv_row_stride if qkv_row_stride is not None else (hq + 2 * hkv) * head_dim,
             _p(q_bias), _p(k_bias), _p(v_bias), _p(cos), _p(sin), _p(k_pool), _p(v_pool),
-            _p(tables), tables.shape[-1], _p(cu_seqlens), _p(start_pos), start_pos.shape[0],
+            _p(tables), tables.shape[-1], nb, _p(cu_seqlens), _p(start_pos), start_pos.shape[0],
             total_rows, max_ctx, layer, num_layers, hq, hkv, head_dim, block_size, sm_scale,
             _p(out), out_row_stride if out_row_stride is not None else hq * head_dim))
 
@@ -261,7 +277,8 @@ class LucAttn:
         split and no arithmetic (sink: a one-element device int32 tensor)."""
         self._check(self.lib.luc_gather_floor(
             self.ctx, _stream(stream), _p(k_pool), _p(v_pool), _p(tables), tables.shape[-1],
-            _p(positions), batch, max_ctx, layer, num_layers, hkv, head_dim, _p(sink)))
+            pool_pages(k_pool, num_layers, hkv, head_dim), _p(positions), batch, max_ctx, layer,
+            num_layers, hkv, head_dim, _p(sink)))
 
     def stream_read(self, src, sink, stream=None):
         """luc_stream_read of the whole of src (a contiguous device tensor)."""

@@ -46,8 +46,8 @@ def test_code_objects_built_for_gfx950():
 
 def test_abi_version_and_error_string():
     cdll = library.load_cdll()
-    assert cdll.luc_abi_version() == 3
-    rc = cdll.luc_paged_decode(None, None, 0, None, 0, None, 0, None, None, None, 0, None, 1,
+    assert cdll.luc_abi_version() == 4
+    rc = cdll.luc_paged_decode(None, None, 0, None, 0, None, 0, None, None, None, 0, 1, None, 1,
                                1, 0, 1, 14, 2, 64, 16, 0.125, 0, None, 0)
     assert rc == -1
     assert b"null context" in cdll.luc_last_error()
@@ -67,9 +67,10 @@ def _decode(cdll, **kw):
     args = dict(ctx=ctypes.c_void_p(1), stream=None, dtype=0, out=ctypes.c_void_p(16),
                 out_stride=14 * 64, q=ctypes.c_void_p(16), q_stride=14 * 64,
                 k_pool=ctypes.c_void_p(256), v_pool=ctypes.c_void_p(512),
-                tables=ctypes.c_void_p(16), table_stride=256, positions=ctypes.c_void_p(16),
-                batch=32, max_ctx=4096, layer=0, num_layers=24, hq=14, hkv=2, head_dim=64,
-                block_size=16, scale=0.125, split=0, ws=None, ws_bytes=0)
+                tables=ctypes.c_void_p(16), table_stride=256, num_blocks=16384,
+                positions=ctypes.c_void_p(16), batch=32, max_ctx=4096, layer=0, num_layers=24,
+                hq=14, hkv=2, head_dim=64, block_size=16, scale=0.125, split=0, ws=None,
+                ws_bytes=0)
     args.update(kw)
     rc = cdll.luc_paged_decode(*args.values())
     return rc, cdll.luc_last_error().decode()
@@ -88,6 +89,9 @@ def test_decode_argument_checks(cdll):
     assert _decode(cdll, positions=None)[0] == -1
     assert _decode(cdll, batch=0)[0] == 0                  # empty batch: no-op
     assert _decode(cdll, max_ctx=0)[0] == -1
+    assert _decode(cdll, num_blocks=0)[0] == -1           # a pool of no pages
+    rc, msg = _decode(cdll, num_blocks=-3)
+    assert rc == -1 and "num_blocks" in msg
 
 
 def test_workspace_size_policy(cdll):
@@ -160,12 +164,13 @@ def test_decode_step_argument_checks(cdll):
                     qkv_stride=18 * 64, qb=None, kb=None, vb=None, cos=ctypes.c_void_p(16),
                     sin=ctypes.c_void_p(16), k_pool=ctypes.c_void_p(256),
                     v_pool=ctypes.c_void_p(512), tables=ctypes.c_void_p(16), table_stride=256,
-                    positions=ctypes.c_void_p(16), batch=32, max_ctx=4096, layer=0,
+                    num_blocks=16384, positions=ctypes.c_void_p(16), batch=32, max_ctx=4096, layer=0,
                     num_layers=24, hq=14, hkv=2, head_dim=64, block_size=16, scale=0.125,
                     split=0, out=ctypes.c_void_p(16), out_stride=14 * 64, ws=None, ws_bytes=0)
         args.update(kw)
         return cdll.luc_decode_step(*args.values())
     assert call(qkv_stride=14 * 64) == -1      # a qkv row holds q, k and v
+    assert call(num_blocks=0) == -1
     assert call(cos=None) == -1
     assert call(head_dim=80) == -2
     assert call(ws=None, ws_bytes=0) == -5     # split-K needs the workspace
@@ -185,7 +190,8 @@ def test_prefill_argument_checks(cdll):
                     qkv_stride=18 * 64, qb=None, kb=None, vb=None, cos=ctypes.c_void_p(16),
                     sin=ctypes.c_void_p(16), k_pool=ctypes.c_void_p(256),
                     v_pool=ctypes.c_void_p(512), tables=ctypes.c_void_p(16), table_stride=129,
-                    cu=ctypes.c_void_p(16), start=ctypes.c_void_p(16), batch=4, total=8192,
+                    num_blocks=512, cu=ctypes.c_void_p(16), start=ctypes.c_void_p(16), batch=4,
+                    total=8192,
                     max_ctx=2048, layer=0, num_layers=24, hq=14, hkv=2, head_dim=64,
                     block_size=16, scale=0.125, out=ctypes.c_void_p(256), out_stride=14 * 64)
         args.update(kw)
@@ -197,6 +203,7 @@ def test_prefill_argument_checks(cdll):
     assert call(out_stride=14 * 64 + 2) == -1
     assert call(cu=None) == -1 and call(start=None) == -1 and call(cos=None) == -1
     assert call(table_stride=127) == -1                   # 127 pages < 2048 tokens
+    assert call(num_blocks=0) == -1
     assert call(head_dim=80) == -2
     assert call(hq=18) == -2                              # group 9 > 8
     assert call(hq=15) == -1                              # not a multiple of hkv
