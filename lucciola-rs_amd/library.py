@@ -71,11 +71,14 @@ SIGNATURES = {
 
 
 def lib_dir() -> str:
+    """Directory of the gfx950 code objects (and of liblucattn.so)."""
     return os.path.join(_HERE, "lib")
 
 
 def lib_path() -> str:
-    return os.path.join(lib_dir(), "liblucattn.so")
+    """liblucattn.so in lib/, or LUC_LIB_PATH: another build of the same
+    sources (the CPU sanitizer build of sanitize.py)."""
+    return os.environ.get("LUC_LIB_PATH") or os.path.join(lib_dir(), "liblucattn.so")
 
 
 class LucError(RuntimeError):

@@ -18,7 +18,8 @@ import numpy as np
 
 DTYPES = {"bf16": 0, "f16": 1}
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libluc_oracle.so")
+# LUC_ORACLE_LIB: another build of the same source (the CPU sanitizer build)
+LIB_PATH = os.environ.get("LUC_ORACLE_LIB") or os.path.join(_HERE, "libluc_oracle.so")
 
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _i32p = ctypes.POINTER(ctypes.c_int32)
