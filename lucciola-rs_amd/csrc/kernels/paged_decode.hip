@@ -682,6 +682,10 @@ __device__ void decode_impl(const DecodeArgs& A) {
   const int jend = (s_end - 1 - s_begin) / kPage;  // last page of the split
   // single-tile kernel: the pages of this wave's tile (clamped to the split)
   int tpage[S::PAGES];
+  // T1: table entry of the new token's page (page jt_new of the owner wave's
+  // tile; only the owner uses it)
+  const int jt_new = (pos - t_first) / kPage;
+  int new_raw = 0;
   if constexpr (T1) {
 #pragma unroll
     for (int i = 0; i < S::PAGES; ++i) {
@@ -694,22 +698,9 @@ __device__ void decode_impl(const DecodeArgs& A) {
       const bool ok = t >= 0 && t < nb;
       if (!ok && ntw > 0) bad_page = true;
       tpage[i] = ok ? t : 0;
+      new_raw = jt_new == i ? t : new_raw;
     }
   }
-
-  // table entry of the new token's page (the owner wave's cache write)
-  auto page_raw_of_new = [&]() __attribute__((always_inline)) -> int {
-    if constexpr (T1) {  // in the owner's only tile: one of its pages
-      const int jt = (pos - t_first) / kPage;
-      const int e = min(max(min(p0 + j0 + jt, p0 + jend) - tstart, 0), S::PAGES - 1);
-      int t = traw[0];
-#pragma unroll
-      for (int k = 1; k < S::PAGES; ++k) t = e == k ? traw[k] : t;
-      return t;
-    } else {
-      return page_raw((pos - s_begin) / kPage);
-    }
-  };
 
   // The step variant's prologue operands (q and k of the new token with their
   // biases, the cos/sin row, v + v_bias) are loaded before the KV stream is
@@ -1150,7 +1141,9 @@ __device__ void decode_impl(const DecodeArgs& A) {
 
   if constexpr (APPEND) {
     // the cache write of the new token (none through a page outside the pool)
-    const int new_page = page_raw_of_new();
+    int new_page;
+    if constexpr (T1) new_page = new_raw;
+    else new_page = page_raw((pos - s_begin) / kPage);
     if (owns && lane < S::CH && new_page >= 0 && new_page < nb) {
       const int64_t slot = (int64_t)new_page * page_stride + head_off + (int64_t)(pos % kPage) * D + lane * 8;
       *(uint4*)(A.k_pool + slot) = *(const uint4*)(s_knew[qi] + lane * 8);

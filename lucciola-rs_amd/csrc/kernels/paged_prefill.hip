@@ -18,8 +18,11 @@
 // and then tile p: causal tile t reads about t+1 token blocks, so every pair
 // carries the same work, the grid is one wave of equal workgroups and none
 // waits on a long tail.  For each tile the workgroup walks the tokens
-// 0..(last position of its rows) in blocks of 64, in a three-stage LDS ring:
-// blocks i+1 and i+2 load while block i is computed.
+// 0..(last position of its rows) in blocks of 64, grouped into super-blocks
+// (two blocks at head_dim 64 with 8 waves, else one) in an LDS ring of NS
+// stages (four at head_dim 64, three at 128): super-block J + NS - 2 loads
+// while super-block J is computed, and the waves meet at one barrier per
+// super-block.
 //   - K and V blocks [64 tokens][D] straight into LDS (global_load_lds_dwordx4,
 //     one wave-wide load = 1 KB of a page), each token row XOR-swizzled by
 //     16-byte chunk so the operand reads below do not collide.  Tokens past
@@ -125,6 +128,74 @@ __device__ inline void lds_tr16x2(uint32_t a, uint2* x) {
       : "=&v"(x[0]), "=&v"(x[1])
       : "v"(a), "n"(OFF0), "n"(OFF1)
       : "memory");
+}
+
+// head_dim 64: the operand reads of one block, issued ahead of the VALU work
+// that hides their latency, and waited for separately.  The outputs are not
+// valid until the matching wait, whose "+v" operands keep every use behind it.
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+// K of a 64-token block: chunk k of token lane % 32 of each 32-token half
+// (x[k] first half, x[4 + k] second half, HOFF bytes further)
+template <int HOFF>
+__device__ inline void lds_k_issue(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, u32x4_t* x) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %9\n\t"
+      "ds_read_b128 %2, %10\n\t"
+      "ds_read_b128 %3, %11\n\t"
+      "ds_read_b128 %4, %8 offset:%12\n\t"
+      "ds_read_b128 %5, %9 offset:%12\n\t"
+      "ds_read_b128 %6, %10 offset:%12\n\t"
+      "ds_read_b128 %7, %11 offset:%12"
+      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]),
+        "=&v"(x[6]), "=&v"(x[7])
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "n"(HOFF)
+      : "memory");
+}
+__device__ inline void lds_wait_k(u32x4_t* x) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),
+                 "+v"(x[6]), "+v"(x[7])
+               :
+               : "memory");
+}
+// V^T of a 64-token block (row stride R bytes): x[4c + 2db + j] is the
+// transposing read of token group 16c + 8j through address a_db, i.e. the
+// 8-byte halves of the A operand of PV step c = (32-token half, 16-token
+// step) and 32-dim tile db
+template <int R>
+__device__ inline void lds_v_issue(uint32_t a0, uint32_t a1, u32x2_t* x) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %16 offset:%18\n\t"
+      "ds_read_b64_tr_b16 %1, %16 offset:%19\n\t"
+      "ds_read_b64_tr_b16 %2, %17 offset:%18\n\t"
+      "ds_read_b64_tr_b16 %3, %17 offset:%19\n\t"
+      "ds_read_b64_tr_b16 %4, %16 offset:%20\n\t"
+      "ds_read_b64_tr_b16 %5, %16 offset:%21\n\t"
+      "ds_read_b64_tr_b16 %6, %17 offset:%20\n\t"
+      "ds_read_b64_tr_b16 %7, %17 offset:%21\n\t"
+      "ds_read_b64_tr_b16 %8, %16 offset:%22\n\t"
+      "ds_read_b64_tr_b16 %9, %16 offset:%23\n\t"
+      "ds_read_b64_tr_b16 %10, %17 offset:%22\n\t"
+      "ds_read_b64_tr_b16 %11, %17 offset:%23\n\t"
+      "ds_read_b64_tr_b16 %12, %16 offset:%24\n\t"
+      "ds_read_b64_tr_b16 %13, %16 offset:%25\n\t"
+      "ds_read_b64_tr_b16 %14, %17 offset:%24\n\t"
+      "ds_read_b64_tr_b16 %15, %17 offset:%25"
+      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]),
+        "=&v"(x[6]), "=&v"(x[7]), "=&v"(x[8]), "=&v"(x[9]), "=&v"(x[10]), "=&v"(x[11]),
+        "=&v"(x[12]), "=&v"(x[13]), "=&v"(x[14]), "=&v"(x[15])
+      : "v"(a0), "v"(a1), "n"(0), "n"(8 * R), "n"(16 * R), "n"(24 * R), "n"(32 * R),
+        "n"(40 * R), "n"(48 * R), "n"(56 * R)
+      : "memory");
+}
+__device__ inline void lds_wait_v(u32x2_t* x) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),
+                 "+v"(x[6]), "+v"(x[7]), "+v"(x[8]), "+v"(x[9]), "+v"(x[10]), "+v"(x[11]),
+                 "+v"(x[12]), "+v"(x[13]), "+v"(x[14]), "+v"(x[15])
+               :
+               : "memory");
 }
 
 // Waves per prefill workgroup for group size G (<= 8).
@@ -329,7 +400,8 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   const uint4 ones = make_uint4(one2, one2, one2, one2);
 
   // ---- mask, online softmax (exp2 domain) and O^T += V^T P^T of block blk ----
-  auto softmax_pv = [&](int blk, f32x16* sc) __attribute__((always_inline)) {
+  // (a) mask, block max and the lazy move of the running max
+  auto softmax_max = [&](int blk, f32x16* sc) __attribute__((always_inline)) {
     const int t0 = blk * BT;
     // sc[hf][4i + j]: token t0 + 32hf + 8i + 4g + j, q row my_i
     float mb = -INFINITY;
@@ -370,10 +442,26 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) osum[e] *= alpha;
     }
+  };
+  // (b) the weights exp2(s * scale - m)
+  auto softmax_exp = [&](f32x16* sc) __attribute__((always_inline)) {
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[hf][e] = __builtin_amdgcn_exp2f(fmaf(sc[hf][e], scale, -m_run));
+  };
+  // B = P^T of PV step (hf, mm): slots 0..3 = tokens 16mm + 4g + j, slots
+  // 4..7 = 16mm + 8 + 4g + j of half hf
+  auto p_operand = [&](const f32x16* sc, int hf, int mm) __attribute__((always_inline)) {
+    const int i0 = 2 * mm, i1 = 2 * mm + 1;
+    return make_uint4(pack2(sc[hf][4 * i0], sc[hf][4 * i0 + 1], DT),
+                      pack2(sc[hf][4 * i0 + 2], sc[hf][4 * i0 + 3], DT),
+                      pack2(sc[hf][4 * i1], sc[hf][4 * i1 + 1], DT),
+                      pack2(sc[hf][4 * i1 + 2], sc[hf][4 * i1 + 3], DT));
+  };
+  auto softmax_pv = [&](int blk, f32x16* sc) __attribute__((always_inline)) {
+    softmax_max(blk, sc);
+    softmax_exp(sc);
 
     // O^T += V^T P^T, 16 tokens per MFMA
     const uint32_t vbase = lds_addr(s_kv[(blk / SB) % NS][1]) + (blk % SB) * KB;
@@ -409,20 +497,68 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   // and the barrier also tells every wave that super-block J-2 is consumed,
   // so its stage takes super-block J + NS - 2.
   const int nsb = (nblk + SB - 1) / SB;
+  auto boundary = [&](int blk) __attribute__((always_inline)) {  // before block blk + 1
+    if ((blk + 1) % SB == 0) {
+      const int J = (blk + 1) / SB;
+      wait_blocks(min(NS - 3, nsb - 1 - J));
+      __builtin_amdgcn_s_barrier();
+      if (J + NS - 2 < nsb) {
+        issue(J + NS - 2, (J + NS - 2) % NS, pgn);
+        if (J + NS - 1 < nsb) load_pages(J + NS - 1, pgn);
+      }
+    }
+  };
   auto step = [&](int blk, f32x16* cur, f32x16* nxt) __attribute__((always_inline)) {
-    if (blk + 1 < nblk) {
-      if ((blk + 1) % SB == 0) {
-        const int J = (blk + 1) / SB;
-        wait_blocks(min(NS - 3, nsb - 1 - J));
-        __builtin_amdgcn_s_barrier();
-        if (J + NS - 2 < nsb) {
-          issue(J + NS - 2, (J + NS - 2) % NS, pgn);
-          if (J + NS - 1 < nsb) load_pages(J + NS - 1, pgn);
+    if constexpr (D == 64) {
+      // the LDS reads of K(blk + 1) go out before the mask and max of block
+      // blk, those of V(blk) before its exponentials, so both land while
+      // the VALU works; the scores of blk + 1 reach the matrix cores before
+      // the exponentials, the PV of blk after them
+      u32x4_t ka[8];
+      u32x2_t va[16];
+      const bool has_next = blk + 1 < nblk;
+      if (has_next) {
+        boundary(blk);
+        if (active) {
+          const uint32_t kbase = lds_addr(s_kv[((blk + 1) / SB) % NS][0]) + ((blk + 1) % SB) * KB;
+          lds_k_issue<32 * ROWB>(kbase + krel[0], kbase + krel[1], kbase + krel[2], kbase + krel[3], ka);
         }
       }
-      if (active) qk(blk + 1, nxt);
+      if (active) {
+        softmax_max(blk, cur);
+        if (has_next) {
+          lds_wait_k(ka);
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) nxt[hf][e] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NK; ++k)
+              nxt[hf] = mfma32<DT>(__builtin_bit_cast(uint4, ka[4 * hf + k]), qf[k], nxt[hf]);
+          }
+        }
+        const uint32_t vbase = lds_addr(s_kv[(blk / SB) % NS][1]) + (blk % SB) * KB;
+        lds_v_issue<ROWB>(vbase + vrel[0], vbase + vrel[1], va);
+        softmax_exp(cur);
+        lds_wait_v(va);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint4 pb = p_operand(cur, c >> 1, c & 1);
+          osum = mfma32<DT>(ones, pb, osum);
+#pragma unroll
+          for (int db = 0; db < ND; ++db)
+            o[db] = mfma32<DT>(make_uint4(va[4 * c + 2 * db].x, va[4 * c + 2 * db].y,
+                                          va[4 * c + 2 * db + 1].x, va[4 * c + 2 * db + 1].y),
+                               pb, o[db]);
+        }
+      }
+    } else {
+      if (blk + 1 < nblk) {
+        boundary(blk);
+        if (active) qk(blk + 1, nxt);
+      }
+      if (active) softmax_pv(blk, cur);
     }
-    if (active) softmax_pv(blk, cur);
   };
 
   // every wave is done with the previous tile's last stage before it is refilled

@@ -70,7 +70,12 @@ constexpr int kDecodeWaves = 4;
 int decode_tile(int head_dim) { return head_dim == 64 ? 64 : 32; }
 constexpr int kMaxSplitTokens = 128 * LUC_BLOCK_SIZE;
 // Tiles the automatic split choice plans to have in flight at once: about two
-// single-tile waves per SIMD of an MI355X (256 CUs x 4 SIMDs).
+// single-tile waves per SIMD of an MI355X (256 CUs x 4 SIMDs).  The
+// two-tile kernels hold twice the LDS (two workgroups per CU instead of
+// four), so a plan that needs them is made again for half as many tiles:
+// one round of resident workgroups instead of two (batch8_32k, 8 x 32768
+// tokens at head_dim 128: 1024-token splits, 55.7 us per launch against
+// 59.7 us with 512).
 constexpr int kPlanTiles = 256 * 4 * 2;
 
 const char* dt_name(int dtype) { return dtype == LUC_F16 ? "f16" : "bf16"; }
@@ -212,7 +217,7 @@ constexpr int kMaxSplits = 256;
 // each wave at most one tile (the _t1 kernels); longer splits walk two tiles
 // at a time per wave (_t2).  The automatic choice assumes the mean context is
 // half of max_ctx and takes the shortest split that keeps about kPlanTiles
-// tiles per round.  It depends only on the arguments, so
+// tiles per round (kPlanTiles / 2 for the two-tile kernels).  It depends only on the arguments, so
 // luc_paged_decode_workspace_size agrees with the launch.  Returns 0 when
 // max_ctx cannot be covered by kMaxSplits splits.
 int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requested) {
@@ -226,6 +231,7 @@ int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requeste
     const int64_t tiles = (int64_t)batch * hkv *
                           std::max<int64_t>(ceil_div(ceil_div(max_ctx, 2), decode_tile(head_dim)), 1);
     st = ceil_div(tiles, kPlanTiles) * unit;
+    if (st > unit) st = ceil_div(tiles, kPlanTiles / 2) * unit;
   }
   st = std::min<int64_t>(std::max<int64_t>(st, floor_tokens), kMaxSplitTokens);
   return (int)st;

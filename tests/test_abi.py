@@ -119,8 +119,11 @@ def test_workspace_size_policy(cdll):
     # the automatic split keeps about 2048 tiles per round: the batch32_mixed
     # shape (mean context about half of 4096) gets one tile per wave
     assert ws(32, 14, 2, 64, 4096, 0) == expect(32, 14, 2, 64, 16)
-    # ... and longer batches get longer splits
+    # ... and longer batches get longer splits, planned for half as many
+    # tiles once they need the two-tile kernels (two workgroups per CU):
+    # 8 x 32768 tokens at d=128 -> 1024-token splits
     assert ws(64, 28, 4, 128, 16384, 0) == expect(64, 28, 4, 128, 16384 // 2048)
+    assert ws(8, 12, 2, 128, 32768, 0) == expect(8, 12, 2, 128, 32768 // 1024)
     # a split holds at most 128 pages: longer contexts than 256 x 2048 tokens
     # are not supported
     assert ws(1, 4, 1, 64, 256 * 2048, 0) > 0
