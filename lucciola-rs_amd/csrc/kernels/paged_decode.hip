@@ -673,11 +673,9 @@ __device__ void decode_impl(const DecodeArgs& A) {
   };
   auto page_of = [&](int j) -> int64_t {  // physical page j of the split, inside the pool
     const int p = page_raw(j);
-    if (p < 0 || p >= nb) {
-      bad_page = true;
-      return 0;
-    }
-    return p;
+    const bool ok = p >= 0 && p < nb;
+    bad_page |= !ok;
+    return ok ? p : 0;
   };
   const int jend = (s_end - 1 - s_begin) / kPage;  // last page of the split
   // single-tile kernel: the pages of this wave's tile (clamped to the split)
