@@ -516,6 +516,23 @@ __device__ __attribute__((always_inline)) inline void finish_split(
   }
 
   // ---- the last split of (b, h) to finish merges the partials ----
+  // Ordering of the hand-off (message passing between workgroups that may
+  // sit on different XCDs):
+  //  - every partial is written and read only by agent-scope atomic accesses
+  //    (global_store / global_load with sc1): each one is performed at the
+  //    point of coherence of the whole device, never in a non-coherent cache;
+  //  - the compiler keeps the order: the volatile asm with a "memory" clobber
+  //    and the barriers let no memory access move across them;
+  //  - the hardware keeps the order: s_waitcnt vmcnt(0) returns only when
+  //    this wave's stores are acknowledged, so every partial has reached the
+  //    point of coherence before the barrier and thread 0's counter update;
+  //  - the merging workgroup issues its partial loads only after its update
+  //    returned nsplit - 1 (passed on through s_last and a barrier), so
+  //    they are performed after every other split's stores.
+  // A release / acquire pair at agent scope would add a write-back and an
+  // invalidation of the whole L2 (buffer_wbl2 / buffer_inv), needed only for
+  // data written by plain stores; none of the merge's data is, and with them
+  // the kernel measured 5x slower.
   if (nsplit > 1) {
     // this wave's partial stores have completed (at agent scope) before the
     // workgroup's arrival is counted
