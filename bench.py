@@ -33,7 +33,9 @@ Also reported:
                 batch64_long (B=64, 28q/4kv, d=128, bf16, ctx U{1024..16384})
                 and batch8_32k (B=8, 12q/2kv, d=128, bf16, ctx 32768), 4
                 layers rotated, per launch: us, algorithmic GB/s, fraction
-                of 8 TB/s;
+                of 8 TB/s, and the two memory floors below for the same
+                bytes (the gather with 4-tile workgroups, not the long
+                splits the decode kernel uses there);
   floors        (in roofline) luc_gather_floor: the same K/V page slabs as
                 the decode kernel reads, with its work split and no
                 arithmetic, and luc_stream_read: the same bytes read
@@ -279,6 +281,7 @@ def long_context_bench(lib, torch, name, seed, layers=4, launches=40):
            "layers_rotated": layers, "us_per_launch": round(us, 2),
            "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbs": round(gbs, 1),
            "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    res.update(floors(lib, torch, cfg, inp, max_ctx, layers, nbytes, launches=launches))
     del inp
     torch.cuda.empty_cache()
     return res
