@@ -115,7 +115,8 @@ int luc_rope_append(luc_ctx* ctx, void* stream, int dtype, void* q, const void* 
 /* Bytes of split-K workspace luc_paged_decode / luc_decode_step need for these
  * sizes (0 when every sequence fits one split; the workspace may then be
  * NULL).  split_tokens: tokens per split-K chunk, rounded up to a multiple of
- * 64 (head_dim 64) or 32 (head_dim 128); 0 = the library's choice.
+ * 256 (head_dim 64) or 128 (head_dim 128), i.e. of 4 tiles of 8 KB of K;
+ * 0 = the library's choice.
  * The workspace must be 256-byte aligned and zero-filled once before its
  * first use; every launch leaves it ready for the next (its split arrival
  * counters, the first 256 KiB, return to zero), whatever the batch and

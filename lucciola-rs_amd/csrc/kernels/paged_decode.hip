@@ -21,14 +21,14 @@
 // across XCDs).
 //
 // Decode kernel work decomposition:
-//   Workgroup = 4 waves = (split, sequence b, kv head h), split-major, so the
+//   Workgroup = W waves = (split, sequence b, kv head h), split-major, so the
 //   splits every sequence has are dispatched first and the workgroups of
 //   splits past a context exit at once.  The G = Hq/Hkv q-heads of kv head h
 //   are processed together, so each KV page is read from HBM once per kv
-//   head (GQA).  Wave w takes tiles w, w + 4, ... of the split: 8 KB tiles of
-//   K (64 tokens at head_dim 64, 32 at 128).  The _t1 kernels give each wave
-//   one tile (a split of 4 tiles); the _t2 kernels walk two tiles at a time,
-//   tile i computed while tile i+1 lands.
+//   head (GQA).  Wave w takes tiles w, w + W, ... of the split: 8 KB tiles of
+//   K (64 tokens at head_dim 64, 32 at 128).  The _t1 kernels have 8 waves,
+//   one tile each (a split of 8 tiles); the _t2 kernels have 4 waves that
+//   walk two tiles at a time, tile i computed while tile i+1 lands.
 //   Prologue: the wave's block-table entries come through the scalar cache;
 //   in the single-tile kernels q arrives by direct-to-LDS loads issued between
 //   the tile's K and V loads, and the step variant's operands (q, k, v, their
@@ -52,7 +52,7 @@
 //        t + TILE/2 packed as an fp16 pair, V of the same two tokens paired by
 //        v_perm, one v_dot2_f32_f16 per (head, dim).  bf16: f32 FMA.
 //   Each wave's token groups are reduced with permlane swaps
-//   (reduce-scatter); the 4 waves merge their (m, l, o) through LDS.  A
+//   (reduce-scatter); the W waves merge their (m, l, o) through LDS.  A
 //   sequence with one split writes its output; otherwise each split writes
 //   (m, l, o) to the workspace and the last split to arrive merges them.
 //   The step variant's last workgroup also writes the roped q and k of the
@@ -1176,23 +1176,22 @@ __device__ void decode_impl(const DecodeArgs& A) {
 
 }  // namespace luc
 
-// Decode kernels: kDecodeWaves = 4 waves per workgroup; _t1 keeps one tile
-// per wave (splits of 4 tiles), _t2 two tiles in flight per wave (longer
-// splits).  Resident-wave targets are per SIMD.
-#define LUC_DECODE_W 4
-#define LUC_DECODE_KERNELS(DTN, DT, D, G, NB, OCC)                                                  \
-  extern "C" __global__ __launch_bounds__(64 * LUC_DECODE_W) __attribute__((amdgpu_waves_per_eu(OCC))) \
+// Decode kernels: _t1 has 8 waves per workgroup, one tile each (splits of 8
+// tiles; 80 KB of LDS, two workgroups per CU), _t2 has 4 waves with two
+// tiles in flight each (longer splits).  Resident-wave targets are per SIMD.
+#define LUC_DECODE_KERNELS(DTN, DT, D, G, NB, OCC, W)                                               \
+  extern "C" __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC)))         \
   void luc_decode_##DTN##_d##D##_g##G##_t##NB(luc::DecodeArgs a) {                                  \
-    luc::decode_impl<DT, D, G, false, LUC_DECODE_W, NB>(a);                                         \
+    luc::decode_impl<DT, D, G, false, W, NB>(a);                                                    \
   }                                                                                                 \
-  extern "C" __global__ __launch_bounds__(64 * LUC_DECODE_W) __attribute__((amdgpu_waves_per_eu(OCC))) \
+  extern "C" __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC)))         \
   void luc_decode_step_##DTN##_d##D##_g##G##_t##NB(luc::DecodeArgs a) {                             \
-    luc::decode_impl<DT, D, G, true, LUC_DECODE_W, NB>(a);                                          \
+    luc::decode_impl<DT, D, G, true, W, NB>(a);                                                     \
   }
 
 #define LUC_DECODE(DTN, DT, D, G)                                                                  \
-  LUC_DECODE_KERNELS(DTN, DT, D, G, 1, 2)                                                          \
-  LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2)
+  LUC_DECODE_KERNELS(DTN, DT, D, G, 1, 2, 8)                                                       \
+  LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2, 4)
 
 #define LUC_DECODE_GROUPS(DTN, DT, D)                                                              \
   LUC_DECODE(DTN, DT, D, 1)                                                                        \

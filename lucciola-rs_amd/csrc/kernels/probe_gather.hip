@@ -2,9 +2,9 @@
 //
 // luc_gather_floor_d{64,128}: reads exactly the K and V page slabs a decode
 // step reads -- every (sequence, kv head) unit's pages 0 .. positions[b] / 16
-// through its block-table row, layer `layer` -- with the decode kernel's own
-// work split (workgroup = 4 waves = (split of 4 tiles, sequence, kv head),
-// split-major; a tile is 8 KB of K: 64 tokens at head_dim 64, 32 at 128;
+// through its block-table row, layer `layer` -- with the single-tile decode
+// kernel's work split (workgroup = 8 waves = (split of 8 tiles, sequence, kv
+// head), split-major; a tile is 8 KB of K: 64 tokens at head_dim 64, 32 at 128;
 // page numbers and the position by scalar loads in one round trip) and
 // nothing else: no q, no scores, no merge.  Every lane keeps an XOR of what
 // it read, so no load is dead; the sink is written only if that XOR equals a
@@ -34,7 +34,7 @@ __device__ void gather_floor_impl(const GatherArgs& A) {
   constexpr int TILE = D == 64 ? 64 : 32;       // tokens of 8 KB of K
   constexpr int PAGES = TILE / kPage;           // pages per tile
   constexpr int LPP = 8 / PAGES;                // 1 KB loads per page slab
-  constexpr int W = 4;                          // waves per workgroup, one tile each
+  constexpr int W = 8;                          // waves per workgroup, one tile each
   typedef __attribute__((address_space(4))) const int const_i32;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -76,10 +76,10 @@ __device__ void gather_floor_impl(const GatherArgs& A) {
 
 }  // namespace luc
 
-extern "C" __global__ __launch_bounds__(256) void luc_gather_floor_d64(luc::GatherArgs a) {
+extern "C" __global__ __launch_bounds__(512) void luc_gather_floor_d64(luc::GatherArgs a) {
   luc::gather_floor_impl<64>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void luc_gather_floor_d128(luc::GatherArgs a) {
+extern "C" __global__ __launch_bounds__(512) void luc_gather_floor_d128(luc::GatherArgs a) {
   luc::gather_floor_impl<128>(a);
 }
 

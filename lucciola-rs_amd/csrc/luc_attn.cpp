@@ -66,7 +66,11 @@ constexpr const char* kCodeObjects[] = {"rope_append.hsaco", "paged_decode.hsaco
 // four waves per workgroup, which share one split; tiles of 64 tokens
 // (head_dim 64) or 32 (128); a split's block-table entries are held in two
 // registers (128 pages).
-constexpr int kDecodeWaves = 4;
+// Waves per workgroup: the single-tile kernels (_t1, one tile per wave)
+// have 8, so a split is 8 tiles; the tile-pair kernels (_t2, longer splits)
+// have 4.  Splits are multiples of 4 tiles.
+constexpr int kT1Waves = 8;
+constexpr int kT2Waves = 4;
 int decode_tile(int head_dim) { return head_dim == 64 ? 64 : 32; }
 constexpr int kMaxSplitTokens = 128 * LUC_BLOCK_SIZE;
 // Tiles the automatic split choice plans to have in flight at once: about two
@@ -212,16 +216,20 @@ int check_cache(const void* k_pool, const void* v_pool, const int32_t* tables, i
 // Splits per sequence are capped at kMaxSplits (the merge's LDS weight table).
 constexpr int kMaxSplits = 256;
 
-// Split-K chunk length in tokens: a multiple of one tile per wave of a
-// workgroup (the unit), at most kMaxSplitTokens.  A split of one unit gives
-// each wave at most one tile (the _t1 kernels); longer splits walk two tiles
-// at a time per wave (_t2).  The automatic choice assumes the mean context is
-// half of max_ctx and takes the shortest split that keeps about kPlanTiles
-// tiles per round (kPlanTiles / 2 for the two-tile kernels).  It depends only on the arguments, so
+// Split-K chunk length in tokens: a multiple of 4 tiles (the unit), at most
+// kMaxSplitTokens.  A split of 8 tiles runs the single-tile kernels (_t1:
+// 8 waves, one tile each); every other split the tile-pair kernels (_t2:
+// 4 waves walking tiles w, w+4, ... two at a time).  The automatic choice
+// assumes the mean context is half of max_ctx and takes the shortest split
+// that keeps about kPlanTiles tiles per round (kPlanTiles / 2 for the
+// tile-pair kernels); a plan of one unit becomes the 8-tile single-tile
+// split (batch32_mixed: 512 tokens, 15.4 us per launch against 15.9 for
+// 4-wave workgroups with 256-token splits: half the partials to merge, the
+// same tile per wave).  It depends only on the arguments, so
 // luc_paged_decode_workspace_size agrees with the launch.  Returns 0 when
 // max_ctx cannot be covered by kMaxSplits splits.
 int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requested) {
-  const int unit = kDecodeWaves * decode_tile(head_dim);
+  const int unit = kT2Waves * decode_tile(head_dim);
   const int64_t floor_tokens = ceil_div(ceil_div(max_ctx, kMaxSplits), unit) * unit;
   if (floor_tokens > kMaxSplitTokens) return 0;
   int64_t st;
@@ -232,6 +240,7 @@ int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requeste
                           std::max<int64_t>(ceil_div(ceil_div(max_ctx, 2), decode_tile(head_dim)), 1);
     st = ceil_div(tiles, kPlanTiles) * unit;
     if (st > unit) st = ceil_div(tiles, kPlanTiles / 2) * unit;
+    else st = (int64_t)kT1Waves * decode_tile(head_dim);
   }
   st = std::min<int64_t>(std::max<int64_t>(st, floor_tokens), kMaxSplitTokens);
   return (int)st;
@@ -266,6 +275,7 @@ struct DecodeLaunch {
   luc_decode_args a{};
   hipFunction_t fn = nullptr;  // split-K decode with the merge in its last split
   dim3 grid;
+  int waves = 0;  // per workgroup
 };
 
 // Shared argument checks and argument block of the two decode entry points.
@@ -315,13 +325,14 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
                              std::to_string(group);
   // the single-tile kernel reads a tile's table entries as one vector, which
   // must fit the table row
-  const bool one_tile = st == kDecodeWaves * decode_tile(head_dim) &&
+  const bool one_tile = st == kT1Waves * decode_tile(head_dim) &&
                         table_stride >= decode_tile(head_dim) / LUC_BLOCK_SIZE;
   if (int rc = get_fn(ctx, std::string(step ? "luc_decode_step_" : "luc_decode_") + suffix +
                                (one_tile ? "_t1" : "_t2"),
                       &L->fn))
     return rc;
   L->grid = dim3((unsigned)grid);
+  L->waves = one_tile ? kT1Waves : kT2Waves;
   luc_decode_args& a = L->a;
   a.q = static_cast<uint16_t*>(const_cast<void*>(q));
   a.q_stride = q_row_stride;
@@ -369,7 +380,7 @@ struct PrefillArgs {
 
 int launch_decode(DecodeLaunch& L, void* stream) {
   void* args[] = {&L.a};
-  return launch(L.fn, L.grid, dim3(kDecodeWaves * 64), stream, args);
+  return launch(L.fn, L.grid, dim3(L.waves * 64), stream, args);
 }
 
 }  // namespace
@@ -820,8 +831,8 @@ int luc_gather_floor(luc_ctx* ctx, void* stream, const void* k_pool, const void*
   if (int rc = check_device(ctx)) return rc;
   hipFunction_t fn;
   if (int rc = get_fn(ctx, "luc_gather_floor_d" + std::to_string(head_dim), &fn)) return rc;
-  // the decode kernel's split: 4 waves, one 8 KB K tile each
-  const int split = kDecodeWaves * decode_tile(head_dim);
+  // the single-tile decode kernel's split: 8 waves, one 8 KB K tile each
+  const int split = kT1Waves * decode_tile(head_dim);
   const int64_t grid = ceil_div(max_ctx, split) * batch * num_kv_heads;
   if (grid > INT32_MAX) return fail(LUC_E_INVALID, "grid too large");
   struct {
@@ -835,7 +846,7 @@ int luc_gather_floor(luc_ctx* ctx, void* stream, const void* k_pool, const void*
   } a{k_pool, v_pool, block_tables, table_stride, positions, batch, layer, num_layers,
       num_kv_heads, max_ctx, num_blocks, sink};
   void* args[] = {&a};
-  return launch(fn, dim3((unsigned)grid), dim3(kDecodeWaves * 64), stream, args);
+  return launch(fn, dim3((unsigned)grid), dim3(kT1Waves * 64), stream, args);
 }
 
 int luc_stream_read(luc_ctx* ctx, void* stream, const void* src, size_t bytes, uint32_t* sink) {

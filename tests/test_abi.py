@@ -110,15 +110,16 @@ def test_workspace_size_policy(cdll):
     assert ws(100, 28, 4, 128, 1000, 128) == expect(100, 28, 4, 128, 8)
     # at most 256 splits per sequence: the split grows with the context
     assert ws(1, 4, 1, 64, 64 * 1024, 64) == expect(1, 4, 1, 64, 256)
-    # rounding of the requested split to one tile per wave of a workgroup
-    # (4 x 64 tokens at d=64, 4 x 32 at d=128)
+    # rounding of the requested split to 4 tiles (4 x 64 tokens at d=64,
+    # 4 x 32 at d=128)
     assert ws(2, 14, 2, 64, 1000, 100) == ws(2, 14, 2, 64, 1000, 256)
     assert ws(2, 14, 2, 64, 1000, 257) == expect(2, 14, 2, 64, 2)
     assert ws(2, 14, 2, 128, 1000, 90) == ws(2, 14, 2, 128, 1000, 128)
     assert ws(1, 4, 1, 96, 1000, 0) == 0
     # the automatic split keeps about 2048 tiles per round: the batch32_mixed
-    # shape (mean context about half of 4096) gets one tile per wave
-    assert ws(32, 14, 2, 64, 4096, 0) == expect(32, 14, 2, 64, 16)
+    # shape (mean context about half of 4096) gets one tile per wave, in the
+    # 8-wave single-tile kernel: 8 tiles of 64 tokens per split
+    assert ws(32, 14, 2, 64, 4096, 0) == expect(32, 14, 2, 64, 8)
     # ... and longer batches get longer splits, planned for half as many
     # tiles once they need the two-tile kernels (two workgroups per CU):
     # 8 x 32768 tokens at d=128 -> 1024-token splits
