@@ -298,35 +298,36 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 
   // Page numbers of super-block sb that this wave's loads need: load jj
   // covers TPL tokens of one page (TPL divides the page), jj = i * W + w for
-  // the K and the V part alike.  Wave-uniform, through the scalar cache, and read
-  // one iteration before the loads they address, so no wait on them
-  // precedes a load.
+  // the K and the V part alike.  Wave-uniform table entries through the
+  // scalar cache, read a stage before the loads they address and checked
+  // only there, so their round trip overlaps a block's compute.
   constexpr int NPG = LOADS / W;
+  auto page_index = [&](int sb, int i) { return min(sb * SB * BT + (i * W + w) * TPL, nkv - 1) / kPage; };
+  auto load_pages = [&](int sb, int* pg) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NPG; ++i) pg[i] = ((const const_i32_p*)trow)[page_index(sb, i)];
+  };
   // A page outside the pool is never used as an address: it reads page 0
   // instead, and the rows whose context reaches it get NaN (bad_tok).
   int bad_tok = 0x7fffffff;
-  auto load_pages = [&](int sb, int* pg) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < NPG; ++i) {
-      const int tb = sb * SB * BT + (i * W + w) * TPL;
-      const int lp = min(tb, nkv - 1) / kPage;
-      const int p = ((const const_i32_p*)trow)[lp];
-      const bool ok = p >= 0 && p < A.num_blocks;
-      if (!ok) bad_tok = min(bad_tok, lp * kPage);
-      pg[i] = ok ? p : 0;
-    }
-  };
-  int pgn[NPG];  // pages of the next block to issue
+  int pgn[NPG];  // table entries of the next super-block to issue
   // Issue the K and V loads of super-block sb into stage st: 2*LOADS
   // wave-wide loads shared round-robin by the waves.  Tokens past the context
   // re-read token nkv - 1 (finite), so their zero weights contribute exactly
   // zero.
   auto issue = [&](int sb, int st, const int* pg) __attribute__((always_inline)) {
+    int pv[NPG];
+#pragma unroll
+    for (int i = 0; i < NPG; ++i) {
+      const bool ok = pg[i] >= 0 && pg[i] < A.num_blocks;
+      if (!ok) bad_tok = min(bad_tok, page_index(sb, i) * kPage);
+      pv[i] = ok ? pg[i] : 0;
+    }
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int kv = i * W / LOADS, jj = i * W % LOADS + w;
       const int tb = sb * SB * BT + jj * TPL;
-      const int page = pg[i % NPG];
+      const int page = pv[i % NPG];
       const int tl = jj * TPL + lane / CH;  // token within the block
       const int c = lane % CH;
       const int t = min(tb + lane / CH, nkv - 1);
@@ -497,15 +498,23 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   // and the barrier also tells every wave that super-block J-2 is consumed,
   // so its stage takes super-block J + NS - 2.
   const int nsb = (nblk + SB - 1) / SB;
-  auto boundary = [&](int blk) __attribute__((always_inline)) {  // before block blk + 1
+  auto boundary = [&](int blk, bool prefetch) __attribute__((always_inline)) {  // before block blk + 1
     if ((blk + 1) % SB == 0) {
       const int J = (blk + 1) / SB;
       wait_blocks(min(NS - 3, nsb - 1 - J));
       __builtin_amdgcn_s_barrier();
       if (J + NS - 2 < nsb) {
         issue(J + NS - 2, (J + NS - 2) % NS, pgn);
-        if (J + NS - 1 < nsb) load_pages(J + NS - 1, pgn);
+        if (prefetch && J + NS - 1 < nsb) load_pages(J + NS - 1, pgn);
       }
+    }
+  };
+  // the table entries the next boundary issues from, read once this block's
+  // work is issued (head_dim 64)
+  auto prefetch_pages = [&](int blk) __attribute__((always_inline)) {
+    if ((blk + 1) % SB == 0) {
+      const int J = (blk + 1) / SB;
+      if (J + NS - 1 < nsb) load_pages(J + NS - 1, pgn);
     }
   };
   auto step = [&](int blk, f32x16* cur, f32x16* nxt) __attribute__((always_inline)) {
@@ -518,7 +527,7 @@ __device__ void prefill_impl(const PrefillArgs& A) {
       u32x2_t va[16];
       const bool has_next = blk + 1 < nblk;
       if (has_next) {
-        boundary(blk);
+        boundary(blk, false);
         if (active) {
           const uint32_t kbase = lds_addr(s_kv[((blk + 1) / SB) % NS][0]) + ((blk + 1) % SB) * KB;
           lds_k_issue<32 * ROWB>(kbase + krel[0], kbase + krel[1], kbase + krel[2], kbase + krel[3], ka);
@@ -552,9 +561,10 @@ __device__ void prefill_impl(const PrefillArgs& A) {
                                pb, o[db]);
         }
       }
+      if (has_next) prefetch_pages(blk);
     } else {
       if (blk + 1 < nblk) {
-        boundary(blk);
+        boundary(blk, true);
         if (active) qk(blk + 1, nxt);
       }
       if (active) softmax_pv(blk, cur);
