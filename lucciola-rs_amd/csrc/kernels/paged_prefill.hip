@@ -152,41 +152,38 @@ __device__ inline void lds_k_issue(uint32_t a0, uint32_t a1, uint32_t a2, uint32
       : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "n"(HOFF)
       : "memory");
 }
+// Waits for the K reads above while N LDS reads issued after them may stay
+// outstanding (LDS reads complete in order; a scalar load still in flight
+// only makes the wait stricter).
+template <int N>
 __device__ inline void lds_wait_k(u32x4_t* x) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
+  asm volatile("s_waitcnt lgkmcnt(%8)"
                : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),
                  "+v"(x[6]), "+v"(x[7])
-               :
+               : "n"(N)
                : "memory");
 }
 // V^T of a 64-token block (row stride R bytes): x[4c + 2db + j] is the
 // transposing read of token group 16c + 8j through address a_db, i.e. the
 // 8-byte halves of the A operand of PV step c = (32-token half, 16-token
-// step) and 32-dim tile db
-template <int R>
-__device__ inline void lds_v_issue(uint32_t a0, uint32_t a1, u32x2_t* x) {
+// step) and 32-dim tile db.  Issued in two halves: half H issues
+// x[8H .. 8H + 7] (PV steps 2H and 2H + 1), so that at most 8 stay
+// outstanding behind another wait (lgkmcnt counts to 15).
+template <int R, int H>
+__device__ inline void lds_v_issue_half(uint32_t a0, uint32_t a1, u32x2_t* x) {
   asm volatile(
-      "ds_read_b64_tr_b16 %0, %16 offset:%18\n\t"
-      "ds_read_b64_tr_b16 %1, %16 offset:%19\n\t"
-      "ds_read_b64_tr_b16 %2, %17 offset:%18\n\t"
-      "ds_read_b64_tr_b16 %3, %17 offset:%19\n\t"
-      "ds_read_b64_tr_b16 %4, %16 offset:%20\n\t"
-      "ds_read_b64_tr_b16 %5, %16 offset:%21\n\t"
-      "ds_read_b64_tr_b16 %6, %17 offset:%20\n\t"
-      "ds_read_b64_tr_b16 %7, %17 offset:%21\n\t"
-      "ds_read_b64_tr_b16 %8, %16 offset:%22\n\t"
-      "ds_read_b64_tr_b16 %9, %16 offset:%23\n\t"
-      "ds_read_b64_tr_b16 %10, %17 offset:%22\n\t"
-      "ds_read_b64_tr_b16 %11, %17 offset:%23\n\t"
-      "ds_read_b64_tr_b16 %12, %16 offset:%24\n\t"
-      "ds_read_b64_tr_b16 %13, %16 offset:%25\n\t"
-      "ds_read_b64_tr_b16 %14, %17 offset:%24\n\t"
-      "ds_read_b64_tr_b16 %15, %17 offset:%25"
-      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]),
-        "=&v"(x[6]), "=&v"(x[7]), "=&v"(x[8]), "=&v"(x[9]), "=&v"(x[10]), "=&v"(x[11]),
-        "=&v"(x[12]), "=&v"(x[13]), "=&v"(x[14]), "=&v"(x[15])
-      : "v"(a0), "v"(a1), "n"(0), "n"(8 * R), "n"(16 * R), "n"(24 * R), "n"(32 * R),
-        "n"(40 * R), "n"(48 * R), "n"(56 * R)
+      "ds_read_b64_tr_b16 %0, %8 offset:%10\n\t"
+      "ds_read_b64_tr_b16 %1, %8 offset:%11\n\t"
+      "ds_read_b64_tr_b16 %2, %9 offset:%10\n\t"
+      "ds_read_b64_tr_b16 %3, %9 offset:%11\n\t"
+      "ds_read_b64_tr_b16 %4, %8 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %5, %8 offset:%13\n\t"
+      "ds_read_b64_tr_b16 %6, %9 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %7, %9 offset:%13"
+      : "=&v"(x[8 * H]), "=&v"(x[8 * H + 1]), "=&v"(x[8 * H + 2]), "=&v"(x[8 * H + 3]),
+        "=&v"(x[8 * H + 4]), "=&v"(x[8 * H + 5]), "=&v"(x[8 * H + 6]), "=&v"(x[8 * H + 7])
+      : "v"(a0), "v"(a1), "n"(32 * H * R), "n"((32 * H + 8) * R), "n"((32 * H + 16) * R),
+        "n"((32 * H + 24) * R)
       : "memory");
 }
 __device__ inline void lds_wait_v(u32x2_t* x) {
@@ -519,10 +516,11 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   };
   auto step = [&](int blk, f32x16* cur, f32x16* nxt) __attribute__((always_inline)) {
     if constexpr (D == 64) {
-      // the LDS reads of K(blk + 1) go out before the mask and max of block
-      // blk, those of V(blk) before its exponentials, so both land while
-      // the VALU works; the scores of blk + 1 reach the matrix cores before
-      // the exponentials, the PV of blk after them
+      // the LDS reads of K(blk + 1) and of the first half of V(blk) go out
+      // before the mask and max of block blk, the second half of V(blk)
+      // before its exponentials, so they land while the VALU works; the
+      // scores of blk + 1 reach the matrix cores before the exponentials,
+      // the PV of blk after them
       u32x4_t ka[8];
       u32x2_t va[16];
       const bool has_next = blk + 1 < nblk;
@@ -534,9 +532,11 @@ __device__ void prefill_impl(const PrefillArgs& A) {
         }
       }
       if (active) {
+        const uint32_t vbase = lds_addr(s_kv[(blk / SB) % NS][1]) + (blk % SB) * KB;
+        lds_v_issue_half<ROWB, 0>(vbase + vrel[0], vbase + vrel[1], va);
         softmax_max(blk, cur);
         if (has_next) {
-          lds_wait_k(ka);
+          lds_wait_k<8>(ka);  // the first V reads of this block may still be in flight
 #pragma unroll
           for (int hf = 0; hf < 2; ++hf) {
 #pragma unroll
@@ -546,8 +546,7 @@ __device__ void prefill_impl(const PrefillArgs& A) {
               nxt[hf] = mfma32<DT>(__builtin_bit_cast(uint4, ka[4 * hf + k]), qf[k], nxt[hf]);
           }
         }
-        const uint32_t vbase = lds_addr(s_kv[(blk / SB) % NS][1]) + (blk % SB) * KB;
-        lds_v_issue<ROWB>(vbase + vrel[0], vbase + vrel[1], va);
+        lds_v_issue_half<ROWB, 1>(vbase + vrel[0], vbase + vrel[1], va);
         softmax_exp(cur);
         lds_wait_v(va);
 #pragma unroll
