@@ -48,7 +48,15 @@ Also reported:
                 bf16 peak; mfma_busy_frac is the share of SIMD cycles with the
                 matrix cores busy, from the committed rocprofv3 PMC summary;
   sampling      luc_sort_and_sample on one logits row (vocab 151936, top_k
-                1024): time per call.
+                1024): time per call;
+  model         the Qwen2 model loop (random-init Qwen2.5-0.5B, bf16, B=1):
+                a 128-token prompt, then greedy decode steps replayed from one
+                HIP graph (Qwen2Model.capture_decode: 24 layers of RMSNorm,
+                qkv GEMM, luc_decode_step, o_proj, RMSNorm, gate|up GEMM,
+                silu*up, down_proj; final norm, lm_head, argmax), time per
+                token and the bytes each token reads (every weight once plus
+                the K/V of its context) against 8 TB/s; also the eager,
+                host-driven loop's time per token.
 """
 from __future__ import annotations
 
@@ -83,6 +91,8 @@ def parse():
                     help="skip the batch64_long / batch8_32k decode measurements")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the prefill and sampling measurements")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the Qwen2 model loop measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (reference for PMC byte counters)")
     return ap.parse_args()
@@ -226,6 +236,57 @@ def sampling_bench(lib, torch, reps=100):
     return {"call": "luc_sort_and_sample (top-k filter + bitonic sort / top-p draw)",
             "vocab": vocab, "top_k": top_k, "top_p": 0.9,
             "us_per_call": round(statistics.median(runs), 2)}
+
+
+def model_bench(lib, torch, prompt_len=128, steps=128, eager_steps=8):
+    """Milliseconds per greedy token of the Qwen2.5-0.5B model loop (random
+    init, B=1): prompt, eager steps (which also set up the GEMM handles), then
+    a graph of one decode step replayed `steps` times, timed with HIP events."""
+    import numpy as np
+    from lucciola_rs_amd.model import QWEN25_05B, Qwen2Model, random_weights
+
+    cfg = QWEN25_05B
+    max_ctx = 512
+    m = Qwen2Model(cfg, random_weights(cfg, seed=2025), max_positions=max_ctx, lib=lib)
+    rng = np.random.default_rng(7)
+    prompt = rng.integers(0, cfg.vocab_size, prompt_len).tolist()
+    m.forward(prompt, 0)
+    tok, pos = m.sample_greedy(), prompt_len
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(eager_steps):
+        m.forward([tok], pos)
+        tok, pos = m.sample_greedy(), pos + 1
+    eager_ms = (time.perf_counter() - t0) * 1e3 / eager_steps
+    graph = m.capture_decode(max_ctx)
+    m.pos.fill_(pos)  # m.idx holds the last token
+    for _ in range(4):
+        graph.replay()
+    torch.cuda.synchronize()
+    ctx0 = pos + 4
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    weights = sum(t.numel() * t.element_size() for t in
+                  [m.lm_head_t, m.final_norm] +
+                  [x for L in m.layers for x in L.values()])
+    mean_ctx = ctx0 + (steps + 1) / 2
+    kv = int(mean_ctx) * cfg.num_hidden_layers * 2 * cfg.num_key_value_heads * cfg.head_dim * 2
+    per_token = weights + kv
+    del graph, m
+    torch.cuda.empty_cache()
+    return {"workload": "qwen2.5-0.5b greedy decode (random init, bf16, B=1, 24 layers)",
+            "prompt": prompt_len, "steps": steps, "mean_ctx": round(mean_ctx, 1),
+            "launch": "hip graph of one decode step (Qwen2Model.capture_decode)",
+            "ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
+            "bytes_per_token": int(per_token), "achieved_gbs": round(per_token / (ms * 1e-3) / 1e9, 1),
+            "frac": round(per_token / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "eager_ms_per_token": round(eager_ms, 3)}
 
 
 def graph_us(torch, fn, n, reps=3):
@@ -419,6 +480,7 @@ def main():
 
     prefill = None if args.no_prefill else prefill_bench(lib, torch)
     sampling = None if args.no_prefill else sampling_bench(lib, torch)
+    model = None if args.no_model else model_bench(lib, torch)
     long_ctx = None
     if not args.no_long_context:
         long_ctx = [long_context_bench(lib, torch, n, args.seed) for n in ("batch64_long", "batch8_32k")]
@@ -486,6 +548,7 @@ def main():
         "long_context": long_ctx,
         "prefill": prefill,
         "sampling": sampling,
+        "model": model,
     }
     print(json.dumps(res), flush=True)
 

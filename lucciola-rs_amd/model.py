@@ -174,6 +174,9 @@ class Qwen2Model:
         return att
 
     def _layer(self, li, h, attention):
+        """One decoder layer on the hidden rows h, which it updates in place
+        (the residual adds are GEMMs with beta = 1 into h: one rounding, and no
+        copy of h into a new output)."""
         cfg = self.cfg
         L = self.layers[li]
         I = cfg.intermediate_size
@@ -181,11 +184,11 @@ class Qwen2Model:
         self.lib.rmsnorm(norm, h, L["in_norm"], cfg.rms_norm_eps)
         qkv = torch.mm(norm, L["qkv_t"])
         att = attention(li, qkv)
-        h = torch.addmm(h, att, L["o_t"])
+        h.addmm_(att, L["o_t"])
         self.lib.rmsnorm(norm, h, L["post_norm"], cfg.rms_norm_eps)
         gate_up = torch.mm(norm, L["gate_up_t"])
         self.lib.silu_mul(gate_up, I)
-        return torch.addmm(h, gate_up[:, :I], L["down_t"])
+        return h.addmm_(gate_up[:, :I], L["down_t"])
 
     # ---- forward (models.rs:693-830) ----
     def forward(self, input_ids, cache_pos: int) -> None:
@@ -228,6 +231,46 @@ class Qwen2Model:
             from .sampler import DeviceSampler
             self._sampler = DeviceSampler(self.lib, self.device)
         return self._sampler.sample(self.logits(), sampler)
+
+    def capture_decode(self, max_ctx: int) -> "torch.cuda.CUDAGraph":
+        """One greedy decode step as a HIP graph, for serving loops with no
+        host work per token: the token in self.idx (the previous step's argmax)
+        at position self.pos goes through every layer, the final norm, lm_head
+        and argmax back into self.idx, and self.pos advances by one.  Each
+        replay is one `forward([tok], pos)` + `sample_greedy()` of the eager
+        loop, computing the same values.  Positions must stay below max_ctx:
+        its pages are taken now, the split-K workspace is sized for it, and the
+        attention launches are bounded by it (the kernels read the actual
+        position from self.pos).  Set self.idx and self.pos before the first
+        replay."""
+        cfg = self.cfg
+        if max_ctx > self.max_positions:
+            raise ValueError(f"max_ctx {max_ctx} exceeds {self.max_positions} positions")
+        for p in range(max_ctx):
+            self.kv.prepare_for_step(p)
+        ws = self.kv.workspace(cfg.num_attention_heads, max_ctx)
+
+        def attention(li, qkv):
+            L = self.layers[li]
+            att = torch.empty(1, cfg.hidden_size, dtype=torch.bfloat16, device=self.device)
+            self.lib.decode_step(qkv, L["q_bias"], L["k_bias"], L["v_bias"], self.rope.cos,
+                                 self.rope.sin, self.kv.k_pool, self.kv.v_pool,
+                                 self.kv.block_table.view(1, -1), self.pos, 1, max_ctx, li,
+                                 cfg.num_hidden_layers, cfg.num_attention_heads,
+                                 cfg.num_key_value_heads, cfg.head_dim, sm_scale(cfg.head_dim), att, ws)
+            return att
+
+        torch.cuda.synchronize(self.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            h = torch.empty(1, cfg.hidden_size, dtype=torch.bfloat16, device=self.device)
+            self.lib.embedding(h, self.embed, self.idx)
+            for li in range(cfg.num_hidden_layers):
+                h = self._layer(li, h, attention)
+            self.lib.rmsnorm(self.hidden, h, self.final_norm, cfg.rms_norm_eps)
+            self.lib.argmax(torch.mm(self.hidden, self.lm_head_t), self.idx)
+            self.pos.add_(1)
+        return graph
 
     def generate(self, prompt_ids, max_new_tokens: int, stop_at_eos: bool = True) -> list[int]:
         """Greedy generation (models.rs:184-243): prefill, then one token per step."""

@@ -328,3 +328,31 @@ def test_sample_token_dispatch(orc, qwen):
             decided += 1
             assert tok == want["token"]
     assert decided >= 6
+
+
+def test_decode_graph_replays_the_eager_loop(qwen):
+    """Qwen2Model.capture_decode: the greedy loop replayed from one HIP graph
+    (token and position on the device, no host work per token) gives the eager
+    loop's tokens step by step: a 32-token prompt, then 48 greedy steps.  The
+    host reads each replay's token before the next replay."""
+    cfg, gpu, _ = qwen
+    rng = np.random.default_rng(41)
+    prompt = rng.integers(0, cfg.vocab_size, 32).tolist()
+    gpu.forward(prompt, 0)
+    eager = [gpu.sample_greedy()]
+    pos = len(prompt)
+    for _ in range(48):
+        gpu.forward([eager[-1]], pos)
+        eager.append(gpu.sample_greedy())
+        pos += 1
+    gpu.forward(prompt, 0)  # the prompt's cache rows again; the graph rewrites the rest
+    assert gpu.sample_greedy() == eager[0]
+    say("  [gpu] decode graph: capture, then 48 replays against the eager loop")
+    graph = gpu.capture_decode(max_ctx=256)
+    gpu.pos.fill_(len(prompt))  # gpu.idx holds the first token
+    for s in range(48):
+        graph.replay()
+        tok = int(gpu.idx.cpu().item())
+        assert tok == eager[s + 1], f"replay {s}: token {tok}, eager loop {eager[s + 1]}"
+    assert int(gpu.pos.cpu().item()) == len(prompt) + 48
+    say(f"  48 replays equal the eager loop's tokens (first {eager[1:6]})")
