@@ -24,7 +24,12 @@ namespace luc {
 constexpr int kNormThreads = 256;
 
 // RMSNorm of `rows` rows of n elements (n a multiple of 8, 16-byte aligned
-// rows): out may alias in.
+// rows): out may alias in.  Rows of up to kNormChunks * 8 * kNormThreads
+// elements stay in registers between the sum and the output (x and the
+// weight are loaded together); the halving tree's first two levels read the
+// partials from LDS in one wave, which adds the rest across its lanes (each
+// level the same additions a[i] + a[i + s] as the tree).
+constexpr int kNormChunks = 4;
 __device__ void rmsnorm_impl(uint16_t* out, const uint16_t* in, const uint16_t* weight, float eps,
                              int n) {
 #pragma clang fp contract(off)
@@ -32,34 +37,67 @@ __device__ void rmsnorm_impl(uint16_t* out, const uint16_t* in, const uint16_t* 
   const int t = threadIdx.x;
   const int64_t row = blockIdx.x;
   const uint4* x = (const uint4*)(in + row * n);
+  const uint4* w = (const uint4*)weight;
+  uint4* y = (uint4*)(out + row * n);
   const int chunks = n / 8;
+  const bool in_regs = chunks <= kNormChunks * kNormThreads;
+  uint4 xv[kNormChunks], wv[kNormChunks];
   float s = 0.0f;
-  for (int c = t; c < chunks; c += kNormThreads) {
-    const uint4 v = x[c];
+  if (in_regs) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float f = St<kBF16>::load(chunk_elem(v, e));
-      s = fmaf(f, f, s);
+    for (int k = 0; k < kNormChunks; ++k) {
+      const int c = t + k * kNormThreads;
+      if (c < chunks) {
+        xv[k] = x[c];
+        wv[k] = w[c];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kNormChunks; ++k)
+      if (t + k * kNormThreads < chunks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float f = St<kBF16>::load(chunk_elem(xv[k], e));
+          s = fmaf(f, f, s);
+        }
+  } else {
+    for (int c = t; c < chunks; c += kNormThreads) {
+      const uint4 v = x[c];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = St<kBF16>::load(chunk_elem(v, e));
+        s = fmaf(f, f, s);
+      }
     }
   }
   part[t] = s;
   __syncthreads();
-  for (int h = kNormThreads / 2; h > 0; h >>= 1) {
-    if (t < h) part[t] = part[t] + part[t + h];
-    __syncthreads();
+  static_assert(kNormThreads == 256, "levels 128 and 64 below, then the 64 lanes of one wave");
+  if (t < 64) {
+    float a = (part[t] + part[t + 128]) + (part[t + 64] + part[t + 192]);
+#pragma unroll
+    for (int h = 32; h > 0; h >>= 1) a = a + __shfl_down(a, h);
+    if (t == 0) part[0] = a;
   }
+  __syncthreads();
   const float inv = 1.0f / sqrtf(part[0] / (float)n + eps);
-  const uint4* w = (const uint4*)weight;
-  uint4* y = (uint4*)(out + row * n);
-  for (int c = t; c < chunks; c += kNormThreads) {
-    const uint4 v = x[c], wv = w[c];
+  auto norm_chunk = [&](uint4 v, uint4 wc) {
     uint16_t o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float f = St<kBF16>::load(chunk_elem(v, e)) * inv;
-      o[e] = St<kBF16>::store(f * St<kBF16>::load(chunk_elem(wv, e)));
+      o[e] = St<kBF16>::store(f * St<kBF16>::load(chunk_elem(wc, e)));
     }
-    y[c] = chunk_pack(o);
+    return chunk_pack(o);
+  };
+  if (in_regs) {
+#pragma unroll
+    for (int k = 0; k < kNormChunks; ++k) {
+      const int c = t + k * kNormThreads;
+      if (c < chunks) y[c] = norm_chunk(xv[k], wv[k]);
+    }
+  } else {
+    for (int c = t; c < chunks; c += kNormThreads) y[c] = norm_chunk(x[c], w[c]);
   }
 }
 

@@ -29,7 +29,7 @@ def bf16_ulps(a, b):
 
 def test_rmsnorm_bit_exact(orc, luc):
     rng = np.random.default_rng(1)
-    for rows, cols in [(1, 896), (7, 896), (3, 4864), (2, 64), (5, 2056)]:
+    for rows, cols in [(1, 896), (7, 896), (3, 4864), (2, 64), (5, 2056), (1, 8192), (2, 8200)]:
         x = to_bf16_bits(rng.standard_normal((rows, cols)) * rng.uniform(0.1, 30))
         w = to_bf16_bits(1 + 0.1 * rng.standard_normal(cols))
         want = orc.rmsnorm(x, w, 1e-6)
