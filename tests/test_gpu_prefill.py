@@ -98,6 +98,20 @@ def test_prefill_with_biases_and_layer(orc, luc, dtype):
                                oracle_prefill(orc, luc, h, layer=layer, bias=bias), dtype)
 
 
+@pytest.mark.parametrize("batch", [16, 17, 24])
+def test_prefill_many_prompts(orc, luc, batch):
+    """Many short ragged prompts, empty ones among them (the first, one in the
+    middle and the last): the append kernel's workgroups straddle several
+    sequences and its cu_seqlens search skips empty ones."""
+    rng = np.random.default_rng(batch)
+    rows = rng.integers(1, 40, batch)
+    rows[[0, batch // 2, batch - 1]] = 0
+    starts = rng.integers(0, 50, batch)
+    cfg = wl.PrefillConfig(f"many{batch}", batch, 0, 14, 2, 64, "bf16", 0, 0, 0.5)
+    h = wl.host_prefill_inputs(cfg, seed=batch, rows=rows, starts=starts)
+    assert_prefill_matches(orc, gpu_prefill(luc, h), oracle_prefill(orc, luc, h), "bf16")
+
+
 def test_prefill_4x2048_full(orc, luc):
     """The full prefill shape: 4 prompts x 2048 rows from an empty cache,
     14q/2kv, d=64, bf16, 128 pages per sequence."""
