@@ -48,9 +48,12 @@
 //     3. Online softmax in the exp2 domain with a lazy reference point: the
 //        running max moves (wave max by a DPP reduction, rescale of o) only
 //        when a score passes it by more than kLazyMax.
-//     4. o += p * V with V in its load layout.  fp16: p of tokens t and
-//        t + TILE/2 packed as an fp16 pair, V of the same two tokens paired by
-//        v_perm, one v_dot2_f32_f16 per (head, dim).  bf16: f32 FMA.
+//     4. o += p * V with V in its load layout: p of tokens t and t + TILE/2
+//        packed as a pair of the storage type, V of the same two tokens
+//        paired by v_perm, one v_dot2_f32_{f16,bf16} per (head, dim).  p is
+//        rounded where it is computed, so l sums the same values the
+//        products use, and the running max is kept on whole numbers, so
+//        that a token's p rounds alike in every split.
 //   Each wave's token groups are reduced with permlane swaps
 //   (reduce-scatter); the W waves merge their (m, l, o) through LDS.  A
 //   sequence with one split writes its output; otherwise each split writes
@@ -291,6 +294,14 @@ __device__ inline float upper_half_value(float x) {
 __device__ inline uint32_t pack_f16(float lo, float hi) {
   const half2_t v = {(_Float16)lo, (_Float16)hi};
   return __builtin_bit_cast(uint32_t, v);
+}
+
+// p of two tokens, already rounded to the storage type, as a pair of it
+// (bf16: the high halves of the f32 bits).
+template <int DT>
+__device__ inline uint32_t pack_p(float lo, float hi) {
+  if constexpr (DT == kF16) return pack_f16(lo, hi);
+  else return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
 // x[i] for a wave-uniform runtime i < N, without indexing a register array.
@@ -563,8 +574,7 @@ __device__ __attribute__((always_inline)) inline void finish_split(
 template <int DT, int D, int G, bool APPEND, int W, int NB>
 __device__ void decode_impl(const DecodeArgs& A) {
   using S = DecodeGeo<D>;
-  constexpr bool PV_DOT2 = (DT == kF16);
-  constexpr int PWORDS = (PV_DOT2 ? S::HALF : S::TILE) * 8;  // p exchange, 32-bit words
+  constexpr int PWORDS = S::HALF * 8;  // p exchange, 32-bit words: G pairs per token pair
   constexpr int HD = D / 2;
   constexpr int GD = G * D;
   constexpr int NV = 8 * G;  // o values per lane: 8 dims x G heads
@@ -937,12 +947,15 @@ __device__ void decode_impl(const DecodeArgs& A) {
       // it starts at the score of lane 0 (the tile's first token, always
       // valid in a wave's first tile) and moves (wave-wide max, rescale of o
       // and l) only when a score exceeds it by more than kLazyMax, which one
-      // ballot detects; p stays <= 2^kLazyMax.
+      // ballot detects; p stays <= 2^kLazyMax.  It is kept on whole numbers:
+      // the p of one token in two splits then differ by a power of two, so
+      // they round alike to the storage type, and the merge weights
+      // 2^(m_s - M) are exact.
       if (m_run[g] == -INFINITY)  // wave-uniform: the wave's first tile
-        m_run[g] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, s)));
+        m_run[g] = floorf(__builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, s))));
       if (__builtin_amdgcn_ballot_w64(s > m_run[g] + kLazyMax) != 0) {  // wave-uniform
-        const float mn = __builtin_bit_cast(
-            float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fmaxf(m_run[g], wave_max(s)))));
+        const float mn = floorf(__builtin_bit_cast(
+            float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fmaxf(m_run[g], wave_max(s))))));
         if (m_run[g] > -INFINITY) {  // (nothing accumulated before the first tile)
           const float alpha = __builtin_amdgcn_exp2f(m_run[g] - mn);
           l_lane[g] *= alpha;
@@ -952,27 +965,22 @@ __device__ void decode_impl(const DecodeArgs& A) {
         m_run[g] = mn;
       }
       p[g] = __builtin_amdgcn_exp2f(s - m_run[g]);
+      // p rounds to the storage type for the PV dot products, and l sums
+      // the rounded values, so the output weights stay normalised (a single
+      // dominant token gives its V exactly)
+      if constexpr (DT == kBF16) p[g] = (float)(__bf16)p[g];
+      else p[g] = (float)(_Float16)p[g];
       l_lane[g] += qh == 0 ? p[g] : 0.0f;
     }
 
     // p to the load layout through LDS
     uint32_t* const sp = s_p[w];
-    if constexpr (PV_DOT2) {
-      uint32_t pk[8];
+    uint32_t pk[8];
 #pragma unroll
-      for (int g = 0; g < 8; ++g) pk[g] = g < G ? pack_f16(p[g], upper_half_value<D>(p[g])) : 0u;
-      if (lane < S::HALF) {
-        *(uint4*)(sp + tq * 8) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        *(uint4*)(sp + tq * 8 + 4) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
-      }
-    } else {
-      float pf[8];
-#pragma unroll
-      for (int g = 0; g < 8; ++g) pf[g] = g < G ? p[g] : 0.0f;
-      if (qh == 0) {
-        *(float4*)(sp + tq * 8) = make_float4(pf[0], pf[1], pf[2], pf[3]);
-        *(float4*)(sp + tq * 8 + 4) = make_float4(pf[4], pf[5], pf[6], pf[7]);
-      }
+    for (int g = 0; g < 8; ++g) pk[g] = g < G ? pack_p<DT>(p[g], upper_half_value<D>(p[g])) : 0u;
+    if (lane < S::HALF) {
+      *(uint4*)(sp + tq * 8) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      *(uint4*)(sp + tq * 8 + 4) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
     }
     wave_lds_sync();
   };
@@ -991,52 +999,29 @@ __device__ void decode_impl(const DecodeArgs& A) {
     // and 0 * stale data must not produce NaN)
     const bool partial = t0 + S::TILE > s_end;
     const uint32_t* const sp = s_p[w];
-    if constexpr (PV_DOT2) {
 #pragma unroll
-      for (int r = 0; r < S::LOADS / 2; ++r) {
-        const int t = r * S::TPL + pv_tok;  // vr[r]: token t; vr[r + LOADS/2]: t + HALF
-        uint4 va = vr[r], vb = vr[r + S::LOADS / 2];
-        if (partial) {
-          if (t0 + t >= s_end) va = make_uint4(0, 0, 0, 0);
-          if (t0 + t + S::HALF >= s_end) vb = make_uint4(0, 0, 0, 0);
-        }
-        const uint4 p0 = *(const uint4*)(sp + t * 8);
-        const uint4 p1 = *(const uint4*)(sp + t * 8 + 4);
-        const uint32_t pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-        const uint32_t aw[4] = {va.x, va.y, va.z, va.w};
-        const uint32_t bw[4] = {vb.x, vb.y, vb.z, vb.w};
-        uint32_t pr[8];  // (v_t[e], v_{t+HALF}[e]) pairs
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pr[2 * e] = __builtin_amdgcn_perm(bw[e], aw[e], 0x05040100u);
-          pr[2 * e + 1] = __builtin_amdgcn_perm(bw[e], aw[e], 0x07060302u);
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[g][e] = St<kF16>::dot2(pr[e], pp[g], o[g][e]);
+    for (int r = 0; r < S::LOADS / 2; ++r) {
+      const int t = r * S::TPL + pv_tok;  // vr[r]: token t; vr[r + LOADS/2]: t + HALF
+      uint4 va = vr[r], vb = vr[r + S::LOADS / 2];
+      if (partial) {
+        if (t0 + t >= s_end) va = make_uint4(0, 0, 0, 0);
+        if (t0 + t + S::HALF >= s_end) vb = make_uint4(0, 0, 0, 0);
       }
-    } else {
+      const uint4 p0 = *(const uint4*)(sp + t * 8);
+      const uint4 p1 = *(const uint4*)(sp + t * 8 + 4);
+      const uint32_t pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+      const uint32_t aw[4] = {va.x, va.y, va.z, va.w};
+      const uint32_t bw[4] = {vb.x, vb.y, vb.z, vb.w};
+      uint32_t pr[8];  // (v_t[e], v_{t+HALF}[e]) pairs
 #pragma unroll
-      for (int r = 0; r < S::LOADS; ++r) {
-        const int t = r * S::TPL + pv_tok;
-        uint4 v = vr[r];
-        if (partial && t0 + t >= s_end) v = make_uint4(0, 0, 0, 0);
-        const float4 pa = *(const float4*)(sp + t * 8);
-        const float4 pb = *(const float4*)(sp + t * 8 + 4);
-        const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-        const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-        float vv[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          vv[2 * e] = St<DT>::lo(vw[e]);
-          vv[2 * e + 1] = St<DT>::hi(vw[e]);
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pv[g], vv[e], o[g][e]);
+      for (int e = 0; e < 4; ++e) {
+        pr[2 * e] = __builtin_amdgcn_perm(bw[e], aw[e], 0x05040100u);
+        pr[2 * e + 1] = __builtin_amdgcn_perm(bw[e], aw[e], 0x07060302u);
       }
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] = St<DT>::dot2(pr[e], pp[g], o[g][e]);
     }
     wave_lds_sync();
   };
