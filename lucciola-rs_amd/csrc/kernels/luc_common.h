@@ -57,6 +57,23 @@ template <> struct St<kF16> {
 };
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// v_mfma_f32_32x32x16_{f16,bf16}: c += a * b, eight 16-bit values per lane
+// in a and b.  Operand layouts: A lane l = row l % 32, k (l / 32) * 8 .. + 8;
+// B lane l = column l % 32, the same k; C lane l = column l % 32, c[4i + j] =
+// row 8i + 4(l / 32) + j.
+template <int DT>
+__device__ inline f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
+  if constexpr (DT == kF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
 
 // 16-byte global load with the non-temporal (streaming) hint.
 __device__ inline uint4 ld_nt16(const uint16_t* p) {

@@ -44,7 +44,11 @@
 //        All K loads of a tile precede its V loads, so the scores start as
 //        soon as K has landed.
 //     2. Scores: lane = token (x2 lanes per token at head_dim 128), all G
-//        heads with v_dot2c_f32_{f16,bf16}, q by DPP broadcast.
+//        heads.  Single-tile kernels: v_dot2c_f32_{f16,bf16}, q by DPP
+//        broadcast.  Tile-pair kernels: v_mfma_f32_32x32x16 with the heads as
+//        rows and the tokens as columns (q the A operand, K read from LDS as
+//        the B operand), then one permlane32 swap per four heads puts every
+//        head of a token in that token's lane.
 //     3. Online softmax in the exp2 domain with a lazy reference point: the
 //        running max moves (wave max by a DPP reduction, rescale of o) only
 //        when a score passes it by more than kLazyMax.
@@ -590,6 +594,12 @@ __device__ void decode_impl(const DecodeArgs& A) {
   constexpr bool T1 = NB == 1;
   constexpr bool FASTQ = T1 && !APPEND;
   constexpr bool FASTA = T1 && APPEND;
+  // The tile-pair kernels take the scores on the matrix cores (MQK): q as the
+  // A operand of v_mfma_f32_32x32x16, KS k-steps of 16 dims, NBLK blocks of
+  // 32 tokens per tile.
+  constexpr bool MQK = !T1;
+  constexpr int KS = D / 16;
+  constexpr int NBLK = S::TILE / 32;
   constexpr int NQ = (GD * 2 + 255) / 256;  // 4-byte direct-to-LDS loads for q
   // FASTA operand block: q of the G heads, then their biases (256-byte
   // padded), then six regions of 2*D bytes: k, k bias, cos, sin, v, v bias.
@@ -647,6 +657,14 @@ __device__ void decode_impl(const DecodeArgs& A) {
   // qhalf = lane / 32 at head_dim 128 (the lane's 64 dims), else 0.
   const int qhalf = D == 128 ? lane / 32 : 0;
   auto q_word = [&](int m) { return (m / 2) * HD + qhalf * 32 + (m % 2) * 16 + (lane & 15); };
+  // MQK: the A operand of k-step ks, q[head lane % 32][16 ks + 8 (lane / 32)
+  // .. + 8] of a row of the G heads' q (4-byte aligned); zero past head G - 1.
+  auto q_operand = [&](const uint16_t* row, int ks) {
+    const int g = lane & 31;
+    const uint32_t* p = (const uint32_t*)(row + min(g, G - 1) * D + 16 * ks + 8 * (lane >> 5));
+    const uint4 v = make_uint4(p[0], p[1], p[2], p[3]);
+    return g < G ? v : make_uint4(0, 0, 0, 0);
+  };
   // single-tile kernel: the page numbers of the wave's tile, through the
   // scalar cache in the same round trip as the position (clamped to the
   // split once the position is known)
@@ -661,8 +679,14 @@ __device__ void decode_impl(const DecodeArgs& A) {
 #pragma unroll
     for (int i = 0; i < S::PAGES; ++i) traw[i] = v[i];
   }
-  uint32_t qd[2 * G];
-  if constexpr (!APPEND && !FASTQ) {
+  uint32_t qd[MQK ? 1 : 2 * G];
+  uint4 qm[MQK ? KS : 1];
+  if constexpr (MQK) {
+    if constexpr (!APPEND) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qm[ks] = q_operand(qrow, ks);
+    }
+  } else if constexpr (!APPEND && !FASTQ) {
 #pragma unroll
     for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)qrow)[q_word(m)];
   }
@@ -853,7 +877,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   if constexpr (T1) {
   } else if constexpr (!APPEND) {
 #pragma unroll
-    for (int m = 0; m < 2 * G; ++m) asm volatile("" ::"v"(qd[m]));
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(qm[ks].x), "v"(qm[ks].y), "v"(qm[ks].z), "v"(qm[ks].w));
   } else {
 #pragma unroll
     for (int i = 0; i < NPAIR; ++i)
@@ -894,7 +918,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       s_vnew[qi][lane + 64 * i] = St<DT>::store(St<DT>::load(rv[i]) + St<DT>::load(rvb[i]));
     wave_lds_sync();
 #pragma unroll
-    for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)s_q[qi])[q_word(m)];
+    for (int ks = 0; ks < KS; ++ks) qm[ks] = q_operand(s_q[qi], ks);
   }
 
   float m_run[G], l_lane[G], o[G][8];
@@ -918,23 +942,55 @@ __device__ void decode_impl(const DecodeArgs& A) {
       wave_lds_sync();
     }
     float acc[G];
+    if constexpr (MQK) {
+      // S = Q K^T on the matrix cores, per 32-token block: rows = the
+      // group's heads, columns = tokens, B lane = (token lane % 32, 8 dims
+      // of chunk 2 ks + lane / 32).  Lane l then holds heads 4(l/32) + j of
+      // token l % 32 in sc[.][j]; one permlane32 swap per j gives every lane
+      // heads j and 4 + j of its own token (lane = token at head_dim 64,
+      // token lane % 32 in both lane halves at 128).
+      f32x16 sc[NBLK];
 #pragma unroll
-    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
-    const uint32_t krow = lds_addr(kb) + tq * S::ROWB;
-    const int sw = tq & 7;
-    auto ka = [&](int c) { return krow + ((uint32_t)((qh * 8 + c) ^ sw) << 4); };
+      for (int nb = 0; nb < NBLK; ++nb) {
+        sc[nb] = f32x16{};
+        const int tok = nb * 32 + (lane & 31);
+        const uint32_t kr = lds_addr(kb) + tok * S::ROWB;
+        const int sw = tok & 7;
+        auto kaddr = [&](int ks) { return kr + ((uint32_t)((2 * ks + (lane >> 5)) ^ sw) << 4); };
 #pragma unroll
-    for (int hc = 0; hc < 2; ++hc) {  // chunks 4*hc .. 4*hc+3 of the lane's 64 dims
-      uint4 kc[4];
-      lds_read4(ka(4 * hc), ka(4 * hc + 1), ka(4 * hc + 2), ka(4 * hc + 3), kc);
-      dot_all_heads<DT, G>(acc, qd, hc, kc);
-    }
-    if constexpr (S::QKL == 2) {
+        for (int k4 = 0; k4 < KS; k4 += 4) {
+          uint4 kc[4];
+          lds_read4(kaddr(k4), kaddr(k4 + 1), kaddr(k4 + 2), kaddr(k4 + 3), kc);
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const uint32_t u = __float_as_uint(acc[g]);
-        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-        acc[g] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+          for (int i = 0; i < 4; ++i) sc[nb] = mfma32<DT>(qm[k4 + i], kc[i], sc[nb]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(sc[0][j]),
+                                                        __float_as_uint(sc[NBLK - 1][j]), false, false);
+        if (j < G) acc[j] = __uint_as_float(r[0]);
+        if (4 + j < G) acc[4 + j] = __uint_as_float(r[1]);
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+      const uint32_t krow = lds_addr(kb) + tq * S::ROWB;
+      const int sw = tq & 7;
+      auto ka = [&](int c) { return krow + ((uint32_t)((qh * 8 + c) ^ sw) << 4); };
+#pragma unroll
+      for (int hc = 0; hc < 2; ++hc) {  // chunks 4*hc .. 4*hc+3 of the lane's 64 dims
+        uint4 kc[4];
+        lds_read4(ka(4 * hc), ka(4 * hc + 1), ka(4 * hc + 2), ka(4 * hc + 3), kc);
+        dot_all_heads<DT, G>(acc, qd, hc, kc);
+      }
+      if constexpr (S::QKL == 2) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const uint32_t u = __float_as_uint(acc[g]);
+          const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+          acc[g] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
       }
     }
 

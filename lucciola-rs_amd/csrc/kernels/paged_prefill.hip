@@ -56,9 +56,6 @@ struct IC {  // a compile-time index passed to a generic lambda
 __device__ inline uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const lds_char_p*)p;
 }
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 struct PrefillArgs {
   const uint16_t* qkv;  // row r at qkv + r*qkv_stride: [q (Hq*D) | k | v], q roped
@@ -75,16 +72,6 @@ struct PrefillArgs {
   int32_t num_blocks;  // pages per pool: table entries outside [0, num_blocks) are never used
   float qk_scale_log2;  // sm_scale * log2(e)
 };
-
-template <int DT>
-__device__ inline f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
-  if constexpr (DT == kF16)
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
 
 // Two values rounded (nearest even) to 16-bit storage, packed: one
 // v_cvt_pk_{f16,bf16}_f32 (these values are compared within tolerance; the
