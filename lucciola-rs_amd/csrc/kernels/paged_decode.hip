@@ -594,10 +594,10 @@ __device__ void decode_impl(const DecodeArgs& A) {
   constexpr bool T1 = NB == 1;
   constexpr bool FASTQ = T1 && !APPEND;
   constexpr bool FASTA = T1 && APPEND;
-  // The tile-pair kernels take the scores on the matrix cores (MQK): q as the
-  // A operand of v_mfma_f32_32x32x16, KS k-steps of 16 dims, NBLK blocks of
-  // 32 tokens per tile.
-  constexpr bool MQK = !T1;
+  // Scores on the matrix cores (MQK): q as the A operand of
+  // v_mfma_f32_32x32x16, KS k-steps of 16 dims, NBLK blocks of 32 tokens per
+  // tile.
+  constexpr bool MQK = true;
   constexpr int KS = D / 16;
   constexpr int NBLK = S::TILE / 32;
   constexpr int NQ = (GD * 2 + 255) / 256;  // 4-byte direct-to-LDS loads for q
@@ -681,12 +681,10 @@ __device__ void decode_impl(const DecodeArgs& A) {
   }
   uint32_t qd[MQK ? 1 : 2 * G];
   uint4 qm[MQK ? KS : 1];
-  if constexpr (MQK) {
-    if constexpr (!APPEND) {
+  if constexpr (MQK && !APPEND && !FASTQ) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qm[ks] = q_operand(qrow, ks);
-    }
-  } else if constexpr (!APPEND && !FASTQ) {
+    for (int ks = 0; ks < KS; ++ks) qm[ks] = q_operand(qrow, ks);
+  } else if constexpr (!MQK && !APPEND && !FASTQ) {
 #pragma unroll
     for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)qrow)[q_word(m)];
   }
@@ -1144,19 +1142,39 @@ __device__ void decode_impl(const DecodeArgs& A) {
     }
     if (ntw > 0) {
       LUC_WAIT_VM(8);  // K and q
-      if constexpr (FASTQ) {  // q words from LDS: qd[m] = word q_word(m)
-        const uint32_t qa = lds_addr(s_qr[w]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
-        read_q_words<0, 2 * G, HD>(qa, qd);
+      // MQK: the A operands from a q row in LDS (asm reads: compiler-visible
+      // reads of LDS would wait for every outstanding load)
+      auto q_operands_lds = [&](const void* row) __attribute__((always_inline)) {
+        const uint32_t qa = lds_addr(row) + (uint32_t)((min(lane & 31, G - 1) * D + 8 * (lane >> 5)) * 2);
 #pragma unroll
-        for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
+        for (int k4 = 0; k4 < KS; k4 += 4) {
+          uint4 x[4];
+          lds_read4(qa + k4 * 32, qa + (k4 + 1) * 32, qa + (k4 + 2) * 32, qa + (k4 + 3) * 32, x);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) qm[k4 + i] = (lane & 31) < G ? x[i] : make_uint4(0, 0, 0, 0);
+        }
+      };
+      if constexpr (FASTQ) {  // q words from LDS: qd[m] = word q_word(m)
+        if constexpr (MQK) {
+          q_operands_lds(s_qr[w]);
+        } else {
+          const uint32_t qa = lds_addr(s_qr[w]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
+          read_q_words<0, 2 * G, HD>(qa, qd);
+#pragma unroll
+          for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
+        }
       }
       if constexpr (FASTA) {
         // q words of the shared roped copy (asm reads: compiler-visible reads
         // of LDS would wait for every outstanding load)
-        const uint32_t qa = lds_addr(s_q[0]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
-        read_q_words<0, 2 * G, HD>(qa, qd);
+        if constexpr (MQK) {
+          q_operands_lds(s_q[0]);
+        } else {
+          const uint32_t qa = lds_addr(s_q[0]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
+          read_q_words<0, 2 * G, HD>(qa, qd);
 #pragma unroll
-        for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
+          for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
+        }
       }
       tile_scores(t_first, 0);
       LUC_WAIT_VM(0);  // V
@@ -1218,7 +1236,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
 }  // namespace luc
 
 // Decode kernels: _t1 has 8 waves per workgroup, one tile each (splits of 8
-// tiles; 80 KB of LDS, two workgroups per CU), _t2 has 4 waves with two
+// tiles; 80 KB of LDS, two workgroups per CU, so four waves per SIMD, which
+// the register target keeps up to group size 7), _t2 has 4 waves with two
 // tiles in flight each (longer splits).  Resident-wave targets are per SIMD.
 #define LUC_DECODE_KERNELS(DTN, DT, D, G, NB, OCC, W)                                               \
   extern "C" __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC)))         \
@@ -1231,7 +1250,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   }
 
 #define LUC_DECODE(DTN, DT, D, G)                                                                  \
-  LUC_DECODE_KERNELS(DTN, DT, D, G, 1, 2, 8)                                                       \
+  LUC_DECODE_KERNELS(DTN, DT, D, G, 1, (G <= 7 ? 4 : 2), 8)                                        \
   LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2, 4)
 
 #define LUC_DECODE_GROUPS(DTN, DT, D)                                                              \
