@@ -34,8 +34,9 @@
 //   the tile's K and V loads, and the step variant's operands (q, k, v, their
 //   biases and the cos/sin rows: one block per workgroup, loaded by wave 0)
 //   by direct-to-LDS loads issued just before wave 0's K tile, so no
-//   vector-memory round trip precedes the KV stream.  q is then held in 2G registers, spread so that DPP row_newbcast
-//   hands every lane the q word it needs as an operand of v_dot2c.
+//   vector-memory round trip precedes the KV stream.  q is then held as the
+//   A operands of the score MFMAs (D/4 registers: lane l holds 8 dims of
+//   head l % 32 per 16-dim step, zero past the group).
 //   Per tile:
 //     1. K goes straight from HBM into LDS (global_load_lds_dwordx4; one
 //        wave-wide load = 1 KB of a page), each token row XOR-swizzled by
@@ -43,12 +44,11 @@
 //        to registers in the same load layout (lane = token x 16-byte chunk).
 //        All K loads of a tile precede its V loads, so the scores start as
 //        soon as K has landed.
-//     2. Scores: lane = token (x2 lanes per token at head_dim 128), all G
-//        heads.  Single-tile kernels: v_dot2c_f32_{f16,bf16}, q by DPP
-//        broadcast.  Tile-pair kernels: v_mfma_f32_32x32x16 with the heads as
-//        rows and the tokens as columns (q the A operand, K read from LDS as
-//        the B operand), then one permlane32 swap per four heads puts every
-//        head of a token in that token's lane.
+//     2. Scores: v_mfma_f32_32x32x16 with the heads as rows and the tokens
+//        as columns (q the A operand, K read from LDS as the B operand); one
+//        permlane32 swap per four heads then puts every head of a token in
+//        that token's lane (x2 lanes per token at head_dim 128), the layout
+//        of the softmax and PV.
 //     3. Online softmax in the exp2 domain with a lazy reference point: the
 //        running max moves (wave max by a DPP reduction, rescale of o) only
 //        when a score passes it by more than kLazyMax.
@@ -112,28 +112,6 @@ __device__ inline void dma4(const void* g, lds_char* l) {
   __builtin_amdgcn_global_load_lds(g, (lds_void*)l, 4, 0, 0);
 }
 
-// x = LDS dword at byte address a + OFF; complete only after lds_wait.
-template <int OFF>
-__device__ inline void lds_read_u32_async(uint32_t a, uint32_t& x) {
-  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(x) : "v"(a), "i"(OFF));
-}
-// Waits for every outstanding LDS read of this wave; x and y come out of it,
-// so their uses stay behind the wait.
-__device__ inline void lds_wait(uint32_t& x, uint32_t& y) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x), "+v"(y));
-}
-
-// Issues the LDS reads of q words M..N-1 of the single-tile kernel: word m
-// of the lane (see q_word in decode_impl) is at byte (m/2 * HD + m%2 * 16) * 4
-// from the lane's base address.
-template <int M, int N, int HD>
-__device__ __attribute__((always_inline)) inline void read_q_words(uint32_t qa, uint32_t* qd) {
-  if constexpr (M < N) {
-    lds_read_u32_async<((M / 2) * HD + (M % 2) * 16) * 4>(qa, qd[M]);
-    read_q_words<M + 1, N, HD>(qa, qd);
-  }
-}
-
 // The operands of one RoPE dword pair from LDS (byte addresses): x and bias
 // words at dims j and j + D/2, the cos and sin of dims j, j + 1; complete on
 // return.  asm for the reason given at lds_read4.
@@ -183,89 +161,6 @@ __device__ inline void lds_read4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t
 // 32-bit LDS address of a pointer into a __shared__ array.
 __device__ inline uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const lds_char*)p;
-}
-
-// Scores of H heads (H <= 4) against one lane's 16 K dwords:
-//   acc[i] += sum over j < 16 of dot2(q word j of head i, k[j]),
-// where q word j is lane j of this lane's 16-lane row of register q[i] (DPP
-// row_newbcast hands it to every lane of the row).  The dots are issued
-// j-major, head-minor, so consecutive instructions are independent and one
-// wave alone keeps the VALU busy.  The compiler does not see the
-// instructions inside the asm, so the block pads both hazards itself:
-// s_nop 1 before (a VALU write of q just before a DPP read of it needs 2 wait
-// states) and s_nop 2 after (a v_dot result read by any VALU instruction
-// other than the same dot reading it as accumulator needs 3 wait states;
-// without them the next instruction can read a stale accumulator).
-#define LUC_DQ1(OP, j) OP " %[a0], %[q0], %[k" #j "] row_newbcast:" #j "\n\t"
-#define LUC_DQ2(OP, j) LUC_DQ1(OP, j) OP " %[a1], %[q1], %[k" #j "] row_newbcast:" #j "\n\t"
-#define LUC_DQ3(OP, j) LUC_DQ2(OP, j) OP " %[a2], %[q2], %[k" #j "] row_newbcast:" #j "\n\t"
-#define LUC_DQ4(OP, j) LUC_DQ3(OP, j) OP " %[a3], %[q3], %[k" #j "] row_newbcast:" #j "\n\t"
-#define LUC_DQS(H, OP)                                                                      \
-  "s_nop 1\n\t" LUC_DQ##H(OP, 0) LUC_DQ##H(OP, 1) LUC_DQ##H(OP, 2) LUC_DQ##H(OP, 3)        \
-      LUC_DQ##H(OP, 4) LUC_DQ##H(OP, 5) LUC_DQ##H(OP, 6) LUC_DQ##H(OP, 7) LUC_DQ##H(OP, 8)  \
-          LUC_DQ##H(OP, 9) LUC_DQ##H(OP, 10) LUC_DQ##H(OP, 11) LUC_DQ##H(OP, 12)            \
-              LUC_DQ##H(OP, 13) LUC_DQ##H(OP, 14) LUC_DQ##H(OP, 15) "s_nop 2"
-#define LUC_DQ_OUT1 [a0] "+v"(acc[0])
-#define LUC_DQ_OUT2 LUC_DQ_OUT1, [a1] "+v"(acc[1])
-#define LUC_DQ_OUT3 LUC_DQ_OUT2, [a2] "+v"(acc[2])
-#define LUC_DQ_OUT4 LUC_DQ_OUT3, [a3] "+v"(acc[3])
-#define LUC_DQ_IN1 [q0] "v"(q[0])
-#define LUC_DQ_IN2 LUC_DQ_IN1, [q1] "v"(q[1])
-#define LUC_DQ_IN3 LUC_DQ_IN2, [q2] "v"(q[2])
-#define LUC_DQ_IN4 LUC_DQ_IN3, [q3] "v"(q[3])
-#define LUC_DQ_K                                                                             \
-  [k0] "v"(k[0].x), [k1] "v"(k[0].y), [k2] "v"(k[0].z), [k3] "v"(k[0].w), [k4] "v"(k[1].x), \
-      [k5] "v"(k[1].y), [k6] "v"(k[1].z), [k7] "v"(k[1].w), [k8] "v"(k[2].x),               \
-      [k9] "v"(k[2].y), [k10] "v"(k[2].z), [k11] "v"(k[2].w), [k12] "v"(k[3].x),            \
-      [k13] "v"(k[3].y), [k14] "v"(k[3].z), [k15] "v"(k[3].w)
-#define LUC_DQ_ASM(H, OP) asm(LUC_DQS(H, OP) : LUC_DQ_OUT##H : LUC_DQ_IN##H, LUC_DQ_K)
-
-template <int DT, int H>
-__device__ __attribute__((always_inline)) inline void dot_heads(float (&acc)[H], const uint32_t (&q)[H],
-                                                                const uint4 (&k)[4]) {
-  static_assert(H >= 1 && H <= 4, "one block holds 1 to 4 heads");
-  if constexpr (DT == kF16) {
-    if constexpr (H == 1) LUC_DQ_ASM(1, "v_dot2c_f32_f16_dpp");
-    else if constexpr (H == 2) LUC_DQ_ASM(2, "v_dot2c_f32_f16_dpp");
-    else if constexpr (H == 3) LUC_DQ_ASM(3, "v_dot2c_f32_f16_dpp");
-    else LUC_DQ_ASM(4, "v_dot2c_f32_f16_dpp");
-  } else {
-    if constexpr (H == 1) LUC_DQ_ASM(1, "v_dot2c_f32_bf16_dpp");
-    else if constexpr (H == 2) LUC_DQ_ASM(2, "v_dot2c_f32_bf16_dpp");
-    else if constexpr (H == 3) LUC_DQ_ASM(3, "v_dot2c_f32_bf16_dpp");
-    else LUC_DQ_ASM(4, "v_dot2c_f32_bf16_dpp");
-  }
-}
-
-// Scores of all G heads for one 16-dword K chunk: the heads in (at most) two
-// blocks of up to 4; q word hc of head g is in qd[2g + hc].
-template <int DT, int G>
-__device__ __attribute__((always_inline)) inline void dot_all_heads(float (&acc)[G], const uint32_t* qd,
-                                                                    int hc, const uint4 (&k)[4]) {
-  constexpr int H1 = G <= 4 ? G : (G + 1) / 2;
-  constexpr int H2 = G - H1;
-  float a1[H1];
-  uint32_t q1[H1];
-#pragma unroll
-  for (int i = 0; i < H1; ++i) {
-    a1[i] = acc[i];
-    q1[i] = qd[2 * i + hc];
-  }
-  dot_heads<DT, H1>(a1, q1, k);
-#pragma unroll
-  for (int i = 0; i < H1; ++i) acc[i] = a1[i];
-  if constexpr (H2 > 0) {
-    float a2[H2];
-    uint32_t q2[H2];
-#pragma unroll
-    for (int i = 0; i < H2; ++i) {
-      a2[i] = acc[H1 + i];
-      q2[i] = qd[2 * (H1 + i) + hc];
-    }
-    dot_heads<DT, H2>(a2, q2, k);
-#pragma unroll
-    for (int i = 0; i < H2; ++i) acc[H1 + i] = a2[i];
-  }
 }
 
 // Bias + RoPE of one pair (x1, x2) in f32, each product and the
@@ -594,10 +489,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
   constexpr bool T1 = NB == 1;
   constexpr bool FASTQ = T1 && !APPEND;
   constexpr bool FASTA = T1 && APPEND;
-  // Scores on the matrix cores (MQK): q as the A operand of
-  // v_mfma_f32_32x32x16, KS k-steps of 16 dims, NBLK blocks of 32 tokens per
-  // tile.
-  constexpr bool MQK = true;
+  // Scores on the matrix cores: q as the A operand of v_mfma_f32_32x32x16, KS
+  // k-steps of 16 dims, NBLK blocks of 32 tokens per tile.
   constexpr int KS = D / 16;
   constexpr int NBLK = S::TILE / 32;
   constexpr int NQ = (GD * 2 + 255) / 256;  // 4-byte direct-to-LDS loads for q
@@ -652,12 +545,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   const int p0 = s_begin / kPage;  // lane j of tab0 / tab1: page j / 64 + j of the split
   const int tab0 = T1 ? 0 : trow[min(p0 + lane, tmax)];
   const int tab1 = !T1 && ST > 64 * kPage ? trow[min(p0 + 64 + lane, tmax)] : 0;
-  // q registers: qd[2g + hc], lane (row-half qhalf, j = lane % 16) holds q
-  // word g * D/2 + qhalf * 32 + hc * 16 + j of the row (32-bit words), where
-  // qhalf = lane / 32 at head_dim 128 (the lane's 64 dims), else 0.
-  const int qhalf = D == 128 ? lane / 32 : 0;
-  auto q_word = [&](int m) { return (m / 2) * HD + qhalf * 32 + (m % 2) * 16 + (lane & 15); };
-  // MQK: the A operand of k-step ks, q[head lane % 32][16 ks + 8 (lane / 32)
+  // The A operand of k-step ks, q[head lane % 32][16 ks + 8 (lane / 32)
   // .. + 8] of a row of the G heads' q (4-byte aligned); zero past head G - 1.
   auto q_operand = [&](const uint16_t* row, int ks) {
     const int g = lane & 31;
@@ -679,14 +567,10 @@ __device__ void decode_impl(const DecodeArgs& A) {
 #pragma unroll
     for (int i = 0; i < S::PAGES; ++i) traw[i] = v[i];
   }
-  uint32_t qd[MQK ? 1 : 2 * G];
-  uint4 qm[MQK ? KS : 1];
-  if constexpr (MQK && !APPEND && !FASTQ) {
+  uint4 qm[KS];  // q as MFMA A operands
+  if constexpr (!APPEND && !FASTQ) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qm[ks] = q_operand(qrow, ks);
-  } else if constexpr (!MQK && !APPEND && !FASTQ) {
-#pragma unroll
-    for (int m = 0; m < 2 * G; ++m) qd[m] = ((const uint32_t*)qrow)[q_word(m)];
   }
   int pos = A.positions[b];
   if constexpr (T1) {
@@ -940,56 +824,34 @@ __device__ void decode_impl(const DecodeArgs& A) {
       wave_lds_sync();
     }
     float acc[G];
-    if constexpr (MQK) {
-      // S = Q K^T on the matrix cores, per 32-token block: rows = the
-      // group's heads, columns = tokens, B lane = (token lane % 32, 8 dims
-      // of chunk 2 ks + lane / 32).  Lane l then holds heads 4(l/32) + j of
-      // token l % 32 in sc[.][j]; one permlane32 swap per j gives every lane
-      // heads j and 4 + j of its own token (lane = token at head_dim 64,
-      // token lane % 32 in both lane halves at 128).
-      f32x16 sc[NBLK];
+    // S = Q K^T on the matrix cores, per 32-token block: rows = the
+    // group's heads, columns = tokens, B lane = (token lane % 32, 8 dims
+    // of chunk 2 ks + lane / 32).  Lane l then holds heads 4(l/32) + j of
+    // token l % 32 in sc[.][j]; one permlane32 swap per j gives every lane
+    // heads j and 4 + j of its own token (lane = token at head_dim 64,
+    // token lane % 32 in both lane halves at 128).
+    f32x16 sc[NBLK];
 #pragma unroll
-      for (int nb = 0; nb < NBLK; ++nb) {
-        sc[nb] = f32x16{};
-        const int tok = nb * 32 + (lane & 31);
-        const uint32_t kr = lds_addr(kb) + tok * S::ROWB;
-        const int sw = tok & 7;
-        auto kaddr = [&](int ks) { return kr + ((uint32_t)((2 * ks + (lane >> 5)) ^ sw) << 4); };
+    for (int nb = 0; nb < NBLK; ++nb) {
+      sc[nb] = f32x16{};
+      const int tok = nb * 32 + (lane & 31);
+      const uint32_t kr = lds_addr(kb) + tok * S::ROWB;
+      const int sw = tok & 7;
+      auto kaddr = [&](int ks) { return kr + ((uint32_t)((2 * ks + (lane >> 5)) ^ sw) << 4); };
 #pragma unroll
-        for (int k4 = 0; k4 < KS; k4 += 4) {
-          uint4 kc[4];
-          lds_read4(kaddr(k4), kaddr(k4 + 1), kaddr(k4 + 2), kaddr(k4 + 3), kc);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sc[nb] = mfma32<DT>(qm[k4 + i], kc[i], sc[nb]);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(sc[0][j]),
-                                                        __float_as_uint(sc[NBLK - 1][j]), false, false);
-        if (j < G) acc[j] = __uint_as_float(r[0]);
-        if (4 + j < G) acc[4 + j] = __uint_as_float(r[1]);
-      }
-    } else {
-#pragma unroll
-      for (int g = 0; g < G; ++g) acc[g] = 0.0f;
-      const uint32_t krow = lds_addr(kb) + tq * S::ROWB;
-      const int sw = tq & 7;
-      auto ka = [&](int c) { return krow + ((uint32_t)((qh * 8 + c) ^ sw) << 4); };
-#pragma unroll
-      for (int hc = 0; hc < 2; ++hc) {  // chunks 4*hc .. 4*hc+3 of the lane's 64 dims
+      for (int k4 = 0; k4 < KS; k4 += 4) {
         uint4 kc[4];
-        lds_read4(ka(4 * hc), ka(4 * hc + 1), ka(4 * hc + 2), ka(4 * hc + 3), kc);
-        dot_all_heads<DT, G>(acc, qd, hc, kc);
-      }
-      if constexpr (S::QKL == 2) {
+        lds_read4(kaddr(k4), kaddr(k4 + 1), kaddr(k4 + 2), kaddr(k4 + 3), kc);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const uint32_t u = __float_as_uint(acc[g]);
-          const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-          acc[g] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-        }
+        for (int i = 0; i < 4; ++i) sc[nb] = mfma32<DT>(qm[k4 + i], kc[i], sc[nb]);
       }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(sc[0][j]),
+                                                      __float_as_uint(sc[NBLK - 1][j]), false, false);
+      if (j < G) acc[j] = __uint_as_float(r[0]);
+      if (4 + j < G) acc[4 + j] = __uint_as_float(r[1]);
     }
 
     const bool valid = (t0 + tq) < s_end;
@@ -1142,7 +1004,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
     }
     if (ntw > 0) {
       LUC_WAIT_VM(8);  // K and q
-      // MQK: the A operands from a q row in LDS (asm reads: compiler-visible
+      // the A operands from a q row in LDS (asm reads: compiler-visible
       // reads of LDS would wait for every outstanding load)
       auto q_operands_lds = [&](const void* row) __attribute__((always_inline)) {
         const uint32_t qa = lds_addr(row) + (uint32_t)((min(lane & 31, G - 1) * D + 8 * (lane >> 5)) * 2);
@@ -1154,28 +1016,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
           for (int i = 0; i < 4; ++i) qm[k4 + i] = (lane & 31) < G ? x[i] : make_uint4(0, 0, 0, 0);
         }
       };
-      if constexpr (FASTQ) {  // q words from LDS: qd[m] = word q_word(m)
-        if constexpr (MQK) {
-          q_operands_lds(s_qr[w]);
-        } else {
-          const uint32_t qa = lds_addr(s_qr[w]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
-          read_q_words<0, 2 * G, HD>(qa, qd);
-#pragma unroll
-          for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
-        }
-      }
-      if constexpr (FASTA) {
-        // q words of the shared roped copy (asm reads: compiler-visible reads
-        // of LDS would wait for every outstanding load)
-        if constexpr (MQK) {
-          q_operands_lds(s_q[0]);
-        } else {
-          const uint32_t qa = lds_addr(s_q[0]) + (uint32_t)(((lane & 15) + qhalf * 32) * 4);
-          read_q_words<0, 2 * G, HD>(qa, qd);
-#pragma unroll
-          for (int g = 0; g < G; ++g) lds_wait(qd[2 * g], qd[2 * g + 1]);
-        }
-      }
+      if constexpr (FASTQ) q_operands_lds(s_qr[w]);
+      if constexpr (FASTA) q_operands_lds(s_q[0]);  // the shared roped copy
       tile_scores(t_first, 0);
       LUC_WAIT_VM(0);  // V
       tile_pv(t_first, vr0);
