@@ -289,13 +289,16 @@ def model_bench(lib, torch, prompt_len=128, steps=128, eager_steps=8):
             "eager_ms_per_token": round(eager_ms, 3)}
 
 
-def graph_us(torch, fn, n, reps=3):
-    """Median microseconds per call of fn(i), i < n, replayed from a HIP graph."""
+def graph_us(torch, fn, n, reps=5, warm=3):
+    """Median microseconds per call of fn(i), i < n, replayed from a HIP graph
+    after `warm` untimed replays (the first replays of a graph over freshly
+    allocated pools run several microseconds per call slower)."""
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for i in range(n):
             fn(i)
-    g.replay()
+    for _ in range(warm):
+        g.replay()
     torch.cuda.synchronize()
     runs = []
     for _ in range(reps):
