@@ -149,7 +149,23 @@ __device__ void argmax_impl(const uint16_t* x, int n, uint32_t* out) {
   const int t = threadIdx.x;
   float best = -1e30f;
   int idx = -1;
-  for (int i = t; i < n; i += kArgmaxThreads) {  // increasing i: the first of equals stays
+  // increasing i: the first of equals stays.  Sixteen of the thread's loads
+  // go out before any comparison, so the scan waits on memory once per
+  // sixteen elements instead of once per element.
+  constexpr int U = 16;
+  int i = t;
+  for (; i + (U - 1) * kArgmaxThreads < n; i += U * kArgmaxThreads) {
+    float v[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) v[k] = St<kBF16>::load(x[i + k * kArgmaxThreads]);
+#pragma unroll
+    for (int k = 0; k < U; ++k)
+      if (v[k] > best) {
+        best = v[k];
+        idx = i + k * kArgmaxThreads;
+      }
+  }
+  for (; i < n; i += kArgmaxThreads) {
     const float v = St<kBF16>::load(x[i]);
     if (v > best) {
       best = v;

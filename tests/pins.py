@@ -341,8 +341,9 @@ def argmax_tie_order(v):
 def argmax_cases(rng):
     """Logit rows for the greedy index: random rows, three equal maxima, a NaN
     in front, equal maxima at 600 and 1500 (1500 mod 1024 = 476 < 600, so
-    1500 wins), at 1024 and 2048 (thread 0 both: 1024 wins), and a row with
-    nothing above -1e30."""
+    1500 wins), at 1024 and 2048 (thread 0 both: 1024 wins), at 3077 and
+    149509 (thread 5 both, the first in a thread's blocks of sixteen loads and
+    the second past them: 3077 wins), and a row with nothing above -1e30."""
     out = []
     for n in (1, 7, 1000, 2100, 151936):
         x = bits(rng.standard_normal(n), "bf16")
@@ -360,6 +361,10 @@ def argmax_cases(rng):
             u = x.copy()
             u[[1024, 2048]] = bits(np.array([9.0, 9.0]), "bf16")
             out.append(u)
+        if n > 150000:
+            v = x.copy()
+            v[[5 + 1024 * 3, 5 + 1024 * 146]] = bits(np.array([9.0, 9.0]), "bf16")
+            out.append(v)
         out.append(bits(np.full(n, -1e31), "bf16"))
     return out
 
