@@ -61,6 +61,20 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
+// Two ds_read_b64_tr_b16: within each 16-lane group, output lane 4a + c
+// receives element c of the 8-byte chunks read by input lanes 4e + a,
+// e = 0..3.
+template <int OFF0, int OFF1>
+__device__ inline void lds_tr16x2(uint32_t a, uint2* x) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %2 offset:%3\n\t"
+      "ds_read_b64_tr_b16 %1, %2 offset:%4\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x[0]), "=&v"(x[1])
+      : "v"(a), "n"(OFF0), "n"(OFF1)
+      : "memory");
+}
+
 // v_mfma_f32_32x32x16_{f16,bf16}: c += a * b, eight 16-bit values per lane
 // in a and b.  Operand layouts: A lane l = row l % 32, k (l / 32) * 8 .. + 8;
 // B lane l = column l % 32, the same k; C lane l = column l % 32, c[4i + j] =

@@ -203,6 +203,19 @@ __device__ inline uint32_t pack_p(float lo, float hi) {
   else return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
+// The storage-type bits of a p already rounded to that type.
+template <int DT>
+__device__ inline uint16_t p_bits(float p) {
+  if constexpr (DT == kF16) return __builtin_bit_cast(uint16_t, (_Float16)p);
+  else return (uint16_t)(__float_as_uint(p) >> 16);
+}
+
+// 16 bytes to LDS byte address a (asm: a compiler-visible LDS store would
+// wait for every outstanding direct-to-LDS load of the wave).
+__device__ inline void lds_write16(uint32_t a, uint4 v) {
+  asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(__builtin_bit_cast(u32x4_t, v)) : "memory");
+}
+
 // x[i] for a wave-uniform runtime i < N, without indexing a register array.
 template <int N>
 __device__ __attribute__((always_inline)) inline float pick(const float (&x)[N], int i) {
@@ -335,24 +348,40 @@ __device__ void qk_writeback(const DecodeArgs& A, int b, int h, const uint16_t* 
 // counted; the last split of (b, h) to arrive merges the partials.  s_last is
 // one word of LDS; sq / sk are the step variant's roped q and k of the new
 // token, written back into the qkv row by the workgroup that finishes last.
-template <int DT, int D, int G, bool APPEND, int W>
+template <int DT, int D, int G, bool APPEND, int W, bool MPV, int NO, int NA>
 __device__ __attribute__((always_inline)) inline void finish_split(
-    const DecodeArgs& A, float (&o)[G][8], const float (&m_run)[G], const float (&l_lane)[G],
+    const DecodeArgs& A, float (&o)[NO][8], const f32x16 (&oacc)[NA], const float (&m_run)[G],
+    const float (&l_lane)[G],
     float* recs, int rec_stride, uint32_t* s_last, const uint16_t* sq, const uint16_t* sk, int split,
     int bh, int b, int h, int nsplit, uint16_t* out_row) {
   constexpr int GD = G * D;
   constexpr int NV = 8 * G;  // o values per lane: 8 dims x G heads
   constexpr int CH = D / 8;  // 16-byte chunks per token row
   constexpr int NVP = (NV / 4 + 3) / 4 * 4;
-  constexpr int REC_ML = 4 * CH * NVP;
+  // MPV: the record holds o head-major (o[g][d] at g * D + d), then m and l
+  constexpr int REC_ML = MPV ? GD : 4 * CH * NVP;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int pv_ch = lane % CH;
-  // ---- reduce the wave's token groups (lanes sharing pv_ch): reduce-scatter ----
   float lsum[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) lsum[g] = l_lane[g];
   wave_sum_n<G>(lsum);
+  float* const recw = recs + w * rec_stride;
+  if constexpr (MPV) {
+    // o is complete per head in the MFMA accumulators (lane l: head l % 32,
+    // dims 32 db + 8 i + 4 (l / 32) + j in oacc[db][4 i + j])
+    const int hh = lane & 31;
+    if (hh < G) {
+#pragma unroll
+      for (int db = 0; db < NA; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *(float4*)(recw + hh * D + 32 * db + 8 * i + 4 * (lane >> 5)) =
+              make_float4(oacc[db][4 * i], oacc[db][4 * i + 1], oacc[db][4 * i + 2], oacc[db][4 * i + 3]);
+    }
+  } else {
+  // ---- reduce the wave's token groups (lanes sharing pv_ch): reduce-scatter ----
   float u[NV / 2], y[NV / 4];
 #pragma unroll
   for (int k = 0; k < NV / 2; ++k) {
@@ -373,10 +402,9 @@ __device__ __attribute__((always_inline)) inline void finish_split(
   }
 
   // ---- merge the W waves through LDS: each wave's record (o, m, l) ----
-  // the lane holds o values base + k (value v: head v / 8, dim pv_ch * 8 + v % 8)
-  const int base = ((lane >> 5) & 1) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);
+  // the lane holds o values of slot (lane / 16) * CH + pv_ch (value v: head v / 8,
+  // dim pv_ch * 8 + v % 8)
   const bool writer = D == 128 || (lane & 8) == 0;
-  float* const recw = recs + w * rec_stride;
   if (writer) {
     float* const slot = recw + ((lane >> 4) * CH + pv_ch) * NVP;
 #pragma unroll
@@ -384,6 +412,7 @@ __device__ __attribute__((always_inline)) inline void finish_split(
       *(float4*)(slot + k) = make_float4(y[k], k + 1 < NV / 4 ? y[k + 1] : 0.0f,
                                          k + 2 < NV / 4 ? y[k + 2] : 0.0f,
                                          k + 3 < NV / 4 ? y[k + 3] : 0.0f);
+  }
   }
   if (lane == 0) {
 #pragma unroll
@@ -397,7 +426,7 @@ __device__ __attribute__((always_inline)) inline void finish_split(
   for (int e = threadIdx.x; e < GD; e += 64 * W) {
     const int g = e / D, d = e % D;
     const int val = g * 8 + d % 8;  // the value's index in the reduce-scatter
-    const int idx = ((val / (NV / 4)) * CH + d / 8) * NVP + val % (NV / 4);
+    const int idx = MPV ? e : ((val / (NV / 4)) * CH + d / 8) * NVP + val % (NV / 4);
     float mw[W], M = -INFINITY;
 #pragma unroll
     for (int v = 0; v < W; ++v) {
@@ -493,6 +522,13 @@ __device__ void decode_impl(const DecodeArgs& A) {
   // k-steps of 16 dims, NBLK blocks of 32 tokens per tile.
   constexpr int KS = D / 16;
   constexpr int NBLK = S::TILE / 32;
+  // PV on the matrix cores too (MPV): O^T += V^T P^T, V staged in the tile's
+  // own K buffer once the scores have read it; o is then held as D/32 MFMA
+  // accumulators (lane l: head l % 32, dims 32 db + 8 i + 4 (l / 32) + j).
+  // Not in the head_dim 128 tile-pair kernels, whose 64 accumulators would
+  // not fit beside the tile pair in flight.
+  constexpr bool MPV = T1 || D == 64;
+  constexpr int ND = D / 32;
   constexpr int NQ = (GD * 2 + 255) / 256;  // 4-byte direct-to-LDS loads for q
   // FASTA operand block: q of the G heads, then their biases (256-byte
   // padded), then six regions of 2*D bytes: k, k bias, cos, sin, v, v bias.
@@ -515,6 +551,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
   constexpr int NVP = (NV / 4 + 3) / 4 * 4;
   constexpr int REC_ML = 4 * S::CH * NVP;
   static_assert(REC_ML + 2 * G <= S::KBYTES / 4, "merge record fits a K buffer");
+  static_assert(GD + 2 * G <= S::KBYTES / 4, "head-major merge record fits a K buffer");
+  static_assert(G * S::TILE * 2 <= PWORDS * 4, "p of the tile, head-major, fits the p exchange");
   __shared__ __attribute__((aligned(16))) char s_k[W][NB][S::KBYTES];
   __shared__ __attribute__((aligned(16))) uint32_t s_p[W][PWORDS];
   constexpr int NOP = (APPEND && !FASTA) ? W : 1;  // copies of the step operands
@@ -803,13 +841,21 @@ __device__ void decode_impl(const DecodeArgs& A) {
     for (int ks = 0; ks < KS; ++ks) qm[ks] = q_operand(s_q[qi], ks);
   }
 
-  float m_run[G], l_lane[G], o[G][8];
+  float m_run[G], l_lane[G], o[MPV ? 1 : G][8];
+  f32x16 oacc[MPV ? ND : 1];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m_run[g] = -INFINITY;
     l_lane[g] = 0.0f;
+  }
+  if constexpr (MPV) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+    for (int db = 0; db < ND; ++db) oacc[db] = f32x16{};
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
   }
 
   // ---- scores, online softmax and p exchange of the tile at t0 (K in buf) ----
@@ -875,8 +921,16 @@ __device__ void decode_impl(const DecodeArgs& A) {
         if (m_run[g] > -INFINITY) {  // (nothing accumulated before the first tile)
           const float alpha = __builtin_amdgcn_exp2f(m_run[g] - mn);
           l_lane[g] *= alpha;
+          if constexpr (MPV) {  // head g's accumulators are in lanes g and g + 32
+            const bool mine = (lane & 31) == g;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
+            for (int db = 0; db < ND; ++db)
+#pragma unroll
+              for (int k = 0; k < 16; ++k) oacc[db][k] = mine ? oacc[db][k] * alpha : oacc[db][k];
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
+          }
         }
         m_run[g] = mn;
       }
@@ -889,20 +943,29 @@ __device__ void decode_impl(const DecodeArgs& A) {
       l_lane[g] += qh == 0 ? p[g] : 0.0f;
     }
 
-    // p to the load layout through LDS
     uint32_t* const sp = s_p[w];
-    uint32_t pk[8];
+    if constexpr (MPV) {
+      // p through LDS head-major, [g][token] in the storage type (P^T of PV)
+      uint16_t* const sp16 = (uint16_t*)sp;
+      if (qh == 0) {
 #pragma unroll
-    for (int g = 0; g < 8; ++g) pk[g] = g < G ? pack_p<DT>(p[g], upper_half_value<D>(p[g])) : 0u;
-    if (lane < S::HALF) {
-      *(uint4*)(sp + tq * 8) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-      *(uint4*)(sp + tq * 8 + 4) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+        for (int g = 0; g < G; ++g) sp16[g * S::TILE + tq] = p_bits<DT>(p[g]);
+      }
+    } else {
+      // p to the load layout through LDS
+      uint32_t pk[8];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) pk[g] = g < G ? pack_p<DT>(p[g], upper_half_value<D>(p[g])) : 0u;
+      if (lane < S::HALF) {
+        *(uint4*)(sp + tq * 8) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        *(uint4*)(sp + tq * 8 + 4) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+      }
     }
     wave_lds_sync();
   };
 
   // ---- o += p * V of the tile at t0, V in its load layout ----
-  auto tile_pv = [&](int t0, uint4(&vr)[S::LOADS]) __attribute__((always_inline)) {
+  auto tile_pv = [&](int t0, int buf, uint4(&vr)[S::LOADS]) __attribute__((always_inline)) {
     if constexpr (APPEND) {
       if (owns && pos >= t0 && pos < t0 + S::TILE) {  // the new token's V
         const int t = pos - t0;
@@ -914,6 +977,38 @@ __device__ void decode_impl(const DecodeArgs& A) {
     // tokens past the split: V must contribute exactly zero (p is 0 there,
     // and 0 * stale data must not produce NaN)
     const bool partial = t0 + S::TILE > s_end;
+    if constexpr (MPV) {
+      // V into the tile's K buffer (free: the scores have read it), in K's
+      // layout: chunk c of token t at slot c ^ (t & 7)
+      const uint32_t vbase = lds_addr(s_k[w][buf]);
+#pragma unroll
+      for (int r = 0; r < S::LOADS; ++r) {
+        const int t = r * S::TPL + pv_tok;
+        const uint4 v = partial && t0 + t >= s_end ? make_uint4(0, 0, 0, 0) : vr[r];
+        lds_write16(vbase + t * S::ROWB + ((pv_ch ^ (t & 7)) << 4), v);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // O^T += V^T P^T per 16-token step c: A = V^T by transposing reads
+      // (lane: dim 32 db + lane % 32, tokens 16c + 4(lane / 32) + 0..3 and
+      // + 8 + ...), B = P^T (lane: head lane % 32, the same tokens)
+      const int hh = lane & 31, gs = lane >> 5;
+      const uint16_t* const pt = (const uint16_t*)s_p[w] + min(hh, G - 1) * S::TILE + 4 * gs;
+      const int tr = 4 * gs + ((lane & 15) >> 2);
+      const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+      for (int c = 0; c < S::TILE / 16; ++c) {
+        const uint2 pa = *(const uint2*)(pt + 16 * c);
+        const uint2 pb2 = *(const uint2*)(pt + 16 * c + 8);
+        const uint4 pb = hh < G ? make_uint4(pa.x, pa.y, pb2.x, pb2.y) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int db = 0; db < ND; ++db) {
+          uint2 va[2];
+          lds_tr16x2<0, 8 * S::ROWB>(
+              vbase + (16 * c + tr) * S::ROWB + ((((32 * db + tr_d) / 8) ^ tr) << 4) + (tr_d % 8) * 2, va);
+          oacc[db] = mfma32<DT>(make_uint4(va[0].x, va[0].y, va[1].x, va[1].y), pb, oacc[db]);
+        }
+      }
+    } else {
     const uint32_t* const sp = s_p[w];
 #pragma unroll
     for (int r = 0; r < S::LOADS / 2; ++r) {
@@ -938,6 +1033,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[g][e] = St<DT>::dot2(pr[e], pp[g], o[g][e]);
+    }
     }
     wave_lds_sync();
   };
@@ -1020,7 +1116,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       if constexpr (FASTA) q_operands_lds(s_q[0]);  // the shared roped copy
       tile_scores(t_first, 0);
       LUC_WAIT_VM(0);  // V
-      tile_pv(t_first, vr0);
+      tile_pv(t_first, 0, vr0);
     }
   } else {
     // The wave's tiles in pairs: both tiles of a pair are issued
@@ -1035,12 +1131,12 @@ __device__ void decode_impl(const DecodeArgs& A) {
       LUC_WAIT_VM(24);  // K_i
       tile_scores(t0, 0);
       LUC_WAIT_VM(16);  // V_i
-      tile_pv(t0, va);
+      tile_pv(t0, 0, va);
       if (pair) {
         LUC_WAIT_VM(8);  // K_{i+1}
         tile_scores(t0 + WS, 1);
         LUC_WAIT_VM(0);  // V_{i+1}
-        tile_pv(t0 + WS, vb);
+        tile_pv(t0 + WS, 1, vb);
       }
     };
     if (ntw > 0) {
@@ -1071,7 +1167,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
     for (int g = 0; g < G; ++g) l_lane[g] = __builtin_nanf("");
   }
 
-  finish_split<DT, D, G, APPEND, W>(A, o, m_run, l_lane, (float*)s_k[0][0], NB * S::KBYTES / 4,
+  finish_split<DT, D, G, APPEND, W, MPV>(A, o, oacc, m_run, l_lane, (float*)s_k[0][0], NB * S::KBYTES / 4,
                                     &s_p[0][0], s_q[0], s_knew[0], split, bh, b, h, nsplit, out_row);
 }
 

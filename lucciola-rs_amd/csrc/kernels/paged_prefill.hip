@@ -103,19 +103,6 @@ __device__ inline void lds_b128x4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_
       : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "n"(OFF)
       : "memory");
 }
-// Two ds_read_b64_tr_b16: within each 16-lane group, output lane 4a + c
-// receives element c of the 8-byte chunks read by input lanes 4e + a,
-// e = 0..3.
-template <int OFF0, int OFF1>
-__device__ inline void lds_tr16x2(uint32_t a, uint2* x) {
-  asm volatile(
-      "ds_read_b64_tr_b16 %0, %2 offset:%3\n\t"
-      "ds_read_b64_tr_b16 %1, %2 offset:%4\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(x[0]), "=&v"(x[1])
-      : "v"(a), "n"(OFF0), "n"(OFF1)
-      : "memory");
-}
 
 // head_dim 64: the operand reads of one block, issued ahead of the VALU work
 // that hides their latency, and waited for separately.  The outputs are not
