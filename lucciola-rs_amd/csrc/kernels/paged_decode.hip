@@ -52,14 +52,19 @@
 //     3. Online softmax in the exp2 domain with a lazy reference point: the
 //        running max moves (wave max by a DPP reduction, rescale of o) only
 //        when a score passes it by more than kLazyMax.
-//     4. o += p * V with V in its load layout: p of tokens t and t + TILE/2
-//        packed as a pair of the storage type, V of the same two tokens
-//        paired by v_perm, one v_dot2_f32_{f16,bf16} per (head, dim).  p is
-//        rounded where it is computed, so l sums the same values the
-//        products use, and the running max is kept on whole numbers, so
+//     4. o += p * V.  Single-tile and head_dim 64 kernels: O^T += V^T P^T on
+//        v_mfma_f32_32x32x16, V written into the tile's K buffer once the
+//        scores have read it and read back transposed (ds_read_b64_tr_b16),
+//        p through LDS head-major; o stays in the MFMA accumulators.  The
+//        head_dim 128 tile-pair kernels: V in its load layout, p of tokens t
+//        and t + TILE/2 packed as a pair of the storage type, V of the same
+//        two tokens paired by v_perm, one v_dot2_f32_{f16,bf16} per (head,
+//        dim).  p is rounded where it is computed, so l sums the same values
+//        the products use, and the running max is kept on whole numbers, so
 //        that a token's p rounds alike in every split.
-//   Each wave's token groups are reduced with permlane swaps
-//   (reduce-scatter); the W waves merge their (m, l, o) through LDS.  A
+//   The dot2 form reduces each wave's token groups with permlane swaps
+//   (reduce-scatter); the MFMA form's accumulators are already complete.
+//   The W waves merge their (m, l, o) through LDS.  A
 //   sequence with one split writes its output; otherwise each split writes
 //   (m, l, o) to the workspace and the last split to arrive merges them.
 //   The step variant's last workgroup also writes the roped q and k of the
