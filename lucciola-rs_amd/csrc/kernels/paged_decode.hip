@@ -1180,7 +1180,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
 
 // Decode kernels: _t1 has 8 waves per workgroup, one tile each (splits of 8
 // tiles; 80 KB of LDS, two workgroups per CU, so four waves per SIMD, which
-// the register target keeps up to group size 7), _t2 has 4 waves with two
+// the register target keeps up to group size 7 at head_dim 64 and 6 at 128),
+// _t2 has 4 waves with two
 // tiles in flight each (longer splits).  Resident-wave targets are per SIMD.
 #define LUC_DECODE_KERNELS(DTN, DT, D, G, NB, OCC, W)                                               \
   extern "C" __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC)))         \
@@ -1193,7 +1194,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   }
 
 #define LUC_DECODE(DTN, DT, D, G)                                                                  \
-  LUC_DECODE_KERNELS(DTN, DT, D, G, 1, (G <= 7 ? 4 : 2), 8)                                        \
+  LUC_DECODE_KERNELS(DTN, DT, D, G, 1, ((D == 64 ? G <= 7 : G <= 6) ? 4 : 2), 8)                   \
   LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2, 4)
 
 #define LUC_DECODE_GROUPS(DTN, DT, D)                                                              \
