@@ -9,10 +9,12 @@ Workload (default `batch32_mixed`): B=32 sequences, Qwen2.5-0.5B heads
 16384-page pool handed out by a seeded shuffle, 24 layers.  A step is one
 layer's decode step for the whole batch (luc_decode_step, one launch): RoPE(q,
 k) + paged append of one new token per sequence, split-K paged attention whose
-last split per sequence merges the partials (log-sum-exp).  Successive steps walk the 24 layers so the working set (~830 MB)
-does not fit the 256 MB Infinity Cache.  Inputs are resident in HBM before
-timing; the K steps are replayed from a HIP graph, bracketed by
-torch.cuda.synchronize().
+last split per sequence merges the partials (log-sum-exp).  Successive steps
+walk the 24 layers (all of them when K >= 24) so the working set (~830 MB at 24
+layers) does not fit the 256 MB Infinity Cache.  Inputs are resident in HBM
+before timing; the K steps are captured in one HIP graph, replayed three
+times untimed and then three times timed, each timed replay bracketed by
+torch.cuda.synchronize(); ms_per_step is the median replay over K.
 
 Also reported:
   roofline      the paged decode operation (luc_paged_decode: the split-K
@@ -21,7 +23,8 @@ Also reported:
                 over its average duration, measured with HIP events around a
                 graph of back-to-back launches on the launch stream;
                 `traffic` is the HBM bytes per launch read from the committed
-                rocprofv3 PMC summary, if present;
+                rocprofv3 PMC summary, if that summary measured the code
+                object loaded now (its SHA-256 matches), else null;
   cpu_baseline  the oracle (C restatement of the reference's attention, OpenMP)
                 on one full layer step of the same workload on the host, on the
                 process's CPU share (the cores it may run on, at most the
@@ -30,7 +33,8 @@ Also reported:
                 is the same for the single-sequence workload (B=1, ctx 512,
                 14q/2kv, fp16), the one the reference's own path serves;
   long_context  the paged decode operation (luc_paged_decode) on
-                batch64_long (B=64, 28q/4kv, d=128, bf16, ctx U{1024..16384})
+                batch64_long (B=64, 28q/4kv, d=128, bf16, ctx U{1024..16384};
+                the automatic split and the configuration's 512-token split)
                 and batch8_32k (B=8, 12q/2kv, d=128, bf16, ctx 32768), 4
                 layers rotated, per launch: us, algorithmic GB/s, fraction
                 of 8 TB/s, and the two memory floors below for the same
@@ -46,7 +50,10 @@ Also reported:
                 call (HIP events over a graph of back-to-back calls) and the
                 attention's algorithmic FLOP rate against the 2.5 PFLOP/s dense
                 bf16 peak; mfma_busy_frac is the share of SIMD cycles with the
-                matrix cores busy, from the committed rocprofv3 PMC summary;
+                matrix cores busy, from the committed rocprofv3 PMC summary
+                (null unless it measured the code object loaded now);
+  code_objects  the first 16 hex digits of the SHA-256 of each code object
+                the measured kernels come from;
   sampling      luc_sort_and_sample on one logits row (vocab 151936, top_k
                 1024): time per call;
   model         the Qwen2 model loop (random-init Qwen2.5-0.5B, bf16, B=1):
@@ -74,6 +81,58 @@ PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_batch32_mixed_traffic.json")
 MFMA_FILE = os.path.join(ROOT, "profiles", "prefill_4x2048_mfma.json")
+CODE_DIR = os.path.join(ROOT, "lucciola-rs_amd", "lib")
+
+
+def code_object_sha256(name):
+    """SHA-256 of the machine code of the gfx950 code object lib/<name>.hsaco
+    that the library loads: its .text (the kernels' instructions) and .rodata
+    (their kernel descriptors: register counts, LDS size) sections, in that
+    order (None if it is not built).  The rest of the file (symbol tables)
+    names hipcc's temporary files and so differs from build to build of the
+    same source."""
+    import hashlib
+    import struct
+    path = os.path.join(CODE_DIR, name + ".hsaco")
+    if not os.path.exists(path):
+        return None
+    with open(path, "rb") as f:
+        elf = f.read()
+    if elf[:4] != b"\x7fELF" or elf[4] != 2 or elf[5] != 1:
+        return None  # not a little-endian ELF64 file
+    shoff, = struct.unpack_from("<Q", elf, 0x28)
+    shentsize, shnum, shstrndx = struct.unpack_from("<HHH", elf, 0x3A)
+    secs = [struct.unpack_from("<IIQQQQ", elf, shoff + i * shentsize) for i in range(shnum)]
+    strtab_off = secs[shstrndx][4]
+
+    def name_of(sec):
+        start = strtab_off + sec[0]
+        return elf[start:elf.index(b"\0", start)].decode()
+
+    by_name = {name_of(sec): sec for sec in secs}
+    h = hashlib.sha256()
+    for sec_name in (".text", ".rodata"):
+        sec = by_name.get(sec_name)
+        if sec is None:
+            return None
+        h.update(elf[sec[4]:sec[4] + sec[5]])
+    return h.hexdigest()
+
+
+def profile_value(path, key):
+    """`key` of a committed rocprofv3 PMC summary, or None when the summary is
+    missing or was measured on another build of its code object: the summary
+    names the code object and the SHA-256 it measured ("code_object",
+    "code_object_sha256"), and a figure is used only if that hash equals the
+    hash of the code object loaded now."""
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        prof = json.load(f)
+    name, sha = prof.get("code_object"), prof.get("code_object_sha256")
+    if not name or not sha or code_object_sha256(name) != sha:
+        return None
+    return prof.get(key)
 
 
 def parse():
@@ -192,11 +251,9 @@ def prefill_bench(lib, torch, reps=50):
 
 def mfma_busy():
     """Fraction of SIMD cycles with the matrix cores busy during the prefill
-    attention kernel, from the committed rocprofv3 PMC summary (or None)."""
-    if not os.path.exists(MFMA_FILE):
-        return None
-    with open(MFMA_FILE) as f:
-        return json.load(f).get("mfma_busy_frac")
+    attention kernel, from the committed rocprofv3 PMC summary (None unless it
+    measured the code object loaded now)."""
+    return profile_value(MFMA_FILE, "mfma_busy_frac")
 
 
 def sampling_bench(lib, torch, reps=100):
@@ -312,10 +369,12 @@ def graph_us(torch, fn, n, reps=5, warm=3):
     return statistics.median(runs)
 
 
-def long_context_bench(lib, torch, name, seed, layers=4, launches=40):
+def long_context_bench(lib, torch, name, seed, layers=4, launches=40, split_tokens=0):
     """luc_paged_decode on a long-context workload: us per launch (graph of
     back-to-back launches over `layers` rotated layers), algorithmic GB/s
-    and fraction of the 8 TB/s peak."""
+    and fraction of the 8 TB/s peak.  split_tokens 0 is the library's
+    automatic split; 512 is the split the batch64_long configuration names
+    (8..32 splits per sequence of its longer contexts)."""
     import numpy as np
     from lucciola_rs_amd import workloads as wl
     from lucciola_rs_amd.engine import sm_scale
@@ -326,12 +385,12 @@ def long_context_bench(lib, torch, name, seed, layers=4, launches=40):
     ctx = inp["ctx"]
     max_ctx = int(ctx.max())
     out = torch.empty((cfg.batch, cfg.hq * cfg.head_dim), dtype=cfg.torch_dtype, device=dev)
-    ws = lib.workspace(cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, max_ctx, 0)
+    ws = lib.workspace(cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, max_ctx, split_tokens)
 
     def call(i):
         lib.paged_decode(out, inp["qkv"], inp["k_pool"], inp["v_pool"], inp["tables"],
                          inp["positions"], cfg.batch, max_ctx, i % layers, layers, cfg.hq, cfg.hkv,
-                         cfg.head_dim, sm_scale(cfg.head_dim), 0, ws,
+                         cfg.head_dim, sm_scale(cfg.head_dim), split_tokens, ws,
                          out_row_stride=out.shape[-1], q_row_stride=cfg.row)
 
     for i in range(layers):
@@ -342,7 +401,8 @@ def long_context_bench(lib, torch, name, seed, layers=4, launches=40):
     gbs = nbytes / (us * 1e-6) / 1e9
     res = {"workload": name, "batch": cfg.batch, "q_heads": cfg.hq, "kv_heads": cfg.hkv,
            "head_dim": cfg.head_dim, "dtype": cfg.dtype, "mean_ctx": float(np.mean(ctx)),
-           "layers_rotated": layers, "us_per_launch": round(us, 2),
+           "layers_rotated": layers, "split_tokens": split_tokens or "auto",
+           "us_per_launch": round(us, 2),
            "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbs": round(gbs, 1),
            "frac": round(gbs / PEAK_HBM_GBS, 4)}
     res.update(floors(lib, torch, cfg, inp, max_ctx, layers, nbytes, launches=launches))
@@ -425,36 +485,40 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
-    def timed(fn, n):
-        """Milliseconds for n calls of fn, launched eagerly or replayed from a graph."""
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        if args.eager:
+    def timed(fn, n, reps=3):
+        """Milliseconds for n calls of fn, launched eagerly or replayed from a
+        graph: the median of `reps` timed runs of the n calls, each bracketed
+        by synchronizations (graphs: after three untimed replays, the first of
+        which uploads the graph)."""
+        runs = []
+        g = None
+        if not args.eager:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(n):
+                    fn(i)
+            for _ in range(3):
+                g.replay()
+        for _ in range(reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
             e0.record()
-            for i in range(n):
-                fn(i)
+            if g is None:
+                for i in range(n):
+                    fn(i)
+            else:
+                g.replay()
             e1.record()
             torch.cuda.synchronize()
-            return e0.elapsed_time(e1)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for i in range(n):
-                fn(i)
-        g.replay()  # first replay uploads the graph
-        torch.cuda.synchronize()
-        e0.record()
-        g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1)
+            runs.append(e0.elapsed_time(e1))
+        return statistics.median(runs)
 
-    # --- the K timed steps ---
+    # --- the K timed steps (median of three timed runs of all K) ---
     step_ms_total = timed(step, args.steps)
     ms_per_step = step_ms_total / args.steps
     # --- the decode kernel alone (graph of back-to-back launches) ---
-    dec_runs = [timed(decode_only, args.steps) / args.steps for _ in range(3)]
-    dec_ms = statistics.median(dec_runs)
+    dec_ms = timed(decode_only, args.steps) / args.steps
 
     if args.copy_calibration:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -475,7 +539,7 @@ def main():
         with open(TRAFFIC_FILE) as f:
             tr = json.load(f)
         if tr.get("workload") == args.workload and tr.get("split_tokens", 0) == args.split_tokens:
-            traffic = tr.get("hbm_bytes_per_launch")
+            traffic = profile_value(TRAFFIC_FILE, "hbm_bytes_per_launch")
 
     fl = floors(lib, torch, cfg, inp, max_ctx, L, dec_bytes)
     del inp, qkv, kp, vp
@@ -486,7 +550,8 @@ def main():
     model = None if args.no_model else model_bench(lib, torch)
     long_ctx = None
     if not args.no_long_context:
-        long_ctx = [long_context_bench(lib, torch, n, args.seed) for n in ("batch64_long", "batch8_32k")]
+        long_ctx = [long_context_bench(lib, torch, n, args.seed, split_tokens=st)
+                    for n, st in (("batch64_long", 0), ("batch64_long", 512), ("batch8_32k", 0))]
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -537,7 +602,8 @@ def main():
         "config": {"workload": cfg.name, "batch": cfg.batch, "q_heads": cfg.hq,
                    "kv_heads": cfg.hkv, "head_dim": cfg.head_dim,
                    "ctx": f"U{{{cfg.ctx_lo}..{cfg.ctx_hi}}}", "mean_ctx": float(np.mean(ctx)),
-                   "page_size": 16, "pool_pages": cfg.pool_pages, "layers_rotated": L,
+                   "page_size": 16, "pool_pages": cfg.pool_pages,
+                   "layers_rotated": min(L, args.steps),
                    "step": "luc_decode_step: rope + append + split-K decode with in-kernel LSE merge (one launch, one layer)",
                    "bytes_per_step": int(step_bytes),
                    "launch": "eager" if args.eager else "hip graph",
@@ -548,6 +614,8 @@ def main():
                      "us_per_launch": round(dec_ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": int(dec_bytes), **fl},
         "cpu_baseline": cpu,
+        "code_objects": {n: (code_object_sha256(n) or "")[:16] for n in
+                         ("paged_decode", "paged_prefill", "rope_append")},
         "long_context": long_ctx,
         "prefill": prefill,
         "sampling": sampling,
