@@ -28,8 +28,9 @@
  *    kv_cache.rs:57-59; its kernels read table entries unchecked,
  *    kv_cache.cu:28, attention.cu:82).  A table entry outside [0, num_blocks)
  *    is never used as an address: the cache write that would go through it is
- *    skipped (the row is left untouched, as for a position outside its table
- *    row) and every attention output whose context reaches that page is NaN.
+ *    skipped (the row's q and k are still roped in place, by every entry point
+ *    alike) and every attention output whose context reaches that page is NaN.
+ *    A position outside its table row (or negative) leaves the row untouched.
  *    num_blocks < 1 is LUC_E_INVALID.
  *  - Only block_size 16 (kv_cache.rs:35) and head_dim 64/128
  *    (kernels.rs:37-46) are supported; Hq must be a multiple of Hkv with
@@ -173,8 +174,12 @@ int luc_decode_step(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t qk
  * It has no counterpart in the reference (whose attention needs no
  * workspace).  The same launch and results as luc_decode_step with the same
  * arguments, except that the split-K workspace is the library's own fixed
- * scratch: a device array of LUC_SCRATCH_BYTES per GPU, resolved and
- * zero-filled by luc_init, held until the process ends.  Calls whose
+ * scratch: a device array of LUC_SCRATCH_BYTES per GPU, held until the
+ * process ends.  Every luc_init resolves its address on its device; the first
+ * luc_init for a device zero-fills it, and so does any later luc_init that
+ * finds the address changed (the device was reset).  Every launch leaves its
+ * arrival counters at zero again, so later contexts on the device reuse it
+ * as it is.  Calls whose
  * workspace (luc_paged_decode_workspace_size of the same sizes) exceeds
  * LUC_SCRATCH_BYTES fail with LUC_E_WORKSPACE before any launch.  The entry
  * point itself calls no allocator.  Every call on one GPU shares that GPU's

@@ -87,10 +87,10 @@ __device__ void rope_append_impl(uint16_t* q, const uint16_t* q_bias, uint16_t* 
   int64_t slot0 = 0;  // pool offset of (pos, head 0, dim 0)
   if (flags & kWriteKV) {
     const int64_t phys = tables[(int64_t)seq * table_stride + pos / kPage];
-    // a page outside the pool: the row is left untouched, as for a position
-    // outside the table row (the reference reads the entry unchecked,
-    // kv_cache.cu:28)
-    if (phys < 0 || phys >= num_blocks) return;
+    // a page outside the pool is never an address: q and k are still roped
+    // in place, only the cache write is skipped (the reference reads the
+    // entry unchecked, kv_cache.cu:28); the step kernel does the same
+    if (phys < 0 || phys >= num_blocks) flags &= ~kWriteKV;
     const int64_t page_elems = (int64_t)kPage * head_dim;
     slot0 = ((phys * num_layers + layer) * hkv) * page_elems + (int64_t)(pos % kPage) * head_dim;
   }
@@ -211,9 +211,12 @@ __device__ void rope_append_vec_impl(uint16_t* q, const uint16_t* q_bias, uint16
     c0 = cp[0]; c1 = cp[1]; s0 = sp[0]; s1 = sp[1];
   }
   int64_t slot0 = 0;  // pool offset of (pos, head 0, dim 0)
-  if (flags & kWriteKV) {
+  bool write_kv = (flags & kWriteKV) != 0;
+  if (write_kv) {
     const int64_t phys = tables[(int64_t)seq * table_stride + pos / kPage];
-    if (phys < 0 || phys >= num_blocks) return;  // outside the pool: the row is left untouched
+    // a page outside the pool is never an address: q and k are still roped
+    // in place, only the cache write is skipped (as in the step kernel)
+    write_kv = phys >= 0 && phys < num_blocks;
     slot0 = ((phys * num_layers + layer) * hkv) * head_stride + (int64_t)(pos % kPage) * D;
   }
   if (rot) {
@@ -222,12 +225,12 @@ __device__ void rope_append_vec_impl(uint16_t* q, const uint16_t* q_bias, uint16
       *(uint4*)(x + i) = a;
       *(uint4*)(x + i + HALF) = b;
     }
-    if (!isq && (flags & kWriteKV)) {
+    if (!isq && write_kv) {
       uint16_t* dst = k_pool + slot0 + h * head_stride + i;
       *(uint4*)dst = a;
       *(uint4*)(dst + HALF) = b;
     }
-  } else {
+  } else if (write_kv) {
     uint16_t o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)

@@ -4,9 +4,9 @@
 // The array below is device memory that the library owns for the life of the
 // process, one copy per GPU.  Its host-side name is only a stand-in for the
 // symbol: host code never passes `scratch` itself to a kernel or a copy.  At
-// set-up (luc_init), once per device and with that device current,
-// hipGetSymbolAddress gives that device's address of its copy; the context
-// keeps it, and every later use goes through that address.
+// set-up (every luc_init, with its device current) hipGetSymbolAddress gives
+// that device's address of its copy; the context keeps it, and every later
+// use goes through that address.
 //
 // Compiled by hipcc for gfx950 and linked into liblucattn.so.
 #include <hip/hip_runtime.h>
@@ -37,21 +37,22 @@ namespace luc_internal {
 
 int fail(int code, const char* fmt, ...);
 
-// Address of this device's scratch, resolved and zero-filled on the first
-// call for `device` (the caller has made `device` current).  Later calls for
-// the same device return the same address.
+// Address of this device's scratch (the caller has made `device` current),
+// resolved on every call: the first call for `device`, and any call that
+// finds the address changed since (the device was reset and its code
+// reloaded), zero-fills it.  Otherwise the contents are kept: every decode
+// launch leaves the arrival counters at zero again.
 int scratch_setup(int device, void** out) {
   *out = nullptr;
   if (device < 0 || device >= kMaxDevices)
     return fail(LUC_E_INVALID, "scratch: device %d outside [0, %d)", device, kMaxDevices);
   std::lock_guard<std::mutex> lock(g_mu);
-  if (!g_ptr[device]) {
-    void* ptr = nullptr;
-    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !ptr)
-      return fail(LUC_E_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-    // the arrival counters must start at zero; every decode launch leaves
-    // them at zero again
+  void* ptr = nullptr;
+  hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr)
+    return fail(LUC_E_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+  if (g_ptr[device] != ptr) {
+    // the arrival counters must start at zero
     const size_t n16 = LUC_SCRATCH_BYTES / 16;
     hipLaunchKernelGGL(luc_scratch_clear, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0,
                        nullptr, static_cast<uint4*>(ptr), n16);

@@ -373,7 +373,7 @@ void orc_prefill(uint16_t* out, int64_t out_stride, uint16_t* qkv, int64_t qkv_s
         float o[ORC_MAXD];
         attend_head(o, qkv + r * qkv_stride + (int64_t)h * head_dim, k_pool, v_pool,
                     block_tables + (int64_t)b * table_stride, layer, ORC_MUTANT == 9 ? h % num_kv_heads : h / group, num_kv_heads,
-                    head_dim, pos, sm_scale, block_size, num_layers, dtype);
+                    head_dim, ORC_MUTANT == 17 ? pos + 1 : pos, sm_scale, block_size, num_layers, dtype);
         for (int i = 0; i < head_dim; ++i)
             out[r * out_stride + (int64_t)h * head_dim + i] = st(o[i], dtype);
     }

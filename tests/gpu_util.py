@@ -79,3 +79,50 @@ def max_abs(orc, a_bits, b_bits, dtype):
     a = orc.to_f32(a_bits, dtype).astype(np.float64)
     b = orc.to_f32(b_bits, dtype).astype(np.float64)
     return float(np.max(np.abs(a - b)))
+
+
+def storage_ulp(x, dtype):
+    """The spacing of the storage type (bf16: 8 significant bits, fp16: 11,
+    normal range) at magnitude |x|, for float64 arrays."""
+    mant = 8 if dtype == "bf16" else 11
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -126)))
+    if dtype == "f16":
+        e = np.maximum(e, -14)  # fp16 subnormals: fixed spacing 2^-24
+    return 2.0 ** (e - (mant - 1))
+
+
+def ulp_gate(orc, got_bits, want_bits, dtype, max_ulps=4, max_frac=None):
+    """Attention outputs [rows, heads, d] against the oracle's, in storage
+    units at the row's scale: |got - want| over the storage spacing at
+    max(|want|, rms), rms being the root mean square of that (row, head)'s
+    output vector.  Every element must be within `max_ulps` such units and,
+    with max_frac, at most that fraction of the elements may differ at all.
+
+    Why units at the row's scale: the MFMA paths round each softmax weight p
+    to the storage type before the PV product (the 16-bit B operand), the
+    reference keeps it in f32.  With a relative error up to 2^-9 (bf16) or
+    2^-12 (fp16) per weight, the output moves by about 0.3 storage units at
+    the row's RMS (standard deviation), independent of the context length,
+    and an element near zero shows the same absolute error.  A dropped or
+    doubled token moves every element of a row by (v_t - o) / n: at n = 2048
+    and |v_t - o| ~ 0.5 that is ~5.6 units at the row's RMS, so a gate of a
+    few units still sees it in some element of every affected row.  The
+    units at rms / 4 are reported too.  Returns the report line; asserts."""
+    a = orc.to_f32(got_bits, dtype).astype(np.float64)
+    b = orc.to_f32(want_bits, dtype).astype(np.float64)
+    rms = np.sqrt(np.mean(b * b, axis=-1, keepdims=True))
+    err = np.abs(a - b)
+    units = err / storage_ulp(np.maximum(np.abs(b), rms), dtype)
+    units4 = err / storage_ulp(np.maximum(np.abs(b), rms / 4), dtype)
+    diff = int(np.count_nonzero(a != b))
+    hist = [int(np.count_nonzero(units <= 0.5)), int(np.count_nonzero((units > 0.5) & (units <= 1.5))),
+            int(np.count_nonzero((units > 1.5) & (units <= 2.5))), int(np.count_nonzero(units > 2.5))]
+    line = (f"storage units at the row's rms: max {units.max():.3f} (at rms/4: {units4.max():.3f}), "
+            f"elements <=0.5 / ~1 / ~2 / >2.5 units: {hist}, {diff} of {a.size} differ "
+            f"({diff / a.size:.2%})")
+    say("  " + line)
+    assert np.all(np.isfinite(a) == np.isfinite(b)), "finite / non-finite outputs differ"
+    assert units.max() <= max_ulps + 1e-9, line
+    if max_frac is not None:
+        assert diff <= max_frac * a.size, line
+    return line

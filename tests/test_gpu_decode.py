@@ -49,11 +49,19 @@ def test_decode_small_configs(orc, luc, name, batch, lo, hi, dtype, fused):
 
 @pytest.mark.parametrize("group", [1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("head_dim", [64, 128])
-def test_decode_every_group_size(orc, luc, group, head_dim):
+@pytest.mark.parametrize("dtype,kernel", [("bf16", "t1"), ("bf16", "t2"), ("f16", "t2")])
+def test_decode_every_group_size(orc, luc, group, head_dim, dtype, kernel):
+    """Every group size on both kernel shapes: the automatic split of these
+    small batches runs the single-tile (_t1) kernels; 256-token splits at
+    head_dim 64 and 512 at 128 run the tile-pair (_t2) kernels (two tiles
+    per wave, the head_dim 128 ones with PV on v_dot2), in both dtypes."""
     hkv = 2
-    cfg = wl.DecodeConfig(f"g{group}", 3, group * hkv, hkv, head_dim, "bf16", 1, 900, 3 * 57, 0.5)
+    cfg = wl.DecodeConfig(f"g{group}", 3, group * hkv, hkv, head_dim, dtype, 1, 900, 3 * 57, 0.5)
     h = wl.host_decode_inputs(cfg, seed=group)
-    assert_step_matches(orc, gpu_step(luc, h), oracle_step(orc, luc, h), "bf16")
+    split = 0 if kernel == "t1" else (256 if head_dim == 64 else 512)
+    assert_step_matches(orc, gpu_step(luc, h, split_tokens=split), oracle_step(orc, luc, h), dtype)
+    assert_step_matches(orc, gpu_step(luc, h, split_tokens=split, fused=False),
+                        oracle_step(orc, luc, h), dtype)
 
 
 def test_decode_layers_and_page_boundaries(orc, luc):

@@ -127,7 +127,7 @@ class OracleAttentionModel(Qwen2Model):
         self.bias_host = [tuple(from_dev(L[k]) for k in ("q_bias", "k_bias", "v_bias"))
                           for L in self.layers]
 
-    def _oracle(self, li, qkv, run):
+    def _oracle(self, li, qkv, run, first_pos):
         cfg = self.cfg
         qb, kb, vb = self.bias_host[li]
         table = self.kv.block_table.view(1, -1).cpu().numpy().astype(np.int32)
@@ -136,73 +136,178 @@ class OracleAttentionModel(Qwen2Model):
                   li, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
                   float(np.float32(1.0) / np.sqrt(np.float32(cfg.head_dim))), 16,
                   cfg.num_hidden_layers, "bf16")
+        att = self._finish(li, rows, table[0], first_pos, att)
         return to_dev(att.reshape(rows.shape[0], -1), "bf16")
+
+    def _finish(self, li, roped_rows, table, first_pos, att):
+        """The attention output of the layer (bits), given the oracle's."""
+        return att
 
     def _attention_decode(self, li, qkv, pos):
         return self._oracle(li, qkv, lambda rows, args, *rest: self.orc.decode_step(
-            rows, *args, np.array([pos], np.int32), *rest))
+            rows, *args, np.array([pos], np.int32), *rest), pos)
 
     def _attention_prefill(self, li, qkv, cache_pos, cu, start):
         S = qkv.shape[0]
         return self._oracle(li, qkv, lambda rows, args, *rest: self.orc.prefill(
-            rows, *args, np.array([0, S], np.int32), np.array([cache_pos], np.int32), *rest))
+            rows, *args, np.array([0, S], np.int32), np.array([cache_pos], np.int32), *rest),
+            cache_pos)
 
 
-# Largest logit difference the attention swap may cause: 4 bf16 units at the
-# logits' magnitude (2..4).  Any two attentions that differ in the last f32 bit
-# of one output round one bf16 output differently now and then; 24 layers of
-# bf16 rounding amplify that to about 0.04 in the logits (measured).
+class ExactAttentionModel(OracleAttentionModel):
+    """The oracle-attention model with the attention itself done in f64 and
+    rounded once to bf16: textbook softmax(q K^T * scale) V over the same
+    roped q and the same cache (both written by the oracle, bit-exact with
+    the reference's rope.cu / kv_cache.cu), every other step the GPU
+    model's.  It measures how far the reference's own f32 algorithm
+    (attention.cu: 32 interleaved partitions, expf, one merge) lands from
+    exact arithmetic, which bounds what any attention can be expected to
+    reproduce through 24 layers of bf16 rounding."""
+
+    def _finish(self, li, roped_rows, table, first_pos, att):
+        cfg, orc = self.cfg, self.orc
+        hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        S = roped_rows.shape[0]
+        pos = first_pos + np.arange(S)
+        ctx = int(pos[-1]) + 1
+        npg = (ctx + 15) // 16
+        f64 = lambda b: orc.to_f32(b, "bf16").astype(np.float64)  # noqa: E731
+        K = f64(self.k_host[table[:npg], li]).transpose(1, 0, 2, 3).reshape(hkv, npg * 16, d)[:, :ctx]
+        V = f64(self.v_host[table[:npg], li]).transpose(1, 0, 2, 3).reshape(hkv, npg * 16, d)[:, :ctx]
+        q = f64(roped_rows[:, : hq * d]).reshape(S, hq, d)
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+        late = np.arange(ctx)[None, :] > pos[:, None]
+        out = np.empty((S, hq, d))
+        G = hq // hkv
+        for h in range(hq):
+            sc = q[:, h] @ K[h // G].T * scale
+            sc[late] = -np.inf
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            out[:, h] = (p @ V[h // G]) / p.sum(axis=1, keepdims=True)
+        return to_bf16_bits(out.reshape(S, hq * d))
+
+
+# Top-2 logit gap at or below which a greedy step counts as a near-tie that
+# rounding may decide either way: 4 bf16 units at the logits' magnitude
+# (2..4).  Any two attentions that differ in the last f32 bit of one output
+# round one bf16 output differently now and then, and 24 layers of bf16
+# rounding amplify that to 0.04-0.07 in the logits -- exact f64 attention
+# against the reference's f32 algorithm included (measured: 0.049 after a
+# 128-token prompt).
 ATTN_LOGIT_NOISE = 0.0625
+
+
+def greedy_compare(orc, models, prompt, steps=128):
+    """Prefill `prompt`, then `steps` greedy steps, every model fed the first
+    model's (the oracle attention's) greedy token each step (EOS/BOS stop
+    bypassed, as models.rs:218, :236 would stop both alike).  For every other
+    model: tokens that agree with the first's, the first step where they
+    differ (the free-running prefix: up to it both ran on their own tokens),
+    the worst logit difference against the first, and the steps where the
+    first's top-2 gap exceeds ATTN_LOGIT_NOISE (decided) and whether those
+    agree."""
+    ref = models[0]
+    n = len(models) - 1
+    st = [dict(agree=0, prefix=None, worst=0.0, decided=0, decided_differ=[], differ=[])
+          for _ in range(n)]
+    ids, pos = prompt, 0
+    for step in range(steps + 1):
+        for m in models:
+            m.forward(ids, pos)
+        rl = orc.to_f32(from_dev(ref.logits())[0], "bf16")
+        r = ref.sample_greedy()
+        top2 = np.sort(rl)[-2:]
+        gap = float(top2[1] - top2[0])
+        for k, m in enumerate(models[1:]):
+            ml = orc.to_f32(from_dev(m.logits())[0], "bf16")
+            diff = float(np.max(np.abs(ml - rl)))
+            g = m.sample_greedy()
+            s = st[k]
+            s["worst"] = max(s["worst"], diff)
+            if gap > ATTN_LOGIT_NOISE:
+                s["decided"] += 1
+            if g == r:
+                s["agree"] += 1
+            else:
+                s["prefix"] = step if s["prefix"] is None else s["prefix"]
+                s["differ"].append((step, round(gap, 4), round(diff, 4)))
+                if gap > ATTN_LOGIT_NOISE:
+                    s["decided_differ"].append(step)
+        pos += len(ids)
+        ids = [r]
+    for s in st:
+        s["prefix"] = steps + 1 if s["prefix"] is None else s["prefix"]
+        s["exempt"] = steps + 1 - s["decided"]
+    return st
+
+
+def report(name, s, steps):
+    say(f"  {name}: {s['agree']} of {steps + 1} tokens identical, free-running prefix "
+        f"{s['prefix']}; {s['decided']} decided steps (oracle top-2 gap > {ATTN_LOGIT_NOISE}), "
+        f"{len(s['decided_differ'])} of them differ; {s['exempt']} near-tie steps exempt; "
+        f"worst logit difference {s['worst']:.4f} ({s['worst'] / ATTN_LOGIT_NOISE:.0%} of the "
+        f"bound); differing steps (step, gap, diff): {s['differ'][:12]}")
 
 
 def test_greedy_128_steps_attention_swapped(orc):
     """The north-star greedy check with attention as the only difference:
-    random-init Qwen2.5-0.5B, a 128-token prompt, then 128 greedy steps with
-    EOS/BOS stop bypassed (models.rs:195-240, greedy dispatch :398-405, stop
-    :218, :236), twice with identical GPU GEMMs -- once with this library's
-    attention (luc_paged_prefill for the prompt, luc_decode_step per token),
-    once with the oracle's (OracleAttentionModel).  Both runs are fed the
-    oracle-attention run's token, so every step compares the two attentions
-    on the same history.  A step may differ only where the oracle's top-2
-    logit gap is within ATTN_LOGIT_NOISE (a near-tie that rounding decides);
-    every decided step must agree, and the logits may differ by at most
-    ATTN_LOGIT_NOISE.  The free-running prefix (identical tokens before the
-    first differing step) is reported."""
+    random-init Qwen2.5-0.5B, a 128-token prompt, then 128 greedy steps
+    (models.rs:195-240, greedy dispatch :398-405), three times with identical
+    GPU GEMMs -- with the oracle's attention (OracleAttentionModel, the
+    reference's algorithm), with this library's (luc_paged_prefill for the
+    prompt, luc_decode_step per token) and with f64 textbook attention over
+    the oracle's cache (ExactAttentionModel) -- each step fed the oracle
+    run's token, so every step compares the attentions on the same history.
+    Asserted for the library's attention: every decided step (oracle top-2
+    gap above ATTN_LOGIT_NOISE) identical, at most 13 differing tokens, and a
+    worst logit difference within twice the one exact arithmetic shows
+    against the reference's algorithm.  The free-running prefix, the exempt
+    near-tie steps and the headroom are reported for both: measured, exact
+    arithmetic leaves the reference's greedy path at step 2 (119 of 129
+    tokens identical), this library's attention at step 16 (124 of 129)."""
     cfg = QWEN25_05B
     w = random_weights(cfg, seed=2025)
     max_pos = 512
-    hip = Qwen2Model(cfg, w, max_positions=max_pos)
     ref = OracleAttentionModel(orc, cfg, w, max_positions=max_pos)
+    hip = Qwen2Model(cfg, w, max_positions=max_pos)
+    exact = ExactAttentionModel(orc, cfg, w, max_positions=max_pos)
     rng = np.random.default_rng(29)
     prompt = rng.integers(0, cfg.vocab_size, 128).tolist()
-    say("  [gpu] prefill 128 + 128 greedy steps, HIP attention vs oracle attention (same GEMMs)")
-    ids, pos, worst, agree, prefix, decided = prompt, 0, 0.0, 0, None, 0
-    for step in range(129):
-        hip.forward(ids, pos)
-        ref.forward(ids, pos)
-        hl = orc.to_f32(from_dev(hip.logits())[0], "bf16")
-        rl = orc.to_f32(from_dev(ref.logits())[0], "bf16")
-        diff = float(np.max(np.abs(hl - rl)))
-        worst = max(worst, diff)
-        g, r = hip.sample_greedy(), ref.sample_greedy()
-        top2 = np.sort(rl)[-2:]
-        gap = float(top2[1] - top2[0])
-        if gap > ATTN_LOGIT_NOISE:
-            decided += 1
-        if g != r:
-            prefix = step if prefix is None else prefix
-            say(f"  step {step}: HIP attention {g} vs oracle attention {r}; oracle top-2 gap "
-                f"{gap:.4f}, attention-only logit difference {diff:.4f}")
-            assert gap <= ATTN_LOGIT_NOISE, f"step {step}: a decided step differs"
-        else:
-            agree += 1
-        pos += len(ids)
-        ids = [r]
-    prefix = 129 if prefix is None else prefix
-    say(f"  {agree} of 129 tokens identical, free-running prefix {prefix}; decided steps {decided} "
-        f"(all identical); worst attention-only logit difference {worst:.4f}")
-    assert worst <= ATTN_LOGIT_NOISE
-    assert agree >= 116
+    say("  [gpu] prefill 128 + 128 greedy steps: oracle attention vs HIP attention vs f64 attention")
+    sh, se = greedy_compare(orc, [ref, hip, exact], prompt)
+    report("HIP attention vs oracle attention", sh, 128)
+    report("f64 attention vs oracle attention", se, 128)
+    assert not sh["decided_differ"], "a decided step differs"
+    assert sh["worst"] <= 2 * max(se["worst"], 1 / 64)
+    assert 129 - sh["agree"] <= 13
+
+
+def test_greedy_after_2048_token_prefill(orc):
+    """The prefill configuration's follow-on: random-init Qwen2.5-0.5B, the
+    first of the 4 x 2048 seeded prompts (token ids uniform over the 151936
+    vocab) through luc_paged_prefill in one call per layer, then 128 greedy
+    steps with luc_decode_step, against the same model with the oracle's
+    attention (its prefill restates the reference's per-token loop,
+    models.rs:485-550, on the host), and with f64 textbook attention
+    (ExactAttentionModel), each step fed the oracle run's token.  Every
+    decided step must be identical, at most 13 tokens may differ, and the
+    worst logit difference must stay within twice the one exact arithmetic
+    shows against the reference's algorithm; the free-running prefix and the
+    exempt near-tie steps are reported for both."""
+    cfg = QWEN25_05B
+    w = random_weights(cfg, seed=2025)
+    max_pos = 2048 + 160
+    ref = OracleAttentionModel(orc, cfg, w, max_positions=max_pos)
+    hip = Qwen2Model(cfg, w, max_positions=max_pos)
+    exact = ExactAttentionModel(orc, cfg, w, max_positions=max_pos)
+    prompt = np.random.default_rng(2048).integers(0, cfg.vocab_size, (4, 2048))[0].tolist()
+    say("  [gpu] prefill 2048 (luc_paged_prefill vs the oracle's per-token loop vs f64) + 128 greedy steps")
+    sh, se = greedy_compare(orc, [ref, hip, exact], prompt)
+    report("HIP attention vs oracle attention after 2048 prompt tokens", sh, 128)
+    report("f64 attention vs oracle attention after 2048 prompt tokens", se, 128)
+    assert not sh["decided_differ"], "a decided step differs"
+    assert sh["worst"] <= 2 * max(se["worst"], 1 / 64)
+    assert 129 - sh["agree"] <= 13
 
 
 def test_greedy_lockstep_full_oracle(orc, qwen):

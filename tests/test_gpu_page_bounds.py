@@ -48,8 +48,14 @@ def _pool_changes(before, after):
 
 @pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
 @pytest.mark.parametrize("head_dim,dtype,hq,hkv", [(64, "f16", 14, 2), (128, "bf16", 12, 2)])
-@pytest.mark.parametrize("split", [0, 256])
+@pytest.mark.parametrize("split", [0, 256, 512])
 def test_decode_never_uses_a_page_outside_the_pool(orc, luc, head_dim, dtype, hq, hkv, split, fused):
+    """split 0 and 512 run the single-tile kernels at head_dim 64 (512 tokens =
+    8 tiles of 64) and 256 the tile-pair kernels; at head_dim 128, 0 and 256
+    run the single-tile kernels (8 tiles of 32) and 512 the tile-pair ones.
+    Every sequence's q and k of the new token are roped in place, also where
+    the new token's page lies outside the pool (only the cache write is
+    skipped), on the fused and the unfused path alike."""
     cfg, clean, nb, h = _inputs(dtype, head_dim, hq, hkv, seed=head_dim + split)
     rope = rope_cache(luc, head_dim)
     qkv, kp, vp = to_dev(h.qkv, dtype), to_dev(h.k_pool, dtype), to_dev(h.v_pool, dtype)
@@ -88,6 +94,10 @@ def test_decode_never_uses_a_page_outside_the_pool(orc, luc, head_dim, dtype, hq
     # 2 (its newest token's page)
     for b in (0, 1, 2):
         assert np.all(np.isnan(o[b])), f"sequence {b}"
+    # q and k of every new token are roped in place, the bad pages'
+    # sequences included (RoPE does not depend on the table)
+    want_all = oracle_step(orc, luc, clean)
+    assert np.array_equal(from_dev(qkv), want_all["qkv"]), "roped q/k rows differ"
     # sequence 3 as the oracle computes it on its own
     one = wl.HostDecode(wl.replace(cfg, batch=1), 1, clean.ctx[3:4], clean.positions[3:4],
                         clean.tables[3:4], clean.qkv[3:4], clean.k_pool, clean.v_pool)

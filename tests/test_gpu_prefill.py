@@ -8,7 +8,7 @@ import torch
 
 from lucciola_rs_amd import workloads as wl
 from lucciola_rs_amd.engine import sm_scale
-from gpu_util import TOL, from_dev, max_abs, rope_cache, say, to_dev
+from gpu_util import TOL, from_dev, max_abs, rope_cache, say, to_dev, ulp_gate
 
 pytestmark = pytest.mark.gpu
 
@@ -56,7 +56,11 @@ def oracle_prefill(orc, luc, h: wl.HostPrefill, layer=0, bias=None):
     return dict(out=out, qkv=qkv, k_pool=kp, v_pool=vp)
 
 
-def assert_prefill_matches(orc, got, want, dtype):
+def assert_prefill_matches(orc, got, want, dtype, max_frac=0.5):
+    """Bit-exact roped q/k and cache; attention outputs within the north-star
+    max-abs tolerance and within 4 storage units of the oracle's at the row's
+    scale (ulp_gate: measured at most ~2.5), with at most `max_frac` of the
+    elements differing at all (measured 18-43%)."""
     assert np.array_equal(got["qkv"], want["qkv"]), "RoPE'd q/k differ"
     assert np.array_equal(got["k_pool"], want["k_pool"]), "K pool differs"
     assert np.array_equal(got["v_pool"], want["v_pool"]), "V pool differs"
@@ -65,6 +69,7 @@ def assert_prefill_matches(orc, got, want, dtype):
     err = max_abs(orc, got["out"], want["out"], dtype)
     say(f"  max|hip - oracle| = {err:.3e} (tol {TOL[dtype]})")
     assert err <= TOL[dtype]
+    ulp_gate(orc, got["out"], want["out"], dtype, max_ulps=4, max_frac=max_frac)
 
 
 SHAPES = [(14, 2, 64), (12, 2, 128), (28, 4, 128)]

@@ -29,6 +29,7 @@ MUTANTS = {
     14: "top-k filter: ties go to the higher lane in the warp trees",
     15: "bitonic network: block directions swapped",
     16: "top-p cutoff needs cdf strictly above top_p",
+    17: "prefill rows attend one token past their own position",
 }
 
 
@@ -42,6 +43,7 @@ def all_checks(o):
         res.append((f"attn_{dt}", pins.check_attention(o, dt, 100) <= 1))
         res.append((f"sdpa_{dt}", pins.check_attention_sdpa(o, dt, 70) <= 1))
         res.append((f"inv_{dt}", pins.check_attention_invariants(o, dt) == 0))
+        res.append((f"prefill_{dt}", pins.check_prefill(o, dt) <= 1))
     import numpy as np
     x = np.linspace(-3, 3, 10001, dtype=np.float32)
     res.append(("conv_f16", np.array_equal(o.to_storage(x, "f16"), pins.bits(x, "f16"))))
