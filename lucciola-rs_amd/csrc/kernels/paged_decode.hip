@@ -95,6 +95,47 @@ struct DecodeGeo {
 
 constexpr int kCpolNT = 2;  // non-temporal load: the KV stream is read once per step
 
+// Byte offset of V[t][d .. d + 3] (d a multiple of 4) of a tile in LDS, for
+// the transposing PV reads: 512-byte blocks of 8 tokens x 32 dims, block
+// (t / 8, d / 32) at ((t / 8) * (D / 32) + d / 32) * 512, inside it token
+// row (t + rot * (d / 32)) % 8 of 64 bytes, 8 bytes per 4 dims.  One
+// transposing read (8 tokens x 32 dims) then covers one block, 256
+// contiguous bytes per 32 lanes; the rotation by rot = 16 / (D / 8) rows per
+// 32-dim block spreads the rows one 16-lane group of a 16-byte write touches
+// (16 lanes x 16 bytes from load layout) over the whole bank row.
+template <int D>
+__device__ __host__ inline int vslot(int t, int d) {
+  constexpr int NUB = D / 32, ROT = 16 / (D / 8);
+  const int ub = d >> 5;
+  return ((t >> 3) * NUB + ub) * 512 + (((t + ROT * ub) & 7) << 6) + (((d & 31) >> 2) << 3);
+}
+
+// XOR key of the 16-byte slots of token row t of a K tile in LDS (slot s of
+// the row holds chunk s ^ key): the 16 rows one 16-lane group of the score
+// reads touches (tokens 16i .. 16i + 15 of a 32-token block, one chunk each)
+// fall on 16 different 16-byte bank groups of the 256-byte bank row.  A
+// head_dim 64 row is half a bank row, so rows t and t + 8 (the same half)
+// need different keys: (t >> 1) & 7.  A head_dim 128 row is a whole bank
+// row: t & 7.
+template <int D>
+__device__ __host__ inline int kswz(int t) {
+  return D == 64 ? (t >> 1) & 7 : t & 7;
+}
+
+// Row pitches (in elements) of per-head rows in LDS that lanes of different
+// heads read together: padded so that the rows of the G <= 8 heads start on
+// different banks (the unpadded rows, 128 or 256 bytes apart, put heads
+// 0, 2, 4, 6 on the same banks).  p of a tile, head-major (16-bit, TILE
+// tokens a row), 16 bytes of padding: row g starts at bank 36 g or 20 g
+// (mod 64); the merge records' o (f32, D a row), 32 bytes: bank 8 g; the
+// step variant's roped q (16-bit, D a row): bank 36 g (D = 64) or 8 g.
+template <int TILE>
+constexpr int kPPitch = TILE + 8;
+template <int D>
+constexpr int kRecPitch = D + 8;
+template <int D>
+constexpr int kQPitch = D + (D == 64 ? 8 : 16);
+
 // Wait until at most N vector memory operations of this wave are in flight.
 // They complete in issue order, so this also covers the LDS writes of
 // global_load_lds, which the compiler does not track.
@@ -215,10 +256,70 @@ __device__ inline uint16_t p_bits(float p) {
   else return (uint16_t)(__float_as_uint(p) >> 16);
 }
 
-// 16 bytes to LDS byte address a (asm: a compiler-visible LDS store would
-// wait for every outstanding direct-to-LDS load of the wave).
-__device__ inline void lds_write16(uint32_t a, uint4 v) {
-  asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(__builtin_bit_cast(u32x4_t, v)) : "memory");
+// The eight 16-byte rows of a tile held in load layout, load r to a0 + r KB
+// (r even) or a1 + (r - 1) KB (r odd), in one asm block (the compiler sees no store to
+// LDS, which would make it wait for the outstanding direct-to-LDS loads); the
+// closing s_nop keeps the data registers of the last write from being
+// overwritten by the instructions that follow.
+__device__ inline void lds_write_tile(uint32_t a0, uint32_t a1, const uint4 (&v)[8]) {
+  asm volatile(
+      "ds_write_b128 %0, %2\n\t"
+      "ds_write_b128 %1, %3\n\t"
+      "ds_write_b128 %0, %4 offset:2048\n\t"
+      "ds_write_b128 %1, %5 offset:2048\n\t"
+      "ds_write_b128 %0, %6 offset:4096\n\t"
+      "ds_write_b128 %1, %7 offset:4096\n\t"
+      "ds_write_b128 %0, %8 offset:6144\n\t"
+      "ds_write_b128 %1, %9 offset:6144\n\t"
+      "s_nop 1" ::"v"(a0), "v"(a1), "v"(__builtin_bit_cast(u32x4_t, v[0])),
+      "v"(__builtin_bit_cast(u32x4_t, v[1])), "v"(__builtin_bit_cast(u32x4_t, v[2])),
+      "v"(__builtin_bit_cast(u32x4_t, v[3])), "v"(__builtin_bit_cast(u32x4_t, v[4])),
+      "v"(__builtin_bit_cast(u32x4_t, v[5])), "v"(__builtin_bit_cast(u32x4_t, v[6])),
+      "v"(__builtin_bit_cast(u32x4_t, v[7]))
+      : "memory");
+}
+
+// Values written by asm loads issued earlier (not yet known to have landed):
+// after the wait for them, pass each through an empty asm so that every use
+// comes after that wait.
+template <int N>
+__device__ inline void pin_regs(uint4 (&x)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    u32x4_t v = __builtin_bit_cast(u32x4_t, x[i]);
+    asm volatile("" : "+v"(v));
+    x[i] = __builtin_bit_cast(uint4, v);
+  }
+}
+
+// Issue (no wait) one transposing 8-byte LDS read at a + OFF: the result is
+// not valid until lds_wait_pin has waited for it.
+template <int OFF>
+__device__ inline uint2 lds_tr_issue(uint32_t a) {
+  uint2 x;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(x) : "v"(a), "n"(OFF) : "memory");
+  return x;
+}
+// Issue (no wait) an 8-byte LDS read at a + OFF.
+template <int OFF>
+__device__ inline uint2 lds_read8_issue(uint32_t a) {
+  uint2 x;
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(x) : "v"(a), "n"(OFF) : "memory");
+  return x;
+}
+// Wait for every LDS access of the wave; the "+v" operands keep each use of
+// the values read behind the wait.
+__device__ inline void lds_wait_pin(uint2 (&x)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]),
+                 "+v"(x[7])
+               :
+               : "memory");
+}
+__device__ inline void lds_pin(uint2 (&x)[8]) {
+  asm volatile(""
+               : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]),
+                 "+v"(x[7]));
 }
 
 // x[i] for a wave-uniform runtime i < N, without indexing a register array.
@@ -336,7 +437,8 @@ __device__ void qk_writeback(const DecodeArgs& A, int b, int h, const uint16_t* 
   uint32_t* qrow = (uint32_t*)(A.q + (int64_t)b * A.q_stride + (int64_t)h * G * D);
   uint32_t* krow = (uint32_t*)(A.k_new + (int64_t)b * A.q_stride + (int64_t)h * D);
   for (int i = threadIdx.x; i < QW + D / 2; i += NT) {
-    if (i < QW) qrow[i] = ((const uint32_t*)sq)[i];
+    // (sq holds head g's row at g * kQPitch<D> elements)
+    if (i < QW) qrow[i] = ((const uint32_t*)sq)[(i / (D / 2)) * (kQPitch<D> / 2) + i % (D / 2)];
     else krow[i - QW] = ((const uint32_t*)sk)[i - QW];
   }
 }
@@ -363,8 +465,8 @@ __device__ __attribute__((always_inline)) inline void finish_split(
   constexpr int NV = 8 * G;  // o values per lane: 8 dims x G heads
   constexpr int CH = D / 8;  // 16-byte chunks per token row
   constexpr int NVP = (NV / 4 + 3) / 4 * 4;
-  // MPV: the record holds o head-major (o[g][d] at g * D + d), then m and l
-  constexpr int REC_ML = MPV ? GD : 4 * CH * NVP;
+  // MPV: the record holds o head-major (o[g][d] at g * kRecPitch<D> + d), then m and l
+  constexpr int REC_ML = MPV ? G * kRecPitch<D> : 4 * CH * NVP;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int pv_ch = lane % CH;
@@ -382,7 +484,7 @@ __device__ __attribute__((always_inline)) inline void finish_split(
       for (int db = 0; db < NA; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          *(float4*)(recw + hh * D + 32 * db + 8 * i + 4 * (lane >> 5)) =
+          *(float4*)(recw + hh * kRecPitch<D> + 32 * db + 8 * i + 4 * (lane >> 5)) =
               make_float4(oacc[db][4 * i], oacc[db][4 * i + 1], oacc[db][4 * i + 2], oacc[db][4 * i + 3]);
     }
   } else {
@@ -431,7 +533,7 @@ __device__ __attribute__((always_inline)) inline void finish_split(
   for (int e = threadIdx.x; e < GD; e += 64 * W) {
     const int g = e / D, d = e % D;
     const int val = g * 8 + d % 8;  // the value's index in the reduce-scatter
-    const int idx = MPV ? e : ((val / (NV / 4)) * CH + d / 8) * NVP + val % (NV / 4);
+    const int idx = MPV ? g * kRecPitch<D> + d : ((val / (NV / 4)) * CH + d / 8) * NVP + val % (NV / 4);
     float mw[W], M = -INFINITY;
 #pragma unroll
     for (int v = 0; v < W; ++v) {
@@ -507,7 +609,10 @@ __device__ __attribute__((always_inline)) inline void finish_split(
 template <int DT, int D, int G, bool APPEND, int W, int NB>
 __device__ void decode_impl(const DecodeArgs& A) {
   using S = DecodeGeo<D>;
-  constexpr int PWORDS = S::HALF * 8;  // p exchange, 32-bit words: G pairs per token pair
+  constexpr int PP = kPPitch<S::TILE>;  // head-major p row pitch (elements)
+  // p exchange, 32-bit words: G pairs per token pair (dot2 form), or G
+  // head-major rows of PP 16-bit values (MPV)
+  constexpr int PWORDS = S::HALF * 8 > (G * PP + 1) / 2 ? S::HALF * 8 : (G * PP + 1) / 2;
   constexpr int HD = D / 2;
   constexpr int GD = G * D;
   constexpr int NV = 8 * G;  // o values per lane: 8 dims x G heads
@@ -556,15 +661,17 @@ __device__ void decode_impl(const DecodeArgs& A) {
   constexpr int NVP = (NV / 4 + 3) / 4 * 4;
   constexpr int REC_ML = 4 * S::CH * NVP;
   static_assert(REC_ML + 2 * G <= S::KBYTES / 4, "merge record fits a K buffer");
-  static_assert(GD + 2 * G <= S::KBYTES / 4, "head-major merge record fits a K buffer");
-  static_assert(G * S::TILE * 2 <= PWORDS * 4, "p of the tile, head-major, fits the p exchange");
+  static_assert(G * kRecPitch<D> + 2 * G <= S::KBYTES / 4, "head-major merge record fits a K buffer");
+  static_assert(G * PP * 2 <= PWORDS * 4, "p of the tile, head-major, fits the p exchange");
   __shared__ __attribute__((aligned(16))) char s_k[W][NB][S::KBYTES];
   __shared__ __attribute__((aligned(16))) uint32_t s_p[W][PWORDS];
   constexpr int NOP = (APPEND && !FASTA) ? W : 1;  // copies of the step operands
-  __shared__ __attribute__((aligned(16))) uint16_t s_q[NOP][APPEND ? GD : 8];
+  constexpr int QP = kQPitch<D>;  // s_q / s_qr row pitch (elements)
+  constexpr int NQL = (G * QP * 2 + 255) / 256;  // 4-byte direct-to-LDS loads of q, padded rows
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[NOP][APPEND ? G * QP : 8];
+  __shared__ __attribute__((aligned(16))) char s_qr[FASTQ ? W : 1][FASTQ ? NQL * 256 : 16];
   __shared__ __attribute__((aligned(16))) uint16_t s_knew[NOP][APPEND ? D : 8];
   __shared__ __attribute__((aligned(16))) uint16_t s_vnew[NOP][APPEND ? D : 8];
-  __shared__ __attribute__((aligned(16))) char s_qr[FASTQ ? W : 1][FASTQ ? NQ * 256 : 16];
   __shared__ __attribute__((aligned(16))) char s_pa[1][FASTA ? PBYTES : 16];
   static_assert((G * 256 + G) * 4 <= W * NB * S::KBYTES, "merge weights fit the K buffers");
 
@@ -590,9 +697,9 @@ __device__ void decode_impl(const DecodeArgs& A) {
   const int tab1 = !T1 && ST > 64 * kPage ? trow[min(p0 + 64 + lane, tmax)] : 0;
   // The A operand of k-step ks, q[head lane % 32][16 ks + 8 (lane / 32)
   // .. + 8] of a row of the G heads' q (4-byte aligned); zero past head G - 1.
-  auto q_operand = [&](const uint16_t* row, int ks) {
+  auto q_operand = [&](const uint16_t* row, int ks, int pitch = D) {
     const int g = lane & 31;
-    const uint32_t* p = (const uint32_t*)(row + min(g, G - 1) * D + 16 * ks + 8 * (lane >> 5));
+    const uint32_t* p = (const uint32_t*)(row + min(g, G - 1) * pitch + 16 * ks + 8 * (lane >> 5));
     const uint4 v = make_uint4(p[0], p[1], p[2], p[3]);
     return g < G ? v : make_uint4(0, 0, 0, 0);
   };
@@ -717,7 +824,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   // page r / LPP at + (r % LPP) * 1KB; the K slot pv_ch of token tl holds
   // chunk pv_ch ^ (tl & 7), where tl & 7 only depends on the parity of r.
   auto k_lane_off = [&](int parity) -> uint32_t {
-    const int sw = (S::TPL == 8) ? pv_tok : ((parity * S::TPL + pv_tok) & 7);
+    const int sw = kswz<D>(parity * S::TPL + pv_tok);
     return (uint32_t)(pv_tok * S::ROWB + ((pv_ch ^ sw) << 4));
   };
   const uint32_t koff0 = k_lane_off(0), koff1 = k_lane_off(1);
@@ -727,7 +834,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
   // (into vr).  Pages past the split re-read the split's last page (a cache
   // hit), which keeps the number of loads per tile fixed at 8 + 8; a tile
   // that starts past the split (the odd tile of a pair) is all such pages.
-  // In the single-tile kernel q follows the K loads (NQ more loads).
+  // In the single-tile kernel q follows the K loads (NQL more loads).
   auto phys_of = [&](int t0, int r) __attribute__((always_inline)) -> int64_t {
     if constexpr (T1) return tpage[r / S::LPP];  // (t0 is the wave's only tile)
     else return page_of(min((t0 - s_begin) / kPage + r / S::LPP, jend));
@@ -777,9 +884,15 @@ __device__ void decode_impl(const DecodeArgs& A) {
             (r % S::LPP) * 1024);
     }
     if constexpr (FASTQ) {
+      // q by 4-byte direct-to-LDS loads into head rows QP elements apart
+      // (padded: the A-operand reads of different heads then fall on
+      // different banks); the padding words re-read the row's start
 #pragma unroll
-      for (int i = 0; i < NQ; ++i)
-        dma4((const char*)qrow + min(i * 256 + lane * 4, GD * 2 - 4), (lds_char*)s_qr[w] + i * 256);
+      for (int i = 0; i < NQL; ++i) {
+        const int o = i * 256 + lane * 4;  // LDS byte of the padded block
+        const int g = min(o / (QP * 2), G - 1), ob = o % (QP * 2);
+        dma4((const char*)qrow + g * D * 2 + (ob < D * 2 ? ob : 0), (lds_char*)s_qr[w] + i * 256);
+      }
     }
   };
   auto issue_v = [&](int t0, uint4(&vr)[S::LOADS]) __attribute__((always_inline)) {
@@ -833,7 +946,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
         const int g = idx / HD, j = idx % HD;
         uint16_t o1, o2;
         rot_pair<DT>(rx1[i], rb1[i], rx2[i], rb2[i], rc[i], rs[i], o1, o2);
-        uint16_t* dst = g < G ? s_q[qi] + g * D : s_knew[qi];
+        uint16_t* dst = g < G ? s_q[qi] + g * QP : s_knew[qi];
         dst[j] = o1;
         dst[j + HD] = o2;
       }
@@ -843,7 +956,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       s_vnew[qi][lane + 64 * i] = St<DT>::store(St<DT>::load(rv[i]) + St<DT>::load(rvb[i]));
     wave_lds_sync();
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qm[ks] = q_operand(s_q[qi], ks);
+    for (int ks = 0; ks < KS; ++ks) qm[ks] = q_operand(s_q[qi], ks, QP);
   }
 
   float m_run[G], l_lane[G], o[MPV ? 1 : G][8];
@@ -870,7 +983,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       if (owns && pos >= t0 && pos < t0 + S::TILE && lane < S::CH) {
         const int t = pos - t0;  // the new token's K row (swizzled slots)
         *(uint4*)(kb + t * S::ROWB + lane * 16) =
-            *(const uint4*)(s_knew[qi] + ((lane ^ (t & 7)) * 8));
+            *(const uint4*)(s_knew[qi] + ((lane ^ kswz<D>(t)) * 8));
       }
       wave_lds_sync();
     }
@@ -887,7 +1000,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       sc[nb] = f32x16{};
       const int tok = nb * 32 + (lane & 31);
       const uint32_t kr = lds_addr(kb) + tok * S::ROWB;
-      const int sw = tok & 7;
+      const int sw = kswz<D>(tok);
       auto kaddr = [&](int ks) { return kr + ((uint32_t)((2 * ks + (lane >> 5)) ^ sw) << 4); };
 #pragma unroll
       for (int k4 = 0; k4 < KS; k4 += 4) {
@@ -954,7 +1067,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       uint16_t* const sp16 = (uint16_t*)sp;
       if (qh == 0) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) sp16[g * S::TILE + tq] = p_bits<DT>(p[g]);
+        for (int g = 0; g < G; ++g) sp16[g * PP + tq] = p_bits<DT>(p[g]);
       }
     } else {
       // p to the load layout through LDS
@@ -984,33 +1097,73 @@ __device__ void decode_impl(const DecodeArgs& A) {
     const bool partial = t0 + S::TILE > s_end;
     if constexpr (MPV) {
       // V into the tile's K buffer (free: the scores have read it), in K's
-      // layout: chunk c of token t at slot c ^ (t & 7)
+      // layout: chunk c of token t at slot c ^ (t & 7).  Load r holds token
+      // r * TPL + pv_tok, so the slot's address is a per-lane base (one per
+      // parity of r when a load holds 4 tokens) plus r KB.  Tokens past the
+      // split (only in a split's last tile: a wave-uniform branch) are zeroed
+      // first.
       const uint32_t vbase = lds_addr(s_k[w][buf]);
+      if (partial) {
 #pragma unroll
-      for (int r = 0; r < S::LOADS; ++r) {
-        const int t = r * S::TPL + pv_tok;
-        const uint4 v = partial && t0 + t >= s_end ? make_uint4(0, 0, 0, 0) : vr[r];
-        lds_write16(vbase + t * S::ROWB + ((pv_ch ^ (t & 7)) << 4), v);
+        for (int r = 0; r < S::LOADS; ++r)
+          if (t0 + r * S::TPL + pv_tok >= s_end) vr[r] = make_uint4(0, 0, 0, 0);
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      uint32_t vlane[2];
+#pragma unroll
+      for (int par = 0; par < 2; ++par)
+        vlane[par] = vbase + vslot<D>(par * S::TPL + pv_tok, 8 * pv_ch);
+      lds_write_tile(vlane[0], vlane[1], vr);
       // O^T += V^T P^T per 16-token step c: A = V^T by transposing reads
       // (lane: dim 32 db + lane % 32, tokens 16c + 4(lane / 32) + 0..3 and
-      // + 8 + ...), B = P^T (lane: head lane % 32, the same tokens)
+      // + 8 + ...), B = P^T (lane: head lane % 32, the same tokens).  Every
+      // operand of the tile is read before one wait (the V writes above
+      // complete first: LDS accesses of a wave are performed in order).
+      constexpr int NC = S::TILE / 16;
+      static_assert(NC * ND == 8, "eight (step, dim block) operands per tile");
       const int hh = lane & 31, gs = lane >> 5;
-      const uint16_t* const pt = (const uint16_t*)s_p[w] + min(hh, G - 1) * S::TILE + 4 * gs;
+      const uint32_t pt = lds_addr((const uint16_t*)s_p[w] + min(hh, G - 1) * PP + 4 * gs);
       const int tr = 4 * gs + ((lane & 15) >> 2);
       const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+      uint32_t vtr[ND];
 #pragma unroll
-      for (int c = 0; c < S::TILE / 16; ++c) {
-        const uint2 pa = *(const uint2*)(pt + 16 * c);
-        const uint2 pb2 = *(const uint2*)(pt + 16 * c + 8);
-        const uint4 pb = hh < G ? make_uint4(pa.x, pa.y, pb2.x, pb2.y) : make_uint4(0, 0, 0, 0);
+      for (int db = 0; db < ND; ++db)
+        vtr[db] = vbase + vslot<D>(tr, 32 * db + tr_d);
+      uint2 va0[8], va1[8], pa[NC], pb[NC];
+      const auto issue_step = [&](auto cc) __attribute__((always_inline)) {
+        constexpr int c = decltype(cc)::value;
+        pa[c] = lds_read8_issue<32 * c>(pt);
+        pb[c] = lds_read8_issue<32 * c + 16>(pt);
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
-          uint2 va[2];
-          lds_tr16x2<0, 8 * S::ROWB>(
-              vbase + (16 * c + tr) * S::ROWB + ((((32 * db + tr_d) / 8) ^ tr) << 4) + (tr_d % 8) * 2, va);
-          oacc[db] = mfma32<DT>(make_uint4(va[0].x, va[0].y, va[1].x, va[1].y), pb, oacc[db]);
+          va0[c * ND + db] = lds_tr_issue<16 * c * S::ROWB>(vtr[db]);
+          va1[c * ND + db] = lds_tr_issue<16 * c * S::ROWB + 8 * S::ROWB>(vtr[db]);
+        }
+      };
+      issue_step(std::integral_constant<int, 0>{});
+      issue_step(std::integral_constant<int, 1>{});
+      if constexpr (NC == 4) {
+        issue_step(std::integral_constant<int, 2>{});
+        issue_step(std::integral_constant<int, 3>{});
+      }
+      lds_wait_pin(va0);
+      lds_pin(va1);
+      uint2 pab[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) pab[c] = make_uint2(0u, 0u);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        pab[c] = pa[c];
+        pab[NC + c] = pb[c];
+      }
+      lds_pin(pab);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint4 pv = hh < G ? make_uint4(pab[c].x, pab[c].y, pab[NC + c].x, pab[NC + c].y)
+                                : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int db = 0; db < ND; ++db) {
+          const int i = c * ND + db;
+          oacc[db] = mfma32<DT>(make_uint4(va0[i].x, va0[i].y, va1[i].x, va1[i].y), pv, oacc[db]);
         }
       }
     } else {
@@ -1082,8 +1235,8 @@ __device__ void decode_impl(const DecodeArgs& A) {
             const uint32_t lo = (uint32_t)o1a | ((uint32_t)o1b << 16);
             const uint32_t hi = (uint32_t)o2a | ((uint32_t)o2b << 16);
             if (g < G) {  // (two stores with known targets: no alias with the loads into LDS)
-              *(uint32_t*)(s_q[qi] + g * D + j) = lo;
-              *(uint32_t*)(s_q[qi] + g * D + j + HD) = hi;
+              *(uint32_t*)(s_q[qi] + g * QP + j) = lo;
+              *(uint32_t*)(s_q[qi] + g * QP + j + HD) = hi;
             } else {
               *(uint32_t*)(s_knew[qi] + j) = lo;
               *(uint32_t*)(s_knew[qi] + j + HD) = hi;
@@ -1108,7 +1261,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       // the A operands from a q row in LDS (asm reads: compiler-visible
       // reads of LDS would wait for every outstanding load)
       auto q_operands_lds = [&](const void* row) __attribute__((always_inline)) {
-        const uint32_t qa = lds_addr(row) + (uint32_t)((min(lane & 31, G - 1) * D + 8 * (lane >> 5)) * 2);
+        const uint32_t qa = lds_addr(row) + (uint32_t)((min(lane & 31, G - 1) * QP + 8 * (lane >> 5)) * 2);
 #pragma unroll
         for (int k4 = 0; k4 < KS; k4 += 4) {
           uint4 x[4];
