@@ -23,11 +23,13 @@
 // stages (four at head_dim 64, three at 128): super-block J + NS - 2 loads
 // while super-block J is computed, and the waves meet at one barrier per
 // super-block.
-//   - K and V blocks [64 tokens][D] straight into LDS (global_load_lds_dwordx4,
-//     one wave-wide load = 1 KB of a page), each token row XOR-swizzled by
-//     16-byte chunk so the operand reads below do not collide.  Tokens past
-//     the context re-read the last valid token (finite), so their zero
-//     weights contribute exactly zero.
+//   - K and V blocks of 64 tokens straight into LDS (global_load_lds_dwordx4,
+//     one wave-wide load = 1 KB of a page, 8 tokens at head_dim 64, 4 of K or
+//     8 tokens x 64 dims of V at 128).  K rows are XOR-swizzled by 16-byte
+//     chunk and V is stored as 8-token x 32-dim sub-blocks, so that the
+//     operand reads below touch every LDS bank once per pass (kkey, vslot).
+//     Tokens past the context re-read the last valid token (finite), so their
+//     zero weights contribute exactly zero.
 //   - per wave, per 32-token half: S^T = K Q^T with v_mfma_f32_32x32x16 (A = K
 //     from LDS, B = Q^T held in registers for the whole kernel).  In the MFMA
 //     accumulator layout lane l holds q row l % 32 and 16 of the tile's
@@ -169,6 +171,24 @@ __device__ inline void lds_wait_v(u32x2_t* x) {
                : "memory");
 }
 
+// 16-byte chunk c of K token row t (within a block) sits at slot c ^ kkey(t):
+// the 16 rows that one pass of ds_read_b128 reads (a 16-byte chunk per lane)
+// then cover all 64 banks (head_dim 64: rows 2m, 2m + 1 share key m and lie
+// 128 bytes apart; head_dim 128: one row is 256 bytes, key t % 16).
+template <int D>
+__device__ constexpr int kkey(int t) {
+  return D == 64 ? (t >> 1) & 7 : t & 15;
+}
+// Byte offset of dims d .. d + 3 of V token t (within a block): 8-token x
+// 32-dim sub-blocks of 512 bytes, token rows of 64 bytes.  A transposing read
+// of tokens t0 .. t0 + 7 (t0 % 8 == 0), dims 32u .. 32u + 31 is one
+// sub-block, its 32-lane halves 256 contiguous bytes; token t + 8 is 16 D
+// bytes further, as in a row-major block.
+template <int D>
+__device__ constexpr uint32_t vslot(int t, int d) {
+  return ((t >> 3) * (D / 32) + (d >> 5)) * 512 + ((t & 7) << 6) + (((d & 31) >> 2) << 3);
+}
+
 // Waves per prefill workgroup for group size G (<= 8).
 constexpr int prefill_waves(int g) { return g <= 4 ? 4 : 8; }
 
@@ -189,9 +209,9 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   constexpr int TPL = 1024 / ROWB;       // tokens per 1 KB load
   constexpr int ND = D / 32;      // 32-dim output tiles
   constexpr int NK = D / 16;      // 16-dim k-steps of QK
-  // NS stages of K and V super-blocks, row-major, 16-byte chunk c of token t
-  // at slot c ^ (t & 7): super-block j is loaded NS - 2 stages before its
-  // scores
+  // NS stages of K and V super-blocks (K row-major, 16-byte chunk c of token
+  // t at slot c ^ kkey(t); V at vslot): super-block j is loaded NS - 2 stages
+  // before its scores
   constexpr int NS = D == 64 ? 4 : 3;
   constexpr int LPW = 2 * LOADS / W;  // loads per wave per stage
   static_assert(LOADS % W == 0, "every wave issues the same number of K (and V) loads");
@@ -242,20 +262,20 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   const float scale = fabsf(A.qk_scale_log2);
   // lane-relative LDS offsets of the operand reads within a stage:
   //   K (A operand of S^T): token lane % 32 (+32 for the second half, an
-  //   immediate offset), chunk of dims 16k + 8g at slot (2k + g) ^ (token & 7);
+  //   immediate offset), chunk of dims 16k + 8g at slot (2k + g) ^ kkey(token);
   //   V^T (ds_read_b64_tr_b16): input lane j = lane % 16 of 16-lane group
   //   k16 = lane / 16 reads token 4g + j / 4 (+ 8, 16, 32 by immediates),
   //   dims 32 db + 16 (k16 % 2) + 4 (j % 4) .. + 3; the group's output lane i
   //   then holds dim 32 db + 16 (k16 % 2) + i of four consecutive tokens.
+  //   One instruction's 64 lanes read one 512-byte V sub-block.
   uint32_t krel[NK], vrel[ND];
 #pragma unroll
-  for (int k = 0; k < NK; ++k) krel[k] = (lane & 31) * ROWB + (((2 * k + g) ^ (lane & 7)) << 4);
+  for (int k = 0; k < NK; ++k) krel[k] = (lane & 31) * ROWB + (((2 * k + g) ^ kkey<D>(lane & 31)) << 4);
   {
     const int tr = 4 * g + ((lane & 15) >> 2);  // token (mod 8) the lane reads
     const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
-    for (int db = 0; db < ND; ++db)
-      vrel[db] = tr * ROWB + ((((32 * db + tr_d) / 8) ^ tr) << 4) + (tr_d % 8) * 2;
+    for (int db = 0; db < ND; ++db) vrel[db] = vslot<D>(tr, 32 * db + tr_d);
   }
   for (int k = 0; k < ntiles; ++k) {
   const int rt = k == 0 ? nt - 1 - pair : pair;
@@ -297,14 +317,22 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int kv = i * W / LOADS, jj = i * W % LOADS + w;
-      const int tb = sb * SB * BT + jj * TPL;
       const int page = pv[i % NPG];
-      const int tl = jj * TPL + lane / CH;  // token within the block
-      const int c = lane % CH;
-      const int t = min(tb + lane / CH, nkv - 1);
+      // the lane's 16 bytes: token tl of the stage, dims dim .. dim + 7
+      int tl, dim;
+      if (kv == 0) {  // K: row-major, the lane's slot lane % CH holds chunk slot ^ kkey
+        tl = jj * TPL + lane / CH;
+        dim = 8 * ((lane % CH) ^ kkey<D>(tl));
+      } else {  // V: sub-blocks 2jj, 2jj + 1 (vslot), 8 tokens x 64 dims
+        constexpr int H = D / 64;  // 1 KB loads per 8 tokens
+        tl = 8 * (jj / H) + ((lane & 31) >> 2);
+        dim = 32 * (2 * (jj % H) + (lane >> 5)) + 8 * (lane & 3);
+      }
+      // (the 8 tokens of a V load lie in the page of the K load jj: both are
+      // 8-aligned within it)
+      const int t = min(sb * SB * BT + tl, nkv - 1);
       const uint16_t* pool = kv ? A.v_pool : A.k_pool;
-      const char* src = (const char*)(pool + (int64_t)page * page_stride + head_off +
-                                      (int64_t)(t % kPage) * D) + ((c ^ (tl & 7)) << 4);
+      const uint16_t* src = pool + (int64_t)page * page_stride + head_off + (int64_t)(t % kPage) * D + dim;
       __builtin_amdgcn_global_load_lds(src, (lds_void_p*)(s_kv[st][kv] + jj * 1024), 16, 0, 0);
     }
   };
