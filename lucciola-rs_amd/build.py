@@ -32,8 +32,9 @@ HIPCC_FLAGS = [
     # no packed-FP32 instructions (v_pk_{add,mul,fma}_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-# per code object: the prefill kernel keeps its MFMA accumulators in ordinary
-# VGPRs (no accvgpr copies of the scores, three waves per SIMD)
+# per code object: the prefill kernels keep their MFMA results in ordinary
+# VGPRs (the scores go straight to the VALU; the two-heads-per-wave kernels
+# hold their K and V operands in AGPRs, read by the MFMAs directly)
 KERNEL_FLAGS = {"paged_prefill": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 

@@ -128,6 +128,17 @@ __device__ inline void lds_k_issue(uint32_t a0, uint32_t a1, uint32_t a2, uint32
       : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "n"(HOFF)
       : "memory");
 }
+// K of one 32-token half of a block: x[k] = chunk k of token lane % 32
+__device__ inline void lds_k4_issue(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, u32x4_t* x) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %5\n\t"
+      "ds_read_b128 %2, %6\n\t"
+      "ds_read_b128 %3, %7"
+      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3])
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "memory");
+}
 // Waits for the K reads above while N LDS reads issued after them may stay
 // outstanding (LDS reads complete in order; a scalar load still in flight
 // only makes the wait stricter).
@@ -162,12 +173,15 @@ __device__ inline void lds_v_issue_half(uint32_t a0, uint32_t a1, u32x2_t* x) {
         "n"((32 * H + 24) * R)
       : "memory");
 }
+// Waits for the V reads above while N LDS reads issued after them may stay
+// outstanding.
+template <int N = 0>
 __device__ inline void lds_wait_v(u32x2_t* x) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
+  asm volatile("s_waitcnt lgkmcnt(%16)"
                : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),
                  "+v"(x[6]), "+v"(x[7]), "+v"(x[8]), "+v"(x[9]), "+v"(x[10]), "+v"(x[11]),
                  "+v"(x[12]), "+v"(x[13]), "+v"(x[14]), "+v"(x[15])
-               :
+               : "n"(N)
                : "memory");
 }
 
@@ -189,7 +203,7 @@ __device__ constexpr uint32_t vslot(int t, int d) {
   return ((t >> 3) * (D / 32) + (d >> 5)) * 512 + ((t & 7) << 6) + (((d & 31) >> 2) << 3);
 }
 
-// Waves per prefill workgroup for group size G (<= 8).
+// Waves per prefill workgroup for group size G (<= 8): one per q-head.
 constexpr int prefill_waves(int g) { return g <= 4 ? 4 : 8; }
 
 template <int DT, int D, int G>
@@ -213,6 +227,8 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   // t at slot c ^ kkey(t); V at vslot): super-block j is loaded NS - 2 stages
   // before its scores
   constexpr int NS = D == 64 ? 4 : 3;
+  // head_dim 64 with two-block super-blocks (8 waves): the software-pipelined steps
+  constexpr bool PIPE = D == 64 && SB == 2;
   constexpr int LPW = 2 * LOADS / W;  // loads per wave per stage
   static_assert(LOADS % W == 0, "every wave issues the same number of K (and V) loads");
   __shared__ __attribute__((aligned(16))) char s_kv[NS][2][KS];
@@ -277,6 +293,28 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 #pragma unroll
     for (int db = 0; db < ND; ++db) vrel[db] = vslot<D>(tr, 32 * db + tr_d);
   }
+  // The 16 bytes that this lane's part of the wave's load i of a stage
+  // fetches: token load_token(i) of the stage, 8 dims, at byte
+  // load_offset(i, token % page) of the page's rows for this layer and head.
+  auto load_token = [&](int i) {
+    const int jj = i * W % LOADS + w;
+    return i * W / LOADS == 0 ? jj * TPL + lane / CH                 // K: row-major
+                              : 8 * (jj / (D / 64)) + ((lane & 31) >> 2);  // V: sub-blocks 2jj, 2jj + 1
+  };
+  auto load_offset = [&](int i, int slot) -> uint32_t {
+    const int jj = i * W % LOADS + w;
+    const int dim = i * W / LOADS == 0
+                        ? 8 * ((lane % CH) ^ kkey<D>(load_token(i)))  // slot lane % CH holds chunk slot ^ kkey
+                        : 32 * (2 * (jj % (D / 64)) + (lane >> 5)) + 8 * (lane & 3);
+    return (uint32_t)(slot * D + dim) * 2;
+  };
+  // stage tokens are page-aligned: token % page = load_token % page.  Kept
+  // in registers except by the 8-wave head_dim 128 kernels, which have none
+  // to spare (they recompute them)
+  constexpr bool KEEP_OFF = !(D == 128 && W == 8);
+  uint32_t lane_off[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) lane_off[i] = KEEP_OFF ? load_offset(i, load_token(i) % kPage) : 0;
   for (int k = 0; k < ntiles; ++k) {
   const int rt = k == 0 ? nt - 1 - pair : pair;
   const int my_i = rt * 32 + (lane & 31);  // the lane's prompt row (q row of the tile)
@@ -314,31 +352,32 @@ __device__ void prefill_impl(const PrefillArgs& A) {
       if (!ok) bad_tok = min(bad_tok, page_index(sb, i) * kPage);
       pv[i] = ok ? pg[i] : 0;
     }
+    const int sbase = sb * SB * BT;
+    // uniform: every token of the stage inside the context, so every lane
+    // reads at its fixed offset within the page (a 32-bit offset from the
+    // page row's scalar base address)
+    const bool whole = sbase + SB * BT <= nkv;
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int kv = i * W / LOADS, jj = i * W % LOADS + w;
-      const int page = pv[i % NPG];
-      // the lane's 16 bytes: token tl of the stage, dims dim .. dim + 7
-      int tl, dim;
-      if (kv == 0) {  // K: row-major, the lane's slot lane % CH holds chunk slot ^ kkey
-        tl = jj * TPL + lane / CH;
-        dim = 8 * ((lane % CH) ^ kkey<D>(tl));
-      } else {  // V: sub-blocks 2jj, 2jj + 1 (vslot), 8 tokens x 64 dims
-        constexpr int H = D / 64;  // 1 KB loads per 8 tokens
-        tl = 8 * (jj / H) + ((lane & 31) >> 2);
-        dim = 32 * (2 * (jj % H) + (lane >> 5)) + 8 * (lane & 3);
-      }
+      const char* const base = (const char*)((kv ? A.v_pool : A.k_pool) +
+                                             (int64_t)pv[i % NPG] * page_stride + head_off);
       // (the 8 tokens of a V load lie in the page of the K load jj: both are
       // 8-aligned within it)
-      const int t = min(sb * SB * BT + tl, nkv - 1);
-      const uint16_t* pool = kv ? A.v_pool : A.k_pool;
-      const uint16_t* src = pool + (int64_t)page * page_stride + head_off + (int64_t)(t % kPage) * D + dim;
-      __builtin_amdgcn_global_load_lds(src, (lds_void_p*)(s_kv[st][kv] + jj * 1024), 16, 0, 0);
+      const uint32_t off = !whole ? load_offset(i, min(sbase + load_token(i), nkv - 1) % kPage)
+                           : KEEP_OFF ? lane_off[i] : load_offset(i, load_token(i) % kPage);
+      __builtin_amdgcn_global_load_lds(base + off, (lds_void_p*)(s_kv[st][kv] + jj * 1024), 16, 0,
+                                       0);
     }
   };
-  // Q^T fragments (B operand): lane l holds q row my_i, dims (l/32)*8 + 16k .. +8
-  // (loaded before the first blocks, so the block waits below can count
-  // only block loads)
+  // s_waitcnt vmcnt(n * LPW): all but this wave's loads of the n most recently
+  // issued super-blocks have landed (loads complete in order)
+  auto wait_blocks = [&](int n) __attribute__((always_inline)) {
+    if (n >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPW) : "memory");
+    else if (n == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+  static_assert(NS - 2 <= 2, "wait_blocks covers up to two newer super-blocks");
   // Q^T fragments (B operand): lane l holds q row my_i, dims (l/32)*8 + 16k .. +8
   // (loaded before the tile's first K/V loads are issued, so the block waits
   // below count only block loads)
@@ -357,14 +396,6 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 #pragma unroll
     for (int k = 0; k < NK; ++k) asm volatile("" ::"v"(qf[k].x), "v"(qf[k].y), "v"(qf[k].z), "v"(qf[k].w));
   }
-  // s_waitcnt vmcnt(n * LPW): all but this wave's loads of the n most recently
-  // issued super-blocks have landed (loads complete in order)
-  auto wait_blocks = [&](int n) __attribute__((always_inline)) {
-    if (n >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPW) : "memory");
-    else if (n == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  };
-  static_assert(NS - 2 <= 2, "wait_blocks covers up to two newer super-blocks");
 
   // ---- S^T = K Q^T of block blk, two 32-token halves ----
   auto qk = [&](int blk, f32x16* sc) __attribute__((always_inline)) {
@@ -401,28 +432,8 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 
   // ---- mask, online softmax (exp2 domain) and O^T += V^T P^T of block blk ----
   // (a) mask, block max and the lazy move of the running max
-  auto softmax_max = [&](int blk, f32x16* sc) __attribute__((always_inline)) {
-    const int t0 = blk * BT;
-    // sc[hf][4i + j]: token t0 + 32hf + 8i + 4g + j, q row my_i
-    float mb = -INFINITY;
-    if (t0 + BT - 1 <= sp + rt * 32) {  // wave-uniform: below the diagonal, no mask
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mb = fmaxf(mb, sc[hf][e]);
-    } else {
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int t = t0 + 32 * hf + 8 * i + 4 * g + j;
-            const float x = t <= my_pos ? sc[hf][4 * i + j] : -INFINITY;
-            sc[hf][4 * i + j] = x;
-            mb = fmaxf(mb, x);
-          }
-    }
+  // mb: the lane's row max of the block's scores (both 32-token halves)
+  auto lazy_update = [&](float mb) __attribute__((always_inline)) {
     {
       const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
       mb = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -442,6 +453,32 @@ __device__ void prefill_impl(const PrefillArgs& A) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) osum[e] *= alpha;
     }
+  };
+  // block blk entirely at or before the tile's first row position: no mask
+  auto unmasked = [&](int blk) { return blk * BT + BT - 1 <= sp + rt * 32; };
+  auto softmax_max = [&](int blk, f32x16* sc) __attribute__((always_inline)) {
+    const int t0 = blk * BT;
+    // sc[hf][4i + j]: token t0 + 32hf + 8i + 4g + j, q row my_i
+    float mb = -INFINITY;
+    if (unmasked(blk)) {  // wave-uniform: below the diagonal
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mb = fmaxf(mb, sc[hf][e]);
+    } else {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int t = t0 + 32 * hf + 8 * i + 4 * g + j;
+            const float x = t <= my_pos ? sc[hf][4 * i + j] : -INFINITY;
+            sc[hf][4 * i + j] = x;
+            mb = fmaxf(mb, x);
+          }
+    }
+    lazy_update(mb);
   };
   // (b) the weights exp2(s * scale - m)
   auto softmax_exp = [&](f32x16* sc) __attribute__((always_inline)) {
@@ -585,10 +622,168 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   wait_blocks(min(NS - 2, nsb - 1));
   __builtin_amdgcn_s_barrier();
   f32x16 sa[2], sb[2];
-  if (active) qk(0, sa);
-  for (int blk = 0; blk < nblk; blk += 2) {
-    step(blk, sa, sb);
-    if (blk + 1 < nblk) step(blk + 1, sb, sa);
+  if constexpr (PIPE) {
+    // A software pipeline over blocks; each step is a fixed sequence of MFMA
+    // slots -- the 8 score MFMAs of the next block (two accumulation chains,
+    // one per 32-token half, run one after the other) and the 12 PV MFMAs of
+    // this block -- each followed by its share of the VALU work (this
+    // block's exponentials and P^T packing, the next block's row max), so
+    // the matrix cores and the VALU of a wave work at once.  Chunk c (of 4)
+    // holds score MFMAs 2c, 2c + 1, the PV MFMAs of step c - 1 and the
+    // weights of PV step c.  LDS reads: the first half of K(blk + 2) goes
+    // out once chain 0 of step blk has read its operands, the second half
+    // after chain 1, V(blk + 1) at the end of step blk.  Super-block J's
+    // barrier comes at the start of step 2J - 2, before K(2J) is read; every
+    // wave has then finished step 2J - 3 and with it every read of
+    // super-block J - 2, whose stage takes super-block J + 2.
+    u32x4_t ka[8];   // K operands (x[k]: first 32-token half, x[4 + k]: second)
+    u32x2_t va[16];  // V^T operands of a block's PV steps
+    uint4 pb[4];     // P^T operands of the current block's PV steps
+    auto kbase = [&](int blk) { return lds_addr(s_kv[(blk / SB) % NS][0]) + (blk % SB) * KB; };
+    // K of one 32-token half (hf) of block blk into x[4 hf .. 4 hf + 3]
+    auto read_k_half = [&](int blk, int hf) __attribute__((always_inline)) {
+      const uint32_t bb = kbase(blk) + hf * 32 * ROWB;
+      lds_k4_issue(bb + krel[0], bb + krel[1], bb + krel[2], bb + krel[3], ka + 4 * hf);
+    };
+    auto read_v = [&](int blk) __attribute__((always_inline)) {
+      const uint32_t bb = lds_addr(s_kv[(blk / SB) % NS][1]) + (blk % SB) * KB;
+      lds_v_issue_half<ROWB, 0>(bb + vrel[0], bb + vrel[1], va);
+      lds_v_issue_half<ROWB, 1>(bb + vrel[0], bb + vrel[1], va);
+    };
+    auto fence = []() __attribute__((always_inline)) { __builtin_amdgcn_sched_barrier(0); };
+    // score MFMA i (0..7) of the next block: chain (half) i / 4, k-step i % 4
+    auto qk_mfma = [&](f32x16* nx, int i) __attribute__((always_inline)) {
+      const int hf = i >> 2, kk = i & 3;
+      f32x16 acc = nx[hf];
+      if (kk == 0)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+      nx[hf] = mfma32<DT>(__builtin_bit_cast(uint4, ka[4 * hf + kk]), qf[kk], acc);
+    };
+    // PV MFMA j (0..2) of step c: the row sums, then O^T dims 32 (j - 1) ..
+    auto pv_mfma = [&](int c, int j) __attribute__((always_inline)) {
+      if (j == 0) {
+        osum = mfma32<DT>(ones, pb[c], osum);
+      } else {
+        const int db = j - 1;
+        o[db] = mfma32<DT>(make_uint4(va[4 * c + 2 * db].x, va[4 * c + 2 * db].y,
+                                      va[4 * c + 2 * db + 1].x, va[4 * c + 2 * db + 1].y),
+                           pb[c], o[db]);
+      }
+    };
+    // weight it (0..7) of PV step c: element 8 (c % 2) + it of half c / 2;
+    // P^T of step c is packed after its eighth weight
+    auto exp_item = [&](f32x16* cu, int c, int it) __attribute__((always_inline)) {
+      const int e = 8 * (c & 1) + it;
+      cu[c >> 1][e] = __builtin_amdgcn_exp2f(fmaf(cu[c >> 1][e], scale, -m_run));
+      if (it == 7) pb[c] = p_operand(cu, c >> 1, c & 1);
+    };
+    auto step64 = [&](int blk, f32x16* cu, f32x16* nx) __attribute__((always_inline)) {
+      if (blk % 2 == 0) {  // super-block J's barrier, before K(2J) is read
+        const int J = (blk + 2) / 2;
+        if (J < nsb) {
+          wait_blocks(min(NS - 3, nsb - 1 - J));
+          __builtin_amdgcn_s_barrier();
+          if (J + 2 < nsb) {
+            issue(J + 2, (J + 2) % NS, pgn);
+            if (J + 3 < nsb) load_pages(J + 3, pgn);
+          }
+        }
+      }
+      if (!active) return;
+      // K(blk + 1), both halves; V(blk), issued after them, may be in flight
+      lds_wait_k<15>(ka);
+      float mx[2] = {-INFINITY, -INFINITY};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (c == 1) lds_wait_v<0>(va);  // V(blk)
+        // MFMA slots: Q P Q P P (c > 0) or Q Q; the weights of step c and
+        // (chunks 2, 3) the row max of chain 0 spread over them
+        const int np = c > 0 ? 3 : 0, n = 2 + np;
+        const int nm = c >= 2 ? 8 : 0;
+        int qi = 0, pi = 0, it = 0, mi = 0;
+#pragma unroll
+        for (int sl = 0; sl < 5; ++sl) {
+          if (sl < n) {
+            const bool q_turn = qi < 2 && (pi >= np || (sl & 1) == 0);
+            if (q_turn) qk_mfma(nx, 2 * c + qi++);
+            else pv_mfma(c - 1, pi++);
+            fence();
+#pragma unroll
+            for (; it < 8 * (sl + 1) / n; ++it) exp_item(cu, c, it);
+#pragma unroll
+            for (; mi < nm * (sl + 1) / n; ++mi) {
+              const int e = 8 * (c - 2) + mi;
+              mx[e & 1] = fmaxf(mx[e & 1], nx[0][e]);
+            }
+            fence();
+          }
+        }
+#pragma unroll
+        for (; it < 8; ++it) exp_item(cu, c, it);
+        // a K half is free once its chain has been issued
+        if (c == 1) read_k_half(blk + 2, 0);
+        if (c == 3) read_k_half(blk + 2, 1);
+      }
+      // tail: the PV MFMAs of step 3 with the row max of chain 1
+      int mi = 0;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        pv_mfma(3, j);
+        fence();
+#pragma unroll
+        for (; mi < 16 * (j + 1) / 3; ++mi) mx[mi & 1] = fmaxf(mx[mi & 1], nx[1][mi]);
+        fence();
+      }
+      // (the max is needed only when there is a next block: without this the
+      // compiler would move it behind that branch, out of the MFMA shadow)
+      asm volatile("" ::"v"(mx[0]), "v"(mx[1]));
+      read_v(blk + 1);  // (past the last block: read, never used)
+      if (blk + 1 < nblk) {  // wave-uniform
+        float mb = fmaxf(mx[0], mx[1]);
+        if (!unmasked(blk + 1)) {  // mask the diagonal block, its max again
+          const int t0 = (blk + 1) * BT;
+          mb = -INFINITY;
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const int t = t0 + 32 * hf + 8 * i + 4 * g + j;
+                const float x = t <= my_pos ? nx[hf][4 * i + j] : -INFINITY;
+                nx[hf][4 * i + j] = x;
+                mb = fmaxf(mb, x);
+              }
+        }
+        lazy_update(mb);
+      }
+    };
+    if (active) {  // block 0's scores and max; K(1) and V(0) in flight
+      read_k_half(0, 0);
+      read_k_half(0, 1);
+      lds_wait_k<0>(ka);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qk_mfma(sa, i);
+      read_k_half(1, 0);
+      read_k_half(1, 1);
+      read_v(0);
+      softmax_max(0, sa);
+    }
+    for (int blk = 0; blk < nblk; blk += 2) {
+      step64(blk, sa, sb);
+      if (blk + 1 < nblk) step64(blk + 1, sb, sa);
+    }
+    if (active) {  // the last reads (never used) land before their registers are reused
+      lds_wait_k<0>(ka);
+      lds_wait_v<0>(va);
+    }
+  } else {
+    if (active) qk(0, sa);
+    for (int blk = 0; blk < nblk; blk += 2) {
+      step(blk, sa, sb);
+      if (blk + 1 < nblk) step(blk + 1, sb, sa);
+    }
   }
 
   // ---- normalise and store: lane holds dims 32db + 8i + 4g + j of row my_i ----
