@@ -3,9 +3,11 @@
 // Semantics (the reference's per-token prefill loop, Qwen2Model::forward_layer
 // src/models.rs:485-550): the prompt rows of sequence b are packed rows
 // cu_seqlens[b] .. cu_seqlens[b+1]-1 of qkv, at positions start_pos[b] + i.
-// By the time this kernel runs, every row's q and k are roped in place and its
-// roped k and v + v_bias are in the cache (the append kernel, launched first
-// on the same stream).  Row i of sequence b and q-head qh then attends to
+// By the time this kernel runs, every row's k is roped in place and its roped
+// k and v + v_bias are in the cache (the append kernel, launched first on the
+// same stream).  q gets its bias and RoPE here, as each row's q is loaded
+// (the append kernel's arithmetic, bit for bit), and is written back in place
+// (when the tables allow 16-byte loads; else the append kernel ropes q too).  Row i of sequence b and q-head qh then attends to
 // cache positions 0..start_pos[b] + i through table row b -- the cached prefix
 // and the prompt rows up to itself -- exactly what the reference's
 // flash_decoding call for that token computes (src/kernels/attention.cu:4-176),
@@ -60,7 +62,7 @@ __device__ inline uint32_t lds_addr(const void* p) {
 }
 
 struct PrefillArgs {
-  const uint16_t* qkv;  // row r at qkv + r*qkv_stride: [q (Hq*D) | k | v], q roped
+  uint16_t* qkv;  // row r at qkv + r*qkv_stride: [q (Hq*D) | k | v]
   int64_t qkv_stride;
   const uint16_t* k_pool;  // [blocks][num_layers][Hkv][16][D]
   const uint16_t* v_pool;
@@ -70,6 +72,11 @@ struct PrefillArgs {
   const int32_t* start_pos;   // [batch]
   uint16_t* out;              // row r at out + r*out_stride, [Hq*D]
   int64_t out_stride;
+  // q's bias + RoPE: with cos_t set, q is roped here (in place, as the
+  // append kernel would) as it is loaded; else the append kernel has done it
+  const uint16_t* q_bias;  // [Hq*D] or null
+  const float* cos_t;      // [positions][D/2], 16-byte aligned, or null
+  const float* sin_t;
   int32_t batch, layer, num_layers, hkv, max_ctx, pairs;  // pairs: tile pairs per sequence
   int32_t num_blocks;  // pages per pool: table entries outside [0, num_blocks) are never used
   float qk_scale_log2;  // sm_scale * log2(e)
@@ -254,6 +261,30 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   const bool active = hg * W + w < G;  // wave-uniform: a q-head of the group
   const int qh = h * G + min(hg * W + w, G - 1);
   const int g = lane >> 5;
+  // q's RoPE here except in the 8-wave head_dim 128 kernels, which have no
+  // registers to spare (the host then has the append kernel rope q)
+  constexpr bool QROPE = !(D == 128 && W == 8);
+  // The lane's share of q-head row qrow (dims g*8 + 16k .. + 8, k < NK), with
+  // bias + RoPE at position pos: dims i and i + D/2 are pairs k and k + NK/2
+  // of the same lane.  Written back in place when `store`.
+  auto rope_q = [&](uint16_t* qrow, int pos, uint4* x, bool store) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < NK; ++k) x[k] = *(const uint4*)(qrow + g * 8 + 16 * k);
+    const bool has_bias = A.q_bias != nullptr;
+    const uint16_t* const brow = A.q_bias + (int64_t)qh * D + g * 8;
+#pragma unroll
+    for (int k = 0; k < NK / 2; ++k) {
+      const uint4 zero = make_uint4(0, 0, 0, 0);
+      const uint4 b1 = has_bias ? *(const uint4*)(brow + 16 * k) : zero;
+      const uint4 b2 = has_bias ? *(const uint4*)(brow + 16 * k + D / 2) : zero;
+      const float4* cp = (const float4*)(A.cos_t + (int64_t)pos * (D / 2) + g * 8 + 16 * k);
+      const float4* spp = (const float4*)(A.sin_t + (int64_t)pos * (D / 2) + g * 8 + 16 * k);
+      rope_rotate8<DT>(x[k], x[k + NK / 2], b1, b2, has_bias, cp[0], cp[1], spp[0], spp[1]);
+    }
+    if (store)
+#pragma unroll
+      for (int k = 0; k < NK; ++k) *(uint4*)(qrow + g * 8 + 16 * k) = x[k];
+  };
   if (sp < 0 || sp + nrows > A.max_ctx) {
     // positions outside the host bound: flagged with NaN, never truncated
     // (such a sequence may have more tiles than the grid has pairs: the
@@ -263,6 +294,12 @@ __device__ void prefill_impl(const PrefillArgs& A) {
         uint16_t* const orow = A.out + (int64_t)(row0 + r) * A.out_stride + (int64_t)qh * D;
         for (int d = 0; d < D; d += 8)
           for (int j = 0; j < 4; ++j) orow[d + 4 * g + j] = St<DT>::store(__builtin_nanf(""));
+        // q still gets its RoPE where its position lies in the table row
+        const int64_t pos = (int64_t)sp + r;
+        if (QROPE && A.cos_t && pos >= 0 && pos < A.table_stride * kPage) {
+          uint4 qv[NK];
+          rope_q(A.qkv + (int64_t)(row0 + r) * A.qkv_stride + (int64_t)qh * D, (int)pos, qv, true);
+        }
       }
     return;
   }
@@ -296,16 +333,16 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   // The 16 bytes that this lane's part of the wave's load i of a stage
   // fetches: token load_token(i) of the stage, 8 dims, at byte
   // load_offset(i, token % page) of the page's rows for this layer and head.
-  auto load_token = [&](int i) {
+  auto load_token = [&](int i, int ln) {
     const int jj = i * W % LOADS + w;
-    return i * W / LOADS == 0 ? jj * TPL + lane / CH                 // K: row-major
-                              : 8 * (jj / (D / 64)) + ((lane & 31) >> 2);  // V: sub-blocks 2jj, 2jj + 1
+    return i * W / LOADS == 0 ? jj * TPL + ln / CH                 // K: row-major
+                              : 8 * (jj / (D / 64)) + ((ln & 31) >> 2);  // V: sub-blocks 2jj, 2jj + 1
   };
-  auto load_offset = [&](int i, int slot) -> uint32_t {
+  auto load_offset = [&](int i, int slot, int ln) -> uint32_t {
     const int jj = i * W % LOADS + w;
     const int dim = i * W / LOADS == 0
-                        ? 8 * ((lane % CH) ^ kkey<D>(load_token(i)))  // slot lane % CH holds chunk slot ^ kkey
-                        : 32 * (2 * (jj % (D / 64)) + (lane >> 5)) + 8 * (lane & 3);
+                        ? 8 * ((ln % CH) ^ kkey<D>(load_token(i, ln)))  // slot ln % CH holds chunk slot ^ kkey
+                        : 32 * (2 * (jj % (D / 64)) + (ln >> 5)) + 8 * (ln & 3);
     return (uint32_t)(slot * D + dim) * 2;
   };
   // stage tokens are page-aligned: token % page = load_token % page.  Kept
@@ -314,7 +351,7 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   constexpr bool KEEP_OFF = !(D == 128 && W == 8);
   uint32_t lane_off[LPW];
 #pragma unroll
-  for (int i = 0; i < LPW; ++i) lane_off[i] = KEEP_OFF ? load_offset(i, load_token(i) % kPage) : 0;
+  for (int i = 0; i < LPW; ++i) lane_off[i] = KEEP_OFF ? load_offset(i, load_token(i, lane) % kPage, lane) : 0;
   for (int k = 0; k < ntiles; ++k) {
   const int rt = k == 0 ? nt - 1 - pair : pair;
   const int my_i = rt * 32 + (lane & 31);  // the lane's prompt row (q row of the tile)
@@ -364,8 +401,13 @@ __device__ void prefill_impl(const PrefillArgs& A) {
                                              (int64_t)pv[i % NPG] * page_stride + head_off);
       // (the 8 tokens of a V load lie in the page of the K load jj: both are
       // 8-aligned within it)
-      const uint32_t off = !whole ? load_offset(i, min(sbase + load_token(i), nkv - 1) % kPage)
-                           : KEEP_OFF ? lane_off[i] : load_offset(i, load_token(i) % kPage);
+      // (the lane's offsets are recomputed from an opaque copy of the lane
+      // index where they are not kept, so that the compiler keeps no other
+      // lane constants alive for them)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const uint32_t off = !whole ? load_offset(i, min(sbase + load_token(i, ln), nkv - 1) % kPage, ln)
+                           : KEEP_OFF ? lane_off[i] : load_offset(i, load_token(i, ln) % kPage, ln);
       __builtin_amdgcn_global_load_lds(base + off, (lds_void_p*)(s_kv[st][kv] + jj * 1024), 16, 0,
                                        0);
     }
@@ -381,21 +423,28 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   // Q^T fragments (B operand): lane l holds q row my_i, dims (l/32)*8 + 16k .. +8
   // (loaded before the tile's first K/V loads are issued, so the block waits
   // below count only block loads)
+  // (with q's RoPE here, loaded and roped once the tile's first super-block
+  // of K/V loads is issued: the two latencies overlap, and that super-block
+  // is waited for before the first scores anyway; written back at the tile's
+  // end)
   uint4 qf[NK];
-  {
-    const uint16_t* qrow = A.qkv + (int64_t)(row0 + min(my_i, nrows - 1)) * A.qkv_stride + (int64_t)qh * D;
+  uint16_t* const qrow = A.qkv + (int64_t)(row0 + min(my_i, nrows - 1)) * A.qkv_stride + (int64_t)qh * D;
+  const bool qrope = QROPE && A.cos_t != nullptr;  // wave-uniform
+  if (!qrope)
 #pragma unroll
     for (int k = 0; k < NK; ++k) qf[k] = *(const uint4*)(qrow + g * 8 + 16 * k);
-    if (neg_scale) {  // S = -(K Q^T) exactly: sign flips commute with rounding
+  auto finish_q = [&]() __attribute__((always_inline)) {
+    if (qrope) rope_q(qrow, sp + min(my_i, nrows - 1), qf, false);
+    if (neg_scale)  // S = -(K Q^T) exactly: sign flips commute with rounding
 #pragma unroll
       for (int k = 0; k < NK; ++k) {
         qf[k].x ^= 0x80008000u; qf[k].y ^= 0x80008000u;
         qf[k].z ^= 0x80008000u; qf[k].w ^= 0x80008000u;
       }
-    }
+    // q is complete here, so the block waits below count only block loads
 #pragma unroll
     for (int k = 0; k < NK; ++k) asm volatile("" ::"v"(qf[k].x), "v"(qf[k].y), "v"(qf[k].z), "v"(qf[k].w));
-  }
+  };
 
   // ---- S^T = K Q^T of block blk, two 32-token halves ----
   auto qk = [&](int blk, f32x16* sc) __attribute__((always_inline)) {
@@ -613,11 +662,13 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   if (k) __builtin_amdgcn_s_barrier();
   if (threadIdx.x == 0) s_bad_tok = 0x7fffffff;  // (read by every wave only after a barrier below)
 #pragma unroll
-  for (int j = 0; j < NS - 1; ++j)
+  for (int j = 0; j < NS - 1; ++j) {
     if (j < nsb) {
       load_pages(j, pgn);
       issue(j, j, pgn);
     }
+    if (j == 0) finish_q();  // (q's loads and super-block 0's are in flight together)
+  }
   if (NS - 1 < nsb) load_pages(NS - 1, pgn);
   wait_blocks(min(NS - 2, nsb - 1));
   __builtin_amdgcn_s_barrier();
@@ -793,6 +844,17 @@ __device__ void prefill_impl(const PrefillArgs& A) {
   const int first_bad = s_bad_tok;
   if (!active) continue;
   if (row_ok) {
+    if (qrope)  // the roped q, in place (its sign flip undone); stored here, not
+                // in the prologue, so that no wait for the tile's first loads
+                // waits for these stores too
+#pragma unroll
+      for (int k = 0; k < NK; ++k) {
+        uint4 x = qf[k];
+        if (neg_scale) {
+          x.x ^= 0x80008000u; x.y ^= 0x80008000u; x.z ^= 0x80008000u; x.w ^= 0x80008000u;
+        }
+        *(uint4*)(qrow + g * 8 + 16 * k) = x;
+      }
     const float inv = my_pos >= first_bad ? __builtin_nanf("") : 1.0f / osum[0];
 #pragma unroll
     for (int db = 0; db < ND; ++db)

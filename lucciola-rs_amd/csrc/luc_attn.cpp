@@ -374,6 +374,9 @@ struct PrefillArgs {
   const int32_t* start_pos;
   void* out;
   int64_t out_stride;
+  const void* q_bias;
+  const float* cos_t;
+  const float* sin_t;
   int32_t batch, layer, num_layers, hkv, max_ctx, pairs, num_blocks;
   float qk_scale_log2;
 };
@@ -692,8 +695,14 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
   const int64_t grid = (int64_t)batch * num_kv_heads * ceil_div(group, waves) * pairs;
   if (grid > INT32_MAX) return fail(LUC_E_INVALID, "batch x kv heads x row tiles too large");
 
-  // 1) bias + RoPE of every prompt row's q and k in place, cache write of the
-  //    roped k and v + v_bias (models.rs:505-534 for each row)
+  // q's bias + RoPE runs in the attention kernel, which loads every row's q
+  // anyway, when the bias and the rotation tables allow its 16-byte loads
+  // (not in the 8-wave head_dim 128 kernels: paged_prefill.hip, QROPE); else
+  // the append kernel ropes q as well
+  const bool fuse_q = (!q_bias || aligned(q_bias, 16)) && aligned(cos_table, 16) &&
+                      aligned(sin_table, 16) && !(head_dim == 128 && group > 4);
+  // 1) bias + RoPE of every prompt row's k (and q unless fused) in place,
+  //    cache write of the roped k and v + v_bias (models.rs:505-534 for each row)
   uint16_t* base = static_cast<uint16_t*>(qkv);
   AppendArgs a;
   a.q = base; a.q_bias = q_bias; a.k = base + (int64_t)num_q_heads * head_dim; a.k_bias = k_bias;
@@ -703,7 +712,7 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
   a.tables = block_tables; a.table_stride = table_stride; a.num_blocks = num_blocks;
   a.k_pool = k_pool; a.v_pool = v_pool;
   a.layer = layer; a.num_layers = num_layers; a.hq = num_q_heads; a.hkv = num_kv_heads;
-  a.head_dim = head_dim; a.flags = kRopeQ | kRopeK | kWriteKV;
+  a.head_dim = head_dim; a.flags = (fuse_q ? 0 : kRopeQ) | kRopeK | kWriteKV;
   if (int rc = launch_append(ctx, stream, dtype, total_rows, a)) return rc;
 
   // 2) causal attention of every row over the cache (models.rs:536-549 per row)
@@ -711,6 +720,7 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
   p.qkv = qkv; p.qkv_stride = qkv_row_stride; p.k_pool = k_pool; p.v_pool = v_pool;
   p.tables = block_tables; p.table_stride = table_stride; p.cu_seqlens = cu_seqlens;
   p.start_pos = start_pos; p.out = out; p.out_stride = out_row_stride; p.batch = batch;
+  p.q_bias = q_bias; p.cos_t = fuse_q ? cos_table : nullptr; p.sin_t = sin_table;
   p.layer = layer; p.num_layers = num_layers; p.hkv = num_kv_heads; p.max_ctx = max_ctx;
   p.pairs = pairs; p.num_blocks = num_blocks; p.qk_scale_log2 = sm_scale * 1.4426950408889634f;
   void* args[] = {&p};
