@@ -114,12 +114,12 @@ __device__ __host__ inline int vslot(int t, int d) {
 // the row holds chunk s ^ key): the 16 rows one 16-lane group of the score
 // reads touches (tokens 16i .. 16i + 15 of a 32-token block, one chunk each)
 // fall on 16 different 16-byte bank groups of the 256-byte bank row.  A
-// head_dim 64 row is half a bank row, so rows t and t + 8 (the same half)
-// need different keys: (t >> 1) & 7.  A head_dim 128 row is a whole bank
-// row: t & 7.
+// head_dim 64 row is half a bank row, so rows 2m and 2m + 1 (the two halves)
+// share key m: (t >> 1) & 7.  A head_dim 128 row is a whole bank row, so
+// the 16 rows need 16 keys: t & 15.
 template <int D>
 __device__ __host__ inline int kswz(int t) {
-  return D == 64 ? (t >> 1) & 7 : t & 7;
+  return D == 64 ? (t >> 1) & 7 : t & 15;
 }
 
 // Row pitches (in elements) of per-head rows in LDS that lanes of different
@@ -822,12 +822,14 @@ __device__ void decode_impl(const DecodeArgs& A) {
 
   // Per-lane byte offsets inside a (page, layer, kv head) slab.  Load r reads
   // page r / LPP at + (r % LPP) * 1KB; the K slot pv_ch of token tl holds
-  // chunk pv_ch ^ (tl & 7), where tl & 7 only depends on the parity of r.
-  auto k_lane_off = [&](int parity) -> uint32_t {
-    const int sw = kswz<D>(parity * S::TPL + pv_tok);
-    return (uint32_t)(pv_tok * S::ROWB + ((pv_ch ^ sw) << 4));
-  };
-  const uint32_t koff0 = k_lane_off(0), koff1 = k_lane_off(1);
+  // chunk pv_ch ^ kswz(tl), where kswz(tl) only depends on r % NKO (tl =
+  // r * TPL + pv_tok: 8 tokens a load with key (tl >> 1) & 7 at head_dim 64,
+  // 4 tokens with key tl & 15 at 128).
+  constexpr int NKO = D == 64 ? 2 : 4;
+  uint32_t koff[NKO];
+#pragma unroll
+  for (int ph = 0; ph < NKO; ++ph)
+    koff[ph] = (uint32_t)(pv_tok * S::ROWB + ((pv_ch ^ kswz<D>(ph * S::TPL + pv_tok)) << 4));
   const uint32_t voff = (uint32_t)(pv_tok * S::ROWB + (pv_ch << 4));
 
   // Issue one tile: all its K loads (into K buffer buf) before its V loads
@@ -880,7 +882,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       const int64_t phys = phys_of(t0, r);
       // wave-uniform slab base (scalar registers) + 32-bit lane offsets
       const char* kslab = (const char*)(A.k_pool + phys * page_stride + head_off);
-      dma16(kslab + ((r & 1) ? koff1 : koff0), kdma + (r - r % S::LPP) * 1024,
+      dma16(kslab + koff[r % NKO], kdma + (r - r % S::LPP) * 1024,
             (r % S::LPP) * 1024);
     }
     if constexpr (FASTQ) {
@@ -1096,12 +1098,11 @@ __device__ void decode_impl(const DecodeArgs& A) {
     // and 0 * stale data must not produce NaN)
     const bool partial = t0 + S::TILE > s_end;
     if constexpr (MPV) {
-      // V into the tile's K buffer (free: the scores have read it), in K's
-      // layout: chunk c of token t at slot c ^ (t & 7).  Load r holds token
-      // r * TPL + pv_tok, so the slot's address is a per-lane base (one per
-      // parity of r when a load holds 4 tokens) plus r KB.  Tokens past the
-      // split (only in a split's last tile: a wave-uniform branch) are zeroed
-      // first.
+      // V into the tile's K buffer (free: the scores have read it), at
+      // vslot.  Load r holds token r * TPL + pv_tok, dims 8 pv_ch .. + 7, so
+      // the lane's 16 bytes go to a per-lane base (one per parity of r) plus
+      // 1 KB per load pair (lds_write_tile).  Tokens past the split (only in
+      // a split's last tile: a wave-uniform branch) are zeroed first.
       const uint32_t vbase = lds_addr(s_k[w][buf]);
       if (partial) {
 #pragma unroll
