@@ -635,9 +635,10 @@ __device__ void decode_impl(const DecodeArgs& A) {
   // PV on the matrix cores too (MPV): O^T += V^T P^T, V staged in the tile's
   // own K buffer once the scores have read it; o is then held as D/32 MFMA
   // accumulators (lane l: head l % 32, dims 32 db + 8 i + 4 (l / 32) + j).
-  // Not in the head_dim 128 tile-pair kernels, whose 64 accumulators would
-  // not fit beside the tile pair in flight.
-  constexpr bool MPV = T1 || D == 64;
+  // Not in the head_dim 128 tile-pair step kernels nor at group size 8
+  // there, whose 64 accumulators would not fit beside the tile pair in
+  // flight and the step operands (they take the dot2 form).
+  constexpr bool MPV = T1 || D == 64 || (!APPEND && G <= 7);
   constexpr int ND = D / 32;
   constexpr int NQ = (GD * 2 + 255) / 256;  // 4-byte direct-to-LDS loads for q
   // FASTA operand block: q of the G heads, then their biases (256-byte
