@@ -823,14 +823,12 @@ __device__ void decode_impl(const DecodeArgs& A) {
 
   // Per-lane byte offsets inside a (page, layer, kv head) slab.  Load r reads
   // page r / LPP at + (r % LPP) * 1KB; the K slot pv_ch of token tl holds
-  // chunk pv_ch ^ kswz(tl), where kswz(tl) only depends on r % NKO (tl =
-  // r * TPL + pv_tok: 8 tokens a load with key (tl >> 1) & 7 at head_dim 64,
-  // 4 tokens with key tl & 15 at 128).
+  // chunk pv_ch ^ kswz(tl), tl = r * TPL + pv_tok.  kswz(tl) is
+  // kswz(pv_tok) ^ 4 (r % NKO) (head_dim 64: 8 tokens a load, key
+  // (tl >> 1) & 7; 128: 4 tokens, key tl & 15), so load r's offset is
+  // koff0 ^ (r % NKO) << 6 (the XOR stays inside the chunk bits).
   constexpr int NKO = D == 64 ? 2 : 4;
-  uint32_t koff[NKO];
-#pragma unroll
-  for (int ph = 0; ph < NKO; ++ph)
-    koff[ph] = (uint32_t)(pv_tok * S::ROWB + ((pv_ch ^ kswz<D>(ph * S::TPL + pv_tok)) << 4));
+  const uint32_t koff0 = (uint32_t)(pv_tok * S::ROWB + ((pv_ch ^ kswz<D>(pv_tok)) << 4));
   const uint32_t voff = (uint32_t)(pv_tok * S::ROWB + (pv_ch << 4));
 
   // Issue one tile: all its K loads (into K buffer buf) before its V loads
@@ -883,7 +881,7 @@ __device__ void decode_impl(const DecodeArgs& A) {
       const int64_t phys = phys_of(t0, r);
       // wave-uniform slab base (scalar registers) + 32-bit lane offsets
       const char* kslab = (const char*)(A.k_pool + phys * page_stride + head_off);
-      dma16(kslab + koff[r % NKO], kdma + (r - r % S::LPP) * 1024,
+      dma16(kslab + (koff0 ^ ((r % NKO) << 6)), kdma + (r - r % S::LPP) * 1024,
             (r % S::LPP) * 1024);
     }
     if constexpr (FASTQ) {
@@ -936,8 +934,15 @@ __device__ void decode_impl(const DecodeArgs& A) {
     __builtin_amdgcn_s_barrier();
     if (ntw > 0) issue_v(t_first, vr0);
   } else if (ntw > 0) {
-    issue(t_first, 0, vr0);
-    issue(t_first + WS, 1, vr1);
+    if constexpr (!APPEND && MPV) {  // K_a K_b V_a V_b (PREK below)
+      issue_k(t_first, 0);
+      issue_k(t_first + WS, 1);
+      issue_v(t_first, vr0);
+      issue_v(t_first + WS, vr1);
+    } else {  // K_a V_a K_b V_b
+      issue(t_first, 0, vr0);
+      issue(t_first + WS, 1, vr1);
+    }
   }
 
   // ---- q of the G heads (roped in the step variant), new token's k, v ----
@@ -1281,33 +1286,52 @@ __device__ void decode_impl(const DecodeArgs& A) {
   } else {
     // The wave's tiles in pairs: both tiles of a pair are issued
     // (unconditionally, so that the loads keep their place ahead of the
-    // waits below), tile i is computed while tile i+1 lands.  In flight after
-    // issuing a pair: K_i V_i K_{i+1} V_{i+1}, 8 loads each, completing in
-    // issue order.  The first pair was issued before the prologue; later
-    // pairs load into registers local to their iteration (no values carried
-    // around the loop).
-    auto pair_compute = [&](int t0, bool pair, uint4(&va)[S::LOADS], uint4(&vb)[S::LOADS])
-                            __attribute__((always_inline)) {
-      LUC_WAIT_VM(24);  // K_i
+    // waits below), tile i is computed while tile i+1 lands.  PREK (the
+    // non-step kernels with PV on the matrix cores): a K buffer takes the same tile of the next pair as
+    // soon as its tile's PV is done, so the next pair's K loads are in flight
+    // while this pair is finished; its V loads (into registers, which hold
+    // one pair) go out when the pair starts.  In flight, in issue order (8
+    // loads each): K_a K_b (issued during the previous pair, or before the
+    // prologue), V_a V_b, then K_a' after tile a's PV and K_b' after tile
+    // b's.  The other kernels, which have no registers to spare for it, issue
+    // a whole pair when it starts: K_a V_a K_b V_b.  The first pair's V
+    // registers come from the prologue, later pairs' are local to their
+    // iteration (no values carried around the loop).
+    constexpr bool PREK = !APPEND && MPV;
+    auto pair_body = [&](int i, uint4(&va)[S::LOADS], uint4(&vb)[S::LOADS]) __attribute__((always_inline)) {
+      const int t0 = t_first + i * WS;
+      const bool pair = i + 1 < ntw, next = i + 2 < ntw;  // (wave-uniform)
+      LUC_WAIT_VM(24);  // K_a
       tile_scores(t0, 0);
-      LUC_WAIT_VM(16);  // V_i
+      if constexpr (PREK) LUC_WAIT_VM(8);  // V_a (and K_b)
+      else LUC_WAIT_VM(16);                // V_a
       tile_pv(t0, 0, va);
+      if (PREK && next) issue_k(t0 + 2 * WS, 0);
       if (pair) {
-        LUC_WAIT_VM(8);  // K_{i+1}
+        if constexpr (!PREK) LUC_WAIT_VM(8);  // K_b
         tile_scores(t0 + WS, 1);
-        LUC_WAIT_VM(0);  // V_{i+1}
+        if (PREK && next) LUC_WAIT_VM(8);  // V_b (K_a' behind it)
+        else LUC_WAIT_VM(0);
         tile_pv(t0 + WS, 1, vb);
       }
+      if (PREK && next) issue_k(t0 + 3 * WS, 1);
     };
     if (ntw > 0) {
-      pair_compute(t_first, ntw > 1, vr0, vr1);
+      pair_body(0, vr0, vr1);
       for (int i = 2; i < ntw; i += 2) {
-        const int t0 = t_first + i * WS;
         uint4 va[S::LOADS], vb[S::LOADS];
-        issue(t0, 0, va);
-        issue(t0 + WS, 1, vb);
-        pair_compute(t0, i + 1 < ntw, va, vb);
+        if constexpr (PREK) {
+          issue_v(t_first + i * WS, va);
+          issue_v(t_first + (i + 1) * WS, vb);
+        } else {
+          issue(t_first + i * WS, 0, va);
+          issue(t_first + (i + 1) * WS, 1, vb);
+        }
+        pair_body(i, va, vb);
       }
+      // (the unused second tile of an odd last pair lands before its
+      // buffers are reused)
+      LUC_WAIT_VM(0);
     }
   }
 
