@@ -1,4 +1,7 @@
-// Split-K paged decode attention for gfx950 (HBM-bound; no MFMA).
+// Split-K paged decode attention for gfx950.  HBM-bound: the scores, and PV
+// in every kernel but the head_dim 128 tile-pair step kernels and group size
+// 8 there, run on v_mfma_f32_32x32x16 to take their arithmetic off the VALU
+// after each tile lands, not for the flops.
 //
 // Semantics: for sequence b and q-head qh, attend with q[b][qh] to positions
 // 0..positions[b] of the paged cache through table row b, scale sm_scale,
@@ -39,8 +42,9 @@
 //   head l % 32 per 16-dim step, zero past the group).
 //   Per tile:
 //     1. K goes straight from HBM into LDS (global_load_lds_dwordx4; one
-//        wave-wide load = 1 KB of a page), each token row XOR-swizzled by
-//        16-byte chunk so the per-token LDS reads are conflict-free; V goes
+//        wave-wide load = 1 KB of a page), each token row's 16-byte chunks
+//        XOR-keyed by kswz(token) so the per-token LDS reads are free of bank
+//        conflicts; V goes
 //        to registers in the same load layout (lane = token x 16-byte chunk).
 //        All K loads of a tile precede its V loads, so the scores start as
 //        soon as K has landed.
@@ -52,11 +56,13 @@
 //     3. Online softmax in the exp2 domain with a lazy reference point: the
 //        running max moves (wave max by a DPP reduction, rescale of o) only
 //        when a score passes it by more than kLazyMax.
-//     4. o += p * V.  Single-tile and head_dim 64 kernels: O^T += V^T P^T on
-//        v_mfma_f32_32x32x16, V written into the tile's K buffer once the
-//        scores have read it and read back transposed (ds_read_b64_tr_b16),
-//        p through LDS head-major; o stays in the MFMA accumulators.  The
-//        head_dim 128 tile-pair kernels: V in its load layout, p of tokens t
+//     4. o += p * V.  Single-tile kernels, head_dim 64 kernels and the
+//        head_dim 128 tile-pair kernels without the step's append at group
+//        size <= 7: O^T += V^T P^T on v_mfma_f32_32x32x16, V written into the
+//        tile's K buffer once the scores have read it and read back
+//        transposed (ds_read_b64_tr_b16), p through LDS head-major; o stays
+//        in the MFMA accumulators.  The other head_dim 128 tile-pair kernels
+//        (step variants, group size 8): V in its load layout, p of tokens t
 //        and t + TILE/2 packed as a pair of the storage type, V of the same
 //        two tokens paired by v_perm, one v_dot2_f32_{f16,bf16} per (head,
 //        dim).  p is rounded where it is computed, so l sums the same values
