@@ -612,6 +612,119 @@ __device__ __attribute__((always_inline)) inline void finish_split(
   }
 }
 
+// Work item i of a split-K launch of the tile-pair kernels, longest first.
+// A workgroup's time grows with its split's length.  In plain split-major
+// order the longest sequences' full splits are the last to start, the short
+// last splits of all sequences are spread over every round, and workgroups
+// of splits past a context take a slot each; the launch ends on long
+// workgroups that started late.  Here the grid's workgroups take, in order:
+//   1. the full splits (split s of a sequence whose context holds
+//      (s + 1) * split_tokens tokens): first the rounds that every valid
+//      sequence has (s < n_min, the fewest full splits of a valid sequence)
+//      split-major, as in plain order; then the rest sequence-major
+//      (sequence b's splits n_min.. in order), kv heads adjacent throughout;
+//   2. each sequence's last, partial split, longest first: ordered by its
+//      length in rounds of UT tokens (one tile for each of the W waves, so
+//      equal rounds are equal work), from the longest class down, sequences
+//      in index order within a class, kv heads adjacent;
+//   3. nothing: the workgroups past the last item return at once.
+// A sequence whose position is invalid (empty context or past max_ctx) gets
+// one item in part 2, split 0, with the shortest class; its workgroup writes
+// the NaN output.  Every (split, sequence, kv head) that the split-K merge
+// counts is exactly one item, so the grid of max_splits * batch * hkv
+// workgroups holds them all.  Returns split * pairs + b * hkv + h, or -1.
+// Lane b of the wave takes sequence b (batch <= kLfMaxBatch = 64 and at most
+// 256 kv heads; other launches keep plain split-major order): one load of
+// the positions, then ballots only, so every lane computes the same,
+// wave-uniform item.
+constexpr int kLfMaxBatch = 64;
+// floor(n / d) for 0 <= n < 2^22 and d > 0 (the operands here: contexts
+// below 2^20, item numbers below 256 splits x 64 sequences x 256 kv heads):
+// the float quotient is within one of it, and one step either way corrects it
+__device__ inline int quot24(int n, int d) {
+  int q = (int)((float)n * __builtin_amdgcn_rcpf((float)d));
+  q += (q + 1) * d <= n ? 1 : (q * d > n ? -1 : 0);
+  return q;
+}
+template <int UT>
+__device__ int longest_first_item(const DecodeArgs& A, int i, int pairs) {
+  constexpr int NQB = 16;  // length classes: split_tokens (<= 2048) / UT (>= 128)
+  const int lane = threadIdx.x & 63;
+  const int ST = A.split_tokens, hkv = A.hkv, B = A.batch;
+  const int ctx = A.positions[min(lane, B - 1)] + 1;  // (lanes past the batch: unused)
+  const bool ok = lane < B && ctx >= 1 && ctx <= A.max_ctx;
+  const int nfull = ok ? quot24(ctx, ST) : 0;  // <= max_splits <= 256: nine bit planes
+  const int r = ok ? ctx - nfull * ST : (lane < B ? 1 : 0);  // tokens of the partial split
+  const int cls = r > 0 ? min((r + UT - 1) / UT, NQB) : 0;  // 0: no partial split
+  // every valid sequence with the same full splits and none partial: plain
+  // split-major order is already longest first
+  const int n0 = __builtin_amdgcn_readfirstlane(nfull);
+  if (__ballot(ok) == __ballot(lane < B) && !__ballot(lane < B && (nfull != n0 || cls > 0)))
+    return i < n0 * pairs ? i : -1;
+  int t = __builtin_amdgcn_readfirstlane(quot24(i, hkv));
+  const int h = i - t * hkv;
+  // set bits of m in the lanes below this one; the lane of the k-th set bit
+  auto below = [&](uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+  };
+  auto select = [&](uint64_t m, int k) {
+    return (int)__builtin_ctzll(__ballot(((m >> lane) & 1) && below(m) == k));
+  };
+  // part 1a: the complete rounds.  n_min, the fewest full splits of a valid
+  // sequence, bit plane by bit plane from the top
+  const uint64_t valid = __ballot(ok);
+  uint64_t cand = valid;
+  int nmin = 0;
+#pragma unroll
+  for (int k = 8; k >= 0; --k) {
+    const uint64_t zero = cand & __ballot(((nfull >> k) & 1) == 0);
+    if (zero) cand = zero;
+    else nmin |= 1 << k;
+  }
+  if (!valid) nmin = 0;  // (no valid sequence: no full split at all)
+  const int nvalid = __popcll(valid);
+  if (t < nmin * nvalid) {  // (nvalid > 0 here)
+    const int split = __builtin_amdgcn_readfirstlane(quot24(t, nvalid));
+    return split * pairs + select(valid, t - split * nvalid) * hkv + h;
+  }
+  t -= nmin * nvalid;
+  // part 1b: the other full splits, sequence-major: the inclusive prefix of
+  // nfull - n_min over the lanes, bit plane by bit plane, and the total
+  const int nrest = ok ? nfull - nmin : 0;
+  int incl = 0, tot = 0;
+#pragma unroll
+  for (int k = 0; k < 9; ++k) {
+    const int bit = (nrest >> k) & 1;
+    const uint64_t m = __ballot(bit);
+    incl += (below(m) + bit) << k;
+    tot += __popcll(m) << k;
+  }
+  if (t < tot) {
+    const int l = (int)__builtin_ctzll(__ballot(incl > t));
+    const int split = nmin + t - __builtin_amdgcn_readlane(incl - nrest, l);
+    return split * pairs + l * hkv + h;
+  }
+  t -= tot;
+  // part 2: the t-th partial split in (class descending, lane) order, by a
+  // radix select over the class's five bit planes
+  cand = __ballot(cls > 0);
+  if (t >= __popcll(cand)) return -1;  // past the last item
+#pragma unroll
+  for (int k = 4; k >= 0; --k) {
+    const uint64_t ones = cand & __ballot((cls >> k) & 1);
+    const int n1 = __popcll(ones);
+    if (t < n1) {
+      cand = ones;
+    } else {
+      t -= n1;
+      cand &= ~ones;
+    }
+  }
+  const int l = select(cand, t);
+  return __builtin_amdgcn_readlane(nfull, l) * pairs + l * hkv + h;
+}
+
 template <int DT, int D, int G, bool APPEND, int W, int NB>
 __device__ void decode_impl(const DecodeArgs& A) {
   using S = DecodeGeo<D>;
@@ -686,8 +799,15 @@ __device__ void decode_impl(const DecodeArgs& A) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave of the workgroup
   const int qi = NOP == 1 ? 0 : w;  // this wave's copy of the step operands
   const int pairs = A.batch * A.hkv;
-  const int split = blockIdx.x / pairs;
-  const int bh = blockIdx.x - split * pairs;
+  // the workgroup's (split, sequence, kv head): split-major, or longest first
+  // (tile-pair kernels with more than one split; the position comes with it)
+  int item = blockIdx.x;  // split * pairs + b * hkv + h
+  if (!T1 && A.max_splits > 1 && A.batch <= kLfMaxBatch && A.hkv <= 256) {
+    item = __builtin_amdgcn_readfirstlane(longest_first_item<WS>(A, item, pairs));
+    if (item < 0) return;
+  }
+  const int split = item / pairs;
+  const int bh = item - split * pairs;
   const int b = bh / A.hkv, h = bh - b * A.hkv;
   const int ST = A.split_tokens;
   const int s_begin = split * ST;

@@ -2,6 +2,8 @@
 oracle, through the C ABI.  Integer/byte work (RoPE'd q and k, cache slots) is
 compared bit for bit; attention outputs within the stated tolerance
 (max-abs 2e-3 fp16, 1e-2 bf16)."""
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -13,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 
 def assert_step_matches(orc, got, want, dtype, gate=None):
-    """Bit-exact cache and roped q/k; attention output within the north-star
+    """Bit-exact cache and roped q/k; attention output within the stated
     tolerance and, where given, within `gate`: a regression bound at about
     ten times the error measured on the same inputs."""
     assert np.array_equal(got["qkv"], want["qkv"]), "RoPE'd q/k differ"
@@ -217,6 +219,52 @@ def test_empty_and_overlong_contexts_give_nan(orc, luc):
     torch.cuda.synchronize()
     o = out.float().cpu().numpy()
     assert np.all(np.isnan(o[1])) and np.all(np.isfinite(o[[0, 2]]))
+
+
+@pytest.mark.parametrize("name,dtype,split", [("batch64_long", "bf16", 512),
+                                               ("batch32_mixed", "f16", 256)])
+def test_longest_first_order_mixed_positions(orc, luc, name, dtype, split):
+    """The tile-pair kernels with several splits per sequence take their work
+    longest first: the full splits, then each sequence's partial last split by
+    length.  A batch mixing contexts that end on a split edge, one token past
+    it, one short of it, short and long ones, an empty context and one past
+    max_ctx gives the oracle's output for every valid sequence and NaN for
+    the others, on two calls in a row on one workspace (the arrival counters
+    left at zero)."""
+    S = split
+    ctxs = [S, S + 1, 3 * S, 3 * S - 1, 17, 1, 2 * S + S // 2, 0, 5 * S + 4, 5 * S, S - 1, 4 * S + 7]
+    max_ctx = 5 * S
+    cfg = wl.scaled(wl.CONFIGS[name], batch=len(ctxs), ctx_lo=max_ctx + 8, ctx_hi=max_ctx + 8)
+    cfg = dataclasses.replace(cfg, dtype=dtype)
+    h = wl.host_decode_inputs(cfg, seed=77, poison=False)
+    pos_np = np.array(ctxs, np.int32) - 1
+    from gpu_util import to_dev
+    from lucciola_rs_amd.engine import sm_scale
+    q = to_dev(h.qkv, dtype)
+    kp, vp = to_dev(h.k_pool, dtype), to_dev(h.v_pool, dtype)
+    tables = torch.from_numpy(h.tables).cuda()
+    pos = torch.from_numpy(pos_np).cuda()
+    ws = luc.workspace(cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, max_ctx, split)
+    outs = []
+    for call in range(2):
+        out = torch.full((cfg.batch, cfg.hq * cfg.head_dim), 7.0, dtype=cfg.torch_dtype, device="cuda")
+        say(f"  [gpu] paged_decode {name} B={cfg.batch} d={cfg.head_dim} {dtype} split {split} "
+            f"max_ctx {max_ctx}, call {call}")
+        luc.paged_decode(out, q, kp, vp, tables, pos, cfg.batch, max_ctx, 0, 1, cfg.hq, cfg.hkv,
+                         cfg.head_dim, sm_scale(cfg.head_dim), split, ws, q_row_stride=cfg.row)
+        torch.cuda.synchronize()
+        outs.append(from_dev(out).reshape(cfg.batch, cfg.hq, cfg.head_dim))
+    assert np.array_equal(outs[0], outs[1]), "the second call differs"
+    o = orc.to_f32(outs[0], dtype)
+    bad = [i for i, c in enumerate(ctxs) if c < 1 or c > max_ctx]
+    good = [i for i in range(len(ctxs)) if i not in bad]
+    assert np.all(np.isnan(o[bad])), "an empty or over-long context without NaN"
+    want = orc.decode_batch(h.qkv[good], h.k_pool, h.v_pool, h.tables[good], pos_np[good], 0,
+                            cfg.hq, cfg.hkv, cfg.head_dim, sm_scale(cfg.head_dim), 16, 1, dtype)
+    assert np.all(np.isfinite(o[good]))
+    err = max_abs(orc, outs[0][good], want, dtype)
+    say(f"  max|hip - oracle| = {err:.3e} over the valid sequences (tol {TOL[dtype]})")
+    assert err <= TOL[dtype]
 
 
 def test_workspace_reuse_across_launches(orc, luc):

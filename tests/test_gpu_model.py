@@ -250,7 +250,7 @@ def report(name, s, steps):
 
 
 def test_greedy_128_steps_attention_swapped(orc):
-    """The north-star greedy check with attention as the only difference:
+    """The 128-step greedy check with attention as the only difference:
     random-init Qwen2.5-0.5B, a 128-token prompt, then 128 greedy steps
     (models.rs:195-240, greedy dispatch :398-405), three times with identical
     GPU GEMMs -- with the oracle's attention (OracleAttentionModel, the

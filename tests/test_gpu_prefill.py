@@ -57,7 +57,7 @@ def oracle_prefill(orc, luc, h: wl.HostPrefill, layer=0, bias=None):
 
 
 def assert_prefill_matches(orc, got, want, dtype, max_frac=0.5):
-    """Bit-exact roped q/k and cache; attention outputs within the north-star
+    """Bit-exact roped q/k and cache; attention outputs within the stated
     max-abs tolerance and within 4 storage units of the oracle's at the row's
     scale (ulp_gate: measured at most ~2.5), with at most `max_frac` of the
     elements differing at all (measured 18-43%)."""
