@@ -56,7 +56,8 @@ def test_decode_every_group_size(orc, luc, group, head_dim, dtype, kernel):
     """Every group size on both kernel shapes: the automatic split of these
     small batches runs the single-tile (_t1) kernels; 256-token splits at
     head_dim 64 and 512 at 128 run the tile-pair (_t2) kernels (two tiles
-    per wave, the head_dim 128 ones with PV on v_dot2), in both dtypes."""
+    per wave; at head_dim 128 the step variants and group size 8 keep PV on
+    v_dot2), in both dtypes."""
     hkv = 2
     cfg = wl.DecodeConfig(f"g{group}", 3, group * hkv, hkv, head_dim, dtype, 1, 900, 3 * 57, 0.5)
     h = wl.host_decode_inputs(cfg, seed=group)
@@ -265,6 +266,32 @@ def test_longest_first_order_mixed_positions(orc, luc, name, dtype, split):
     err = max_abs(orc, outs[0][good], want, dtype)
     say(f"  max|hip - oracle| = {err:.3e} over the valid sequences (tol {TOL[dtype]})")
     assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("batch", [1, 2, 37, 64, 65])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_longest_first_order_batch_sizes(orc, luc, batch, head_dim):
+    """The tile-pair kernels' longest-first work order across batch sizes:
+    one sequence per lane of the ordering wave up to 64, plain split-major
+    order at 65.  Random contexts, a third of those of a split or more cut
+    down to a multiple of the split (only full splits; a context is only
+    ever shortened, so its pages stay allocated), the fused step and the
+    unfused path alike."""
+    hkv, group = 2, 7
+    split = 256 if head_dim == 64 else 512
+    hi = 6 * split
+    cfg = wl.DecodeConfig(f"lf{batch}", batch, group * hkv, hkv, head_dim, "bf16", 1, hi,
+                          batch * (hi // 16 + 1) + 1, 0.5)
+    h = wl.host_decode_inputs(cfg, seed=batch * 7 + head_dim, poison=False)
+    ctx = h.ctx.copy()
+    cut = (np.arange(batch) % 3 == 1) & (ctx >= split)
+    ctx[cut] = ctx[cut] // split * split
+    h = dataclasses.replace(h, ctx=ctx, positions=(ctx - 1).astype(np.int32))
+    want = oracle_step(orc, luc, h)
+    # gate: two bf16 units at |x| < 0.5 (measured at most one)
+    assert_step_matches(orc, gpu_step(luc, h, split_tokens=split), want, "bf16", gate=4e-3)
+    assert_step_matches(orc, gpu_step(luc, h, split_tokens=split, fused=False), want, "bf16",
+                        gate=4e-3)
 
 
 def test_workspace_reuse_across_launches(orc, luc):
