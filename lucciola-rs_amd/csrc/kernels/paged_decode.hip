@@ -1485,22 +1485,26 @@ __device__ void decode_impl(const DecodeArgs& A) {
 
 // Decode kernels: _t1 has 8 waves per workgroup, one tile each (splits of 8
 // tiles; 80 KB of LDS, two workgroups per CU, so four waves per SIMD, which
-// the register target keeps up to group size 7 at head_dim 64 and 6 at 128),
-// _t2 has 4 waves with two
-// tiles in flight each (longer splits).  Resident-wave targets are per SIMD.
-#define LUC_DECODE_KERNELS(DTN, DT, D, G, NB, OCC, W)                                               \
+// the register target keeps up to group size 7 at head_dim 64 and 6 at 128);
+// _t2 has 4 waves with two tiles in flight each (longer splits, two
+// workgroups per CU); _t2w8 the same with 8 waves (one workgroup per CU,
+// about 150 KB of LDS), which the host picks when the launch is a single
+// round of such workgroups: half the splits, so half the partials to merge.
+// Resident-wave targets are per SIMD.
+#define LUC_DECODE_KERNELS(DTN, DT, D, G, NB, OCC, W, SUF)                                          \
   extern "C" __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC)))         \
-  void luc_decode_##DTN##_d##D##_g##G##_t##NB(luc::DecodeArgs a) {                                  \
+  void luc_decode_##DTN##_d##D##_g##G##_t##NB##SUF(luc::DecodeArgs a) {                             \
     luc::decode_impl<DT, D, G, false, W, NB>(a);                                                    \
   }                                                                                                 \
   extern "C" __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(OCC)))         \
-  void luc_decode_step_##DTN##_d##D##_g##G##_t##NB(luc::DecodeArgs a) {                             \
+  void luc_decode_step_##DTN##_d##D##_g##G##_t##NB##SUF(luc::DecodeArgs a) {                        \
     luc::decode_impl<DT, D, G, true, W, NB>(a);                                                     \
   }
 
 #define LUC_DECODE(DTN, DT, D, G)                                                                  \
-  LUC_DECODE_KERNELS(DTN, DT, D, G, 1, ((D == 64 ? G <= 7 : G <= 6) ? 4 : 2), 8)                   \
-  LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2, 4)
+  LUC_DECODE_KERNELS(DTN, DT, D, G, 1, ((D == 64 ? G <= 7 : G <= 6) ? 4 : 2), 8, )                 \
+  LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2, 4, )                                                     \
+  LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2, 8, w8)
 
 #define LUC_DECODE_GROUPS(DTN, DT, D)                                                              \
   LUC_DECODE(DTN, DT, D, 1)                                                                        \

@@ -68,9 +68,12 @@ constexpr const char* kCodeObjects[] = {"rope_append.hsaco", "paged_decode.hsaco
 // registers (128 pages).
 // Waves per workgroup: the single-tile kernels (_t1, one tile per wave)
 // have 8, so a split is 8 tiles; the tile-pair kernels (_t2, longer splits)
-// have 4.  Splits are multiples of 4 tiles.
+// have 4, or 8 (_t2w8) when the launch is a single round of such
+// workgroups (tile_pair_waves).  Splits are multiples of 4 tiles.
 constexpr int kT1Waves = 8;
 constexpr int kT2Waves = 4;
+constexpr int kT2WideWaves = 8;
+constexpr int kCUs = 256;  // the split plan's CU count (MI355X)
 int decode_tile(int head_dim) { return head_dim == 64 ? 64 : 32; }
 constexpr int kMaxSplitTokens = 128 * LUC_BLOCK_SIZE;
 // Tiles the automatic split choice plans to have in flight at once: about two
@@ -216,6 +219,20 @@ int check_cache(const void* k_pool, const void* v_pool, const int32_t* tables, i
 // Splits per sequence are capped at kMaxSplits (the merge's LDS weight table).
 constexpr int kMaxSplits = 256;
 
+// Waves of the tile-pair workgroups for a split of st tokens: 8 (the _t2w8
+// kernels) when the launch is a single round of one such workgroup per CU
+// and each wave gets at least two tiles, else 4.  A single round ends when
+// its workgroups end, so fewer, longer splits (half the partials) win there;
+// over several rounds two 4-wave workgroups per CU hide each other's
+// prologue and merge (batch8_32k, one round: 50.4 us at 2048-token splits
+// on 8 waves against 52.6 at 1024 on 4; batch64_long, 4.8 rounds at 4
+// waves: 207.5 against 202.9).  Depends only on the arguments.
+int tile_pair_waves(int batch, int hkv, int head_dim, int max_ctx, int st) {
+  const int tile = decode_tile(head_dim);
+  if (st % (kT2WideWaves * tile) != 0 || st < 2 * kT2WideWaves * tile) return kT2Waves;
+  return (int64_t)batch * hkv * ceil_div(max_ctx, st) <= kCUs ? kT2WideWaves : kT2Waves;
+}
+
 // Split-K chunk length in tokens: a multiple of 4 tiles (the unit), at most
 // kMaxSplitTokens.  A split of 8 tiles runs the single-tile kernels (_t1:
 // 8 waves, one tile each); every other split the tile-pair kernels (_t2:
@@ -243,6 +260,13 @@ int split_tokens_for(int batch, int hkv, int head_dim, int max_ctx, int requeste
     else st = (int64_t)kT1Waves * decode_tile(head_dim);
   }
   st = std::min<int64_t>(std::max<int64_t>(st, floor_tokens), kMaxSplitTokens);
+  // a 4-wave tile-pair plan of one round (two workgroups per CU): twice the
+  // split on 8-wave workgroups if those fit one round too (half the partials)
+  if (requested <= 0 && st != (int64_t)kT1Waves * decode_tile(head_dim) &&
+      tile_pair_waves(batch, hkv, head_dim, max_ctx, (int)std::min<int64_t>(2 * st, kMaxSplitTokens)) ==
+          kT2WideWaves &&
+      (int64_t)batch * hkv * ceil_div(max_ctx, st) <= 2 * kCUs)
+    st = std::min<int64_t>(2 * st, kMaxSplitTokens);
   return (int)st;
 }
 
@@ -327,12 +351,12 @@ int prepare_decode(const luc_ctx* ctx, int dtype, bool step, void* out, int64_t 
   // must fit the table row
   const bool one_tile = st == kT1Waves * decode_tile(head_dim) &&
                         table_stride >= decode_tile(head_dim) / LUC_BLOCK_SIZE;
+  L->waves = one_tile ? kT1Waves : tile_pair_waves(batch, num_kv_heads, head_dim, max_ctx, st);
   if (int rc = get_fn(ctx, std::string(step ? "luc_decode_step_" : "luc_decode_") + suffix +
-                               (one_tile ? "_t1" : "_t2"),
+                               (one_tile ? "_t1" : L->waves == kT2WideWaves ? "_t2w8" : "_t2"),
                       &L->fn))
     return rc;
   L->grid = dim3((unsigned)grid);
-  L->waves = one_tile ? kT1Waves : kT2Waves;
   luc_decode_args& a = L->a;
   a.q = static_cast<uint16_t*>(const_cast<void*>(q));
   a.q_stride = q_row_stride;
@@ -447,6 +471,7 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
                                 std::to_string(g);
           names.push_back(n + "_t1");
           names.push_back(n + "_t2");
+          names.push_back(n + "_t2w8");
         }
   }
   for (const auto& n : names) {

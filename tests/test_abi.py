@@ -122,9 +122,16 @@ def test_workspace_size_policy(cdll):
     assert ws(32, 14, 2, 64, 4096, 0) == expect(32, 14, 2, 64, 8)
     # ... and longer batches get longer splits, planned for half as many
     # tiles once they need the two-tile kernels (two workgroups per CU):
-    # 8 x 32768 tokens at d=128 -> 1024-token splits
+    # batch64_long (64 x 4 units, 16384 tokens) -> 2048-token splits, several
+    # rounds of 4-wave workgroups
     assert ws(64, 28, 4, 128, 16384, 0) == expect(64, 28, 4, 128, 16384 // 2048)
-    assert ws(8, 12, 2, 128, 32768, 0) == expect(8, 12, 2, 128, 32768 // 1024)
+    # a plan of one round of 4-wave workgroups (8 x 2 units of 32 1024-token
+    # splits) takes twice the split on 8-wave ones if those fit one round
+    # (16 x 16 <= 256 workgroups): batch8_32k -> 2048-token splits
+    assert ws(8, 12, 2, 128, 32768, 0) == expect(8, 12, 2, 128, 32768 // 2048)
+    # ... and keeps its split where they would not: 24 units of 21 768-token
+    # splits (504 4-wave workgroups) would take 24 x 11 > 256 at 1536 tokens
+    assert ws(12, 12, 2, 128, 16000, 0) == expect(12, 12, 2, 128, -(-16000 // 768))
     # a split holds at most 128 pages: longer contexts than 256 x 2048 tokens
     # are not supported
     assert ws(1, 4, 1, 64, 256 * 2048, 0) > 0

@@ -51,17 +51,22 @@ def test_decode_small_configs(orc, luc, name, batch, lo, hi, dtype, fused):
 
 @pytest.mark.parametrize("group", [1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("dtype,kernel", [("bf16", "t1"), ("bf16", "t2"), ("f16", "t2")])
+@pytest.mark.parametrize("dtype,kernel", [("bf16", "t1"), ("bf16", "t2"), ("f16", "t2"),
+                                          ("bf16", "t2w8"), ("f16", "t2w8")])
 def test_decode_every_group_size(orc, luc, group, head_dim, dtype, kernel):
-    """Every group size on both kernel shapes: the automatic split of these
+    """Every group size on every kernel shape: the automatic split of these
     small batches runs the single-tile (_t1) kernels; 256-token splits at
-    head_dim 64 and 512 at 128 run the tile-pair (_t2) kernels (two tiles
-    per wave; at head_dim 128 the step variants and group size 8 keep PV on
-    v_dot2), in both dtypes."""
+    head_dim 64 and 384 at 128 the 4-wave tile-pair (_t2) kernels; 1024 at
+    head_dim 64 and 512 at 128, a multiple of 8 waves' tiles in a launch of
+    one round, the 8-wave ones (_t2w8).  Two tiles per wave; at head_dim 128
+    the step variants and group size 8 keep PV on v_dot2.  Both dtypes."""
     hkv = 2
-    cfg = wl.DecodeConfig(f"g{group}", 3, group * hkv, hkv, head_dim, dtype, 1, 900, 3 * 57, 0.5)
+    hi = 2600 if (kernel, head_dim) == ("t2w8", 64) else 900  # several 1024-token splits
+    cfg = wl.DecodeConfig(f"g{group}", 3, group * hkv, hkv, head_dim, dtype, 1, hi,
+                          3 * (hi // 16 + 1) + 1, 0.5)
     h = wl.host_decode_inputs(cfg, seed=group)
-    split = 0 if kernel == "t1" else (256 if head_dim == 64 else 512)
+    split = {"t1": 0, "t2": 256 if head_dim == 64 else 384,
+             "t2w8": 1024 if head_dim == 64 else 512}[kernel]
     assert_step_matches(orc, gpu_step(luc, h, split_tokens=split), oracle_step(orc, luc, h), dtype)
     assert_step_matches(orc, gpu_step(luc, h, split_tokens=split, fused=False),
                         oracle_step(orc, luc, h), dtype)

@@ -48,11 +48,13 @@ def _pool_changes(before, after):
 
 @pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
 @pytest.mark.parametrize("head_dim,dtype,hq,hkv", [(64, "f16", 14, 2), (128, "bf16", 12, 2)])
-@pytest.mark.parametrize("split", [0, 256, 512])
+@pytest.mark.parametrize("split", [0, 256, 384, 512, 1024])
 def test_decode_never_uses_a_page_outside_the_pool(orc, luc, head_dim, dtype, hq, hkv, split, fused):
     """split 0 and 512 run the single-tile kernels at head_dim 64 (512 tokens =
-    8 tiles of 64) and 256 the tile-pair kernels; at head_dim 128, 0 and 256
-    run the single-tile kernels (8 tiles of 32) and 512 the tile-pair ones.
+    8 tiles of 64), 256 and 384 the 4-wave tile-pair kernels and 1024 the
+    8-wave ones; at head_dim 128, 0 and 256 run the single-tile kernels (8
+    tiles of 32), 384 the 4-wave tile-pair kernels and 512 and 1024 the
+    8-wave ones (a multiple of 8 waves' tiles, one round of workgroups).
     Every sequence's q and k of the new token are roped in place, also where
     the new token's page lies outside the pool (only the cache write is
     skipped), on the fused and the unfused path alike."""
