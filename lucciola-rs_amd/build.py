@@ -24,7 +24,10 @@ LIB = os.path.join(HERE, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-KERNELS = ["rope_append", "paged_decode", "paged_prefill", "model_ops", "sampling", "probe_gather"]
+KERNELS = ["rope_append", "paged_decode", "paged_decode_w8", "paged_prefill", "model_ops", "sampling",
+           "probe_gather"]
+# code objects built from another object's source with extra flags
+KERNEL_SOURCES = {"paged_decode_w8": ("paged_decode", ["-DLUC_DECODE_WIDE"])}
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "--genco", "--no-gpu-bundle-output",
@@ -49,11 +52,12 @@ def _run(cmd, verbose):
 
 
 def build_kernel(name, verbose=False):
-    src = os.path.join(KDIR, name + ".hip")
+    base, defs = KERNEL_SOURCES.get(name, (name, []))
+    src = os.path.join(KDIR, base + ".hip")
     out = os.path.join(LIB, name + ".hsaco")
     tmp = out + ".tmp"
-    _run([os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, *KERNEL_FLAGS.get(name, []), "-I", KDIR, src,
-          "-o", tmp], verbose)
+    _run([os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, *KERNEL_FLAGS.get(name, []), *defs, "-I", KDIR,
+          src, "-o", tmp], verbose)
     os.replace(tmp, out)
     return out
 

@@ -1501,10 +1501,16 @@ __device__ void decode_impl(const DecodeArgs& A) {
     luc::decode_impl<DT, D, G, true, W, NB>(a);                                                     \
   }
 
+// This file builds two code objects: paged_decode.hsaco (the _t1 and _t2
+// kernels) and, with LUC_DECODE_WIDE defined, paged_decode_w8.hsaco (the
+// _t2w8 kernels), compiled in parallel.
+#ifndef LUC_DECODE_WIDE
 #define LUC_DECODE(DTN, DT, D, G)                                                                  \
   LUC_DECODE_KERNELS(DTN, DT, D, G, 1, ((D == 64 ? G <= 7 : G <= 6) ? 4 : 2), 8, )                 \
-  LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2, 4, )                                                     \
-  LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2, 8, w8)
+  LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2, 4, )
+#else
+#define LUC_DECODE(DTN, DT, D, G) LUC_DECODE_KERNELS(DTN, DT, D, G, 2, 2, 8, w8)
+#endif
 
 #define LUC_DECODE_GROUPS(DTN, DT, D)                                                              \
   LUC_DECODE(DTN, DT, D, 1)                                                                        \

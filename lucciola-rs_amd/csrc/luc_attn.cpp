@@ -58,9 +58,10 @@ int fail(int code, const char* fmt, ...) {
     if (e_ != hipSuccess) return fail(LUC_E_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
   } while (0)
 
-constexpr const char* kCodeObjects[] = {"rope_append.hsaco", "paged_decode.hsaco",
-                                         "paged_prefill.hsaco", "model_ops.hsaco",
-                                         "sampling.hsaco", "probe_gather.hsaco"};
+constexpr const char* kCodeObjects[] = {"rope_append.hsaco",   "paged_decode.hsaco",
+                                         "paged_decode_w8.hsaco", "paged_prefill.hsaco",
+                                         "model_ops.hsaco",     "sampling.hsaco",
+                                         "probe_gather.hsaco"};
 
 // Kernel-side constants (kept in step with csrc/kernels/paged_decode.hip):
 // four waves per workgroup, which share one split; tiles of 64 tokens

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_code_objects_built_for_gfx950():
-    for name in ("rope_append", "paged_decode"):
+    for name in ("rope_append", "paged_decode", "paged_decode_w8"):
         path = os.path.join(library.lib_dir(), name + ".hsaco")
         data = open(path, "rb").read()
         assert data[:4] == b"\x7fELF"
