@@ -329,9 +329,11 @@ def model_bench(lib, torch, prompt_len=128, steps=128, eager_steps=8):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    # what a token reads: the one-row products' weights ([out, in], "*_w"),
+    # norms and biases (the transposed copies "*_t" serve prompts only)
     weights = sum(t.numel() * t.element_size() for t in
-                  [m.lm_head_t, m.final_norm] +
-                  [x for L in m.layers for x in L.values()])
+                  [m.lm_head_w, m.final_norm] +
+                  [x for L in m.layers for k, x in L.items() if not k.endswith("_t")])
     mean_ctx = ctx0 + (steps + 1) / 2
     kv = int(mean_ctx) * cfg.num_hidden_layers * 2 * cfg.num_key_value_heads * cfg.head_dim * 2
     per_token = weights + kv

@@ -251,6 +251,17 @@ int luc_paged_prefill(luc_ctx* ctx, void* stream, int dtype, void* qkv, int64_t 
 int luc_rmsnorm(luc_ctx* ctx, void* stream, int dtype, void* out, const void* in,
                 const void* weight, float eps, int rows, int cols);
 
+/* y = x W^T (+ residual) for one row x of k elements and W row-major
+ * [n][k] (bf16): y[i] = round(sum_j x[j] W[i][j] (+ residual[i])), f32
+ * accumulation in a fixed order -- the m = 1 case of Qwen2Model::matmul_bf16
+ * (src/models.rs:251-292, cublasGemmEx with compute type 32F), with residual
+ * as its beta = 1 output (the residual adds, one rounding).  residual may
+ * equal y; x may not overlap y.  k a multiple of 8 in [8, 8192]; x and W
+ * 16-byte aligned.  The decode step's projections (q/k/v, o, gate/up, down)
+ * and lm_head: HBM-bound, every weight byte read once. */
+int luc_gemv(luc_ctx* ctx, void* stream, int dtype, void* y, const void* x, const void* w,
+             const void* residual, int n, int k);
+
 /* In place on rows [gate (intermediate) | up (intermediate)]:
  * gate = round(silu(gate) * up), silu(g) = g / (1 + exp(-g)) in f32 --
  * silu_and_mul_fused_kernel (src/kernels/activation.cu:6-29).

@@ -191,7 +191,77 @@ __device__ void argmax_impl(const uint16_t* x, int n, uint32_t* out) {
   if (t == 0) out[0] = (uint32_t)si[0];
 }
 
+// y[n] = round(sum_k x[k] w[n][k] + res[n]) for one row x of K elements
+// and the N rows of w (row-major [N][K], as the reference's linear weights):
+// the M = 1 case of Qwen2Model::matmul_bf16 (src/models.rs:251-292), f32
+// accumulation; with res the residual the add is its beta = 1 (one rounding).
+// One wave per R rows of w (HBM-bound: every byte of w read once, 16 bytes
+// per lane and load, all of a wave's loads in flight together).  Lane l
+// takes the 8-element chunks c = l, l + 64, ... (C of them at most) of x and
+// of each row; a row's products add in chunk order per lane, element order
+// within a chunk, then over the lanes by a butterfly (xor 32, 16, ..., 1),
+// whose result in lane 0 is stored: a fixed order.  res may alias y (each lane reads its element before
+// writing it); x must not.
+template <int R, int C>
+__device__ void gemv_impl(uint16_t* y, const uint16_t* x, const uint16_t* w, const uint16_t* res,
+                          int n_rows, int k) {
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+  if (n0 >= n_rows) return;  // wave-uniform
+  const int nch = k / 8;
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+  uint4 xv[C], wv[R][C];
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int c = lane + 64 * j;
+    xv[j] = c < nch ? *(const uint4*)(x + 8 * c) : zero;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = min(n0 + r, n_rows - 1);  // (rows past the end re-read the last one)
+    const uint16_t* const wr = w + (int64_t)n * k;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const int c = lane + 64 * j;
+      wv[r][j] = c < nch ? *(const uint4*)(wr + 8 * c) : zero;
+    }
+  }
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < C; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        a = fmaf(St<kBF16>::load(chunk_elem(xv[j], e)), St<kBF16>::load(chunk_elem(wv[r][j], e)), a);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
+    acc[r] = a;
+  }
+  if (lane == 0)  // (the sums in the order lane 0 adds them)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = n0 + r;
+      if (n < n_rows) y[n] = St<kBF16>::store(res ? acc[r] + St<kBF16>::load(res[n]) : acc[r]);
+    }
+}
+
 }  // namespace luc
+
+// Rows per wave and 8-element chunks per lane: four rows of up to 1024
+// elements (the 896-wide hidden state of the q/k/v, o, gate/up and lm_head
+// products) or one row of up to 8192 (the down product's 4864).
+extern "C" __global__ __launch_bounds__(256) void luc_gemv_bf16_r4(uint16_t* y, const uint16_t* x,
+                                                                   const uint16_t* w,
+                                                                   const uint16_t* res, int n, int k) {
+  luc::gemv_impl<4, 2>(y, x, w, res, n, k);
+}
+extern "C" __global__ __launch_bounds__(256) void luc_gemv_bf16_r1(uint16_t* y, const uint16_t* x,
+                                                                   const uint16_t* w,
+                                                                   const uint16_t* res, int n, int k) {
+  luc::gemv_impl<1, 16>(y, x, w, res, n, k);
+}
 
 extern "C" __global__ __launch_bounds__(256) void luc_rmsnorm_bf16(uint16_t* out, const uint16_t* in,
                                                                    const uint16_t* weight, float eps,

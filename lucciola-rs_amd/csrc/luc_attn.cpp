@@ -454,6 +454,7 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
     ctx->modules.push_back(mod);
   }
   std::vector<std::string> names = {"luc_rmsnorm_bf16", "luc_silu_mul_bf16", "luc_embedding_bf16",
+                                    "luc_gemv_bf16_r4",  "luc_gemv_bf16_r1",
                                     "luc_argmax_bf16", "luc_gather_floor_d64",
                                     "luc_gather_floor_d128", "luc_stream_read"};
   for (int npl : {1, 2, 4, 8, 16}) names.push_back("luc_topk_filter_bf16_n" + std::to_string(npl));
@@ -769,6 +770,25 @@ int luc_rmsnorm(luc_ctx* ctx, void* stream, int dtype, void* out, const void* in
   if (int rc = get_fn(ctx, "luc_rmsnorm_bf16", &fn)) return rc;
   void* args[] = {&out, &in, &weight, &eps, &cols};
   return launch(fn, dim3(rows), dim3(256), stream, args);
+}
+
+int luc_gemv(luc_ctx* ctx, void* stream, int dtype, void* y, const void* x, const void* w,
+             const void* residual, int n, int k) {
+  if (!ctx) return fail(LUC_E_INVALID, "null context");
+  if (dtype != LUC_BF16) return fail(LUC_E_UNSUPPORTED, "gemv: bf16 only");
+  if (n < 0) return fail(LUC_E_INVALID, "gemv: n %d < 0", n);
+  if (k < 8 || k > 8192 || k % 8 != 0)
+    return fail(LUC_E_UNSUPPORTED, "gemv: k %d (a multiple of 8 in [8, 8192])", k);
+  if (!y || !x || !w) return fail(LUC_E_INVALID, "gemv: null operand");
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 2) || (residual && !aligned(residual, 2)))
+    return fail(LUC_E_INVALID, "gemv: x and w must be 16-byte aligned");
+  if (n == 0) return LUC_OK;
+  const bool wide = k > 1024;  // one row of up to 8192 per wave, else four of up to 1024
+  hipFunction_t fn;
+  if (int rc = get_fn(ctx, wide ? "luc_gemv_bf16_r1" : "luc_gemv_bf16_r4", &fn)) return rc;
+  const int rows_per_wg = 4 * (wide ? 1 : 4);  // 4 waves per workgroup
+  void* args[] = {&y, const_cast<void**>(&x), const_cast<void**>(&w), const_cast<void**>(&residual), &n, &k};
+  return launch(fn, dim3((unsigned)ceil_div(n, rows_per_wg)), dim3(256), stream, args);
 }
 
 int luc_silu_mul(luc_ctx* ctx, void* stream, int dtype, void* gate_up, int rows, int intermediate) {

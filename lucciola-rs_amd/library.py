@@ -53,6 +53,7 @@ SIGNATURES = {
                                  _i32, _i32, _i32, _f32, _vp, _i64]),
     "luc_rmsnorm": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _f32, _i32, _i32]),
     "luc_silu_mul": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32]),
+    "luc_gemv": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32]),
     "luc_embedding": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32]),
     "luc_argmax": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp]),
     "luc_sort_and_sample": (_i32, [_vp, _vp, _i32, _vp, _i32, _f32, _i32, _f32, _vp, _sz, _vp]),
@@ -261,6 +262,18 @@ class LucAttn:
         cols = x.shape[-1]
         self._check(self.lib.luc_rmsnorm(self.ctx, _stream(stream), dtype_code(x), _p(out), _p(x),
                                          _p(weight), eps, x.numel() // cols, cols))
+
+    def gemv(self, y, x, w, residual=None, stream=None):
+        """luc_gemv: y = x w^T (+ residual) for one row x [k] (or [1, k]) and
+        w [n, k] bf16; residual may be y (an in-place residual add)."""
+        n, k = w.shape
+        if not (w.is_contiguous() and x.is_contiguous() and y.is_contiguous()) or \
+                x.numel() != k or y.numel() != n or \
+                (residual is not None and (residual.numel() != n or not residual.is_contiguous())):
+            raise ValueError(f"gemv: w {tuple(w.shape)}, x {tuple(x.shape)}, y {tuple(y.shape)}: "
+                             "want contiguous x [k], y [n] (and residual [n]) for w [n, k]")
+        self._check(self.lib.luc_gemv(self.ctx, _stream(stream), dtype_code(w), _p(y), _p(x), _p(w),
+                                      _p(residual), n, k))
 
     def silu_mul(self, gate_up, intermediate, stream=None):
         """luc_silu_mul in place on [rows, 2*intermediate] (gate | up) rows."""

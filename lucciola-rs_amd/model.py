@@ -4,7 +4,7 @@ library's kernels.
 
 Per layer (Qwen2Model::forward_layer, models.rs:434-691):
   norm   = rmsnorm(h, input_layernorm)                  luc_rmsnorm
-  qkv    = norm @ qkv_proj^T                            GEMM (hipBLASLt), bf16 out
+  qkv    = norm @ qkv_proj^T                            GEMM, bf16 out (one row: luc_gemv)
   att    = rope + cache write + attention               luc_decode_step (one token)
                                                         / luc_paged_prefill (prompt)
   h      = att @ o_proj^T + h                           GEMM, beta = 1 (one rounding)
@@ -100,9 +100,10 @@ def _dev(bits: np.ndarray, device) -> torch.Tensor:
 
 class Qwen2Model:
     """One sequence through the decoder: `forward(ids, cache_pos)` then
-    `sample_greedy()`, or `generate` (models.rs:184-243).  Every GEMM's weight
-    is held transposed ([in, out], contiguous) so each product is a plain
-    row-major GEMM."""
+    `sample_greedy()`, or `generate` (models.rs:184-243).  The products of a
+    single row (every decode step) are luc_gemv on the weights in the
+    reference's [out, in] layout ("*_w"); those of a prompt are hipBLASLt GEMMs
+    on a transposed copy ([in, out], contiguous: "*_t")."""
 
     def __init__(self, cfg: Qwen2Config, weights: dict, num_blocks: int | None = None,
                  max_positions: int | None = None, device="cuda", lib=None):
@@ -114,20 +115,22 @@ class Qwen2Model:
             raise ValueError(f"unsupported head_dim {d}")
         T = lambda bits: _dev(bits, self.device).t().contiguous()  # noqa: E731  [in, out]
         self.embed = _dev(weights["embed_tokens"], self.device)
-        self.lm_head_t = T(weights.get("lm_head", weights["embed_tokens"]))
+        # [vocab, hidden] for the one-row logits: the embedding when tied
+        self.lm_head_w = _dev(weights["lm_head"], self.device) if "lm_head" in weights else self.embed
         self.final_norm = _dev(weights["final_norm"], self.device)
         self.layers = []
         for lw in weights["layers"]:
             qb = _dev(lw["qkv_bias"], self.device)
             q_dim, k_dim = cfg.hidden_size, cfg.num_key_value_heads * d
+            W = lambda name: _dev(lw[name], self.device)  # noqa: E731  [out, in]
             self.layers.append({
                 "in_norm": _dev(lw["input_layernorm"], self.device),
-                "qkv_t": T(lw["qkv_proj"]),
+                "qkv_t": T(lw["qkv_proj"]), "qkv_w": W("qkv_proj"),
                 "q_bias": qb[:q_dim], "k_bias": qb[q_dim:q_dim + k_dim], "v_bias": qb[q_dim + k_dim:],
-                "o_t": T(lw["o_proj"]),
+                "o_t": T(lw["o_proj"]), "o_w": W("o_proj"),
                 "post_norm": _dev(lw["post_attention_layernorm"], self.device),
-                "gate_up_t": T(lw["gate_up_proj"]),
-                "down_t": T(lw["down_proj"]),
+                "gate_up_t": T(lw["gate_up_proj"]), "gate_up_w": W("gate_up_proj"),
+                "down_t": T(lw["down_proj"]), "down_w": W("down_proj"),
             })
         max_pos = max_positions or cfg.max_position_embeddings
         self.max_positions = max_pos
@@ -175,13 +178,24 @@ class Qwen2Model:
 
     def _layer(self, li, h, attention):
         """One decoder layer on the hidden rows h, which it updates in place
-        (the residual adds are GEMMs with beta = 1 into h: one rounding, and no
-        copy of h into a new output)."""
+        (the residual adds are products with beta = 1 into h: one rounding, and
+        no copy of h into a new output).  One row: luc_gemv; more: GEMMs."""
         cfg = self.cfg
         L = self.layers[li]
         I = cfg.intermediate_size
         norm = torch.empty_like(h)
         self.lib.rmsnorm(norm, h, L["in_norm"], cfg.rms_norm_eps)
+        if h.shape[0] == 1:
+            qkv = torch.empty(1, L["qkv_w"].shape[0], dtype=h.dtype, device=h.device)
+            self.lib.gemv(qkv, norm, L["qkv_w"])
+            att = attention(li, qkv)
+            self.lib.gemv(h, att, L["o_w"], residual=h)
+            self.lib.rmsnorm(norm, h, L["post_norm"], cfg.rms_norm_eps)
+            gate_up = torch.empty(1, 2 * I, dtype=h.dtype, device=h.device)
+            self.lib.gemv(gate_up, norm, L["gate_up_w"])
+            self.lib.silu_mul(gate_up, I)
+            self.lib.gemv(h, gate_up[:, :I], L["down_w"], residual=h)
+            return h
         qkv = torch.mm(norm, L["qkv_t"])
         att = attention(li, qkv)
         h.addmm_(att, L["o_t"])
@@ -219,7 +233,9 @@ class Qwen2Model:
 
     def logits(self) -> torch.Tensor:
         """bf16 logits [1, vocab] of the current hidden state (models.rs:295-342)."""
-        return torch.mm(self.hidden, self.lm_head_t)
+        out = torch.empty(1, self.lm_head_w.shape[0], dtype=torch.bfloat16, device=self.device)
+        self.lib.gemv(out, self.hidden, self.lm_head_w)
+        return out
 
     def sample_greedy(self) -> int:
         self.lib.argmax(self.logits(), self.idx)
@@ -268,7 +284,7 @@ class Qwen2Model:
             for li in range(cfg.num_hidden_layers):
                 h = self._layer(li, h, attention)
             self.lib.rmsnorm(self.hidden, h, self.final_norm, cfg.rms_norm_eps)
-            self.lib.argmax(torch.mm(self.hidden, self.lm_head_t), self.idx)
+            self.lib.argmax(self.logits(), self.idx)
             self.pos.add_(1)
         return graph
 

@@ -61,6 +61,54 @@ def test_silu_mul_matches_oracle(orc, luc):
     assert d.max() <= 1 and np.count_nonzero(d) <= d.size // 1000
 
 
+@pytest.mark.parametrize("n,k,res", [
+    (1152, 896, False),    # q/k/v of Qwen2.5-0.5B
+    (896, 896, True),      # o, residual add in place
+    (9728, 896, False),    # gate | up
+    (896, 4864, True),     # down, residual add in place
+    (1001, 1024, False),   # rows not a multiple of 16, the widest four-row k
+    (37, 1032, True),      # the narrowest one-row k, rows not a multiple of 4
+    (5, 8192, False),      # the widest k
+    (3, 8, True),          # the narrowest k
+])
+def test_gemv_against_f64(luc, n, k, res):
+    """y = x w^T (+ residual) for one bf16 row (models.rs:251-292 at M = 1):
+    f32 products summed in a fixed order, one rounding to bf16.  Against the
+    f64 sum rounded once, an f32 sum of k <= 8192 terms can differ only where
+    the exact result lies within ~k * 2^-24 (relative) of a bf16 rounding
+    boundary: at most one unit, and rarely."""
+    rng = np.random.default_rng(n * 31 + k)
+    x = to_bf16_bits(rng.standard_normal(k))
+    w = to_bf16_bits(rng.standard_normal((n, k)) * 0.05)
+    r = to_bf16_bits(rng.standard_normal(n) * 4) if res else None
+    f = lambda b: (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)  # noqa: E731
+    exact = f(w) @ f(x) + (f(r) if res else 0.0)
+    want = to_bf16_bits(exact.astype(np.float32))  # f64 -> f32 -> bf16: off by one unit at worst
+    tx, tw = to_dev(x, "bf16"), to_dev(w, "bf16")
+    y = to_dev(r, "bf16") if res else torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    say(f"  [gpu] gemv n={n} k={k} residual={res}")
+    luc.gemv(y, tx, tw, residual=y if res else None)
+    torch.cuda.synchronize()
+    d = bf16_ulps(from_dev(y), want)
+    say(f"  max ulp {d.max()}, differing {np.count_nonzero(d)} of {d.size}")
+    assert d.max() <= 1 and np.count_nonzero(d) <= max(2, d.size // 100)
+
+
+def test_gemv_rejects_bad_shapes(luc):
+    """k outside [8, 8192] or not a multiple of 8, and mismatched operands,
+    are refused before any launch."""
+    from lucciola_rs_amd.library import LucError
+    dev = dict(dtype=torch.bfloat16, device="cuda")
+    for k in (12, 8200, 0):
+        w = torch.zeros(4, k, **dev)
+        with pytest.raises(LucError):
+            luc.gemv(torch.empty(4, **dev), torch.zeros(k, **dev), w)
+    with pytest.raises(ValueError):
+        luc.gemv(torch.empty(5, **dev), torch.zeros(64, **dev), torch.zeros(4, 64, **dev))
+    with pytest.raises(ValueError):
+        luc.gemv(torch.empty(4, **dev), torch.zeros(72, **dev), torch.zeros(4, 64, **dev))
+
+
 def test_embedding_gather_and_out_of_range(luc):
     rng = np.random.default_rng(3)
     vocab, hidden = 1000, 896
