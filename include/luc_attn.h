@@ -254,13 +254,32 @@ int luc_rmsnorm(luc_ctx* ctx, void* stream, int dtype, void* out, const void* in
 /* y = x W^T (+ residual) for one row x of k elements and W row-major
  * [n][k] (bf16): y[i] = round(sum_j x[j] W[i][j] (+ residual[i])), f32
  * accumulation in a fixed order -- the m = 1 case of Qwen2Model::matmul_bf16
- * (src/models.rs:251-292, cublasGemmEx with compute type 32F), with residual
+ * (src/models.rs:252-295, cublasGemmEx with compute type 32F), with residual
  * as its beta = 1 output (the residual adds, one rounding).  residual may
  * equal y; x may not overlap y.  k a multiple of 8 in [8, 8192]; x and W
- * 16-byte aligned.  The decode step's projections (q/k/v, o, gate/up, down)
- * and lm_head: HBM-bound, every weight byte read once. */
+ * 16-byte aligned.  The decode step's o and down projections and lm_head:
+ * HBM-bound, every weight byte read once. */
 int luc_gemv(luc_ctx* ctx, void* stream, int dtype, void* y, const void* x, const void* w,
              const void* residual, int n, int k);
+
+/* luc_gemv of x' = luc_rmsnorm(x, norm_weight, eps) (x: one row of k), with
+ * x' formed in registers and never stored: the same bits as luc_rmsnorm then
+ * luc_gemv.  Replaces apply_rmsnorm + matmul_bf16 of one row
+ * (src/models.rs:455-482 for q/k/v, :568-590 for gate/up).  norm_weight
+ * 16-byte aligned. */
+int luc_rmsnorm_gemv(luc_ctx* ctx, void* stream, int dtype, void* y, const void* x,
+                     const void* norm_weight, float eps, const void* w, const void* residual, int n,
+                     int k);
+
+/* act = round(silu(g) * u) (intermediate values) with [g | u] the bf16 rows
+ * x' W^T of W = [gate rows; up rows] ([2 * intermediate][k], the reference's
+ * gate_up_proj) and x' = luc_rmsnorm(x, norm_weight, eps), or x' = x when
+ * norm_weight is NULL: the same bits as luc_rmsnorm, luc_gemv into [g | u]
+ * and luc_silu_mul, without the [g | u] row.  Replaces apply_rmsnorm +
+ * matmul_bf16 + apply_activation_fused of one row (src/models.rs:568-590,
+ * :671).  x and W 16-byte aligned; act may not overlap x. */
+int luc_gate_up_silu(luc_ctx* ctx, void* stream, int dtype, void* act, const void* x,
+                     const void* norm_weight, float eps, const void* w, int intermediate, int k);
 
 /* In place on rows [gate (intermediate) | up (intermediate)]:
  * gate = round(silu(gate) * up), silu(g) = g / (1 + exp(-g)) in f32 --

@@ -1,8 +1,10 @@
-// The Qwen2 model loop's small kernels for gfx950: embedding gather, RMSNorm,
+// The Qwen2 model loop's kernels for gfx950: embedding gather, RMSNorm,
 // fused SiLU * up, greedy argmax -- the reference's batched_embedding_kernel
 // (src/kernels/embedding.cu), rmsnorm_nvidia (src/kernels/rmsnorm.cu),
 // silu_and_mul_fused_kernel (src/kernels/activation.cu) and argmax_kernel
-// (src/kernels/sampling.cu).  bf16 storage, f32 arithmetic.
+// (src/kernels/sampling.cu) -- and the one-row products of a decode step
+// (GEMV, optionally with the RMSNorm of their input and the SiLU * up of their
+// output fused in).  bf16 storage, f32 arithmetic.
 //
 // Fixed arithmetic order, so that a CPU restatement can produce the same bits:
 //   RMSNorm: thread t of 256 sums x*x over its 16-byte chunks c = t, t + 256,
@@ -193,75 +195,180 @@ __device__ void argmax_impl(const uint16_t* x, int n, uint32_t* out) {
 
 // y[n] = round(sum_k x[k] w[n][k] + res[n]) for one row x of K elements
 // and the N rows of w (row-major [N][K], as the reference's linear weights):
-// the M = 1 case of Qwen2Model::matmul_bf16 (src/models.rs:251-292), f32
+// the M = 1 case of Qwen2Model::matmul_bf16 (src/models.rs:252-295), f32
 // accumulation; with res the residual the add is its beta = 1 (one rounding).
-// One wave per R rows of w (HBM-bound: every byte of w read once, 16 bytes
-// per lane and load, all of a wave's loads in flight together).  Lane l
-// takes the 8-element chunks c = l, l + 64, ... (C of them at most) of x and
-// of each row; a row's products add in chunk order per lane, element order
-// within a chunk, then over the lanes by a butterfly (xor 32, 16, ..., 1),
-// whose result in lane 0 is stored: a fixed order.  res may alias y (each lane reads its element before
-// writing it); x must not.
-template <int R, int C>
-__device__ void gemv_impl(uint16_t* y, const uint16_t* x, const uint16_t* w, const uint16_t* res,
-                          int n_rows, int k) {
+// PRE: x is `in` (kGemvPlain), or RMSNorm(in) with weight nw (kGemvNorm),
+// formed in registers by each wave with the bits luc_rmsnorm_bf16 writes:
+// rmsnorm_impl's sum order replayed in one wave -- lane l holds the chunks
+// l + 64 j, i.e. chunk l + 64 j + 256 m of rmsnorm_impl's thread l + 64 j,
+// the chunks a thread adds in increasing order.
+// POST kGemvSiluPair: w holds 2 N rows [gate rows (N) | up rows (N)] and
+// y[n] = round(silu(g) * u), g and u the bf16-rounded products of gate row n
+// and up row n (no res) -- what luc_silu_mul_bf16 makes of the unfused
+// [gate | up] output.  So a fused launch gives the unfused kernels' bits
+// (the reference's apply_rmsnorm + matmul_bf16, models.rs:455-482 and
+// :568-590, and apply_activation_fused, :671).
+// One wave per R rows of w at a time (HBM-bound: every byte of w read once,
+// 16 bytes per lane and load, all of a wave's loads of a group in flight
+// together); the waves stride over the row groups.  Lane l takes the 8-element
+// chunks c = l, l + 64, ... (C of them at most); a row's products add in chunk
+// order per lane, element order within a chunk, then over the lanes: the
+// upper 32 lanes onto the lower (permlane32 swap), the odd 16-lane rows onto
+// the even (permlane16 swap), then the 16 lanes of a row (quad xor 1, quad
+// xor 2, half mirror, mirror) -- a fixed order.  With R = 4 (R = 2) the swaps
+// also gather the rows: lanes [64 r / R, 64 (r + 1) / R) end holding the sum
+// of the wave's row r.  res may alias y (a row's value is read before it is
+// written, by the same lane); in must not.
+enum GemvPre { kGemvPlain = 0, kGemvNorm = 1 };
+enum GemvPost { kGemvStore = 0, kGemvSiluPair = 1 };
+
+template <int R, int C, int PRE, int POST>
+__device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, const uint16_t* res,
+                          const uint16_t* nw, float eps, int n_out, int k) {
+#pragma clang fp contract(off)
+  static_assert(R == 1 || R == 2 || R == 4, "rows per wave");
+  static_assert(POST == kGemvStore || R >= 2, "a silu pair takes two rows");
+  constexpr int kOut = POST == kGemvSiluPair ? R / 2 : R;  // outputs per wave and group
   const int lane = threadIdx.x & 63;
-  const int n0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
-  if (n0 >= n_rows) return;  // wave-uniform
+  const int wpg = blockDim.x >> 6;
+  const int wave = blockIdx.x * wpg + (threadIdx.x >> 6);
+  const int stride = gridDim.x * wpg * kOut;
+  if (wave * kOut >= n_out) return;  // wave-uniform
   const int nch = k / 8;
   const uint4 zero = make_uint4(0, 0, 0, 0);
-  uint4 xv[C], wv[R][C];
+  uint4 xv[C];
 #pragma unroll
   for (int j = 0; j < C; ++j) {
     const int c = lane + 64 * j;
-    xv[j] = c < nch ? *(const uint4*)(x + 8 * c) : zero;
+    xv[j] = c < nch ? *(const uint4*)(in + 8 * c) : zero;
   }
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int n = min(n0 + r, n_rows - 1);  // (rows past the end re-read the last one)
-    const uint16_t* const wr = w + (int64_t)n * k;
+  if constexpr (PRE == kGemvNorm) {
+    uint4 nv[C];
 #pragma unroll
     for (int j = 0; j < C; ++j) {
       const int c = lane + 64 * j;
-      wv[r][j] = c < nch ? *(const uint4*)(wr + 8 * c) : zero;
+      nv[j] = c < nch ? *(const uint4*)(nw + 8 * c) : zero;
     }
-  }
-  float acc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    float a = 0.0f;
+    float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // rmsnorm_impl's threads lane + 64 i
 #pragma unroll
     for (int j = 0; j < C; ++j)
+      if (lane + 64 * j < nch)
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        a = fmaf(St<kBF16>::load(chunk_elem(xv[j], e)), St<kBF16>::load(chunk_elem(wv[r][j], e)), a);
+        for (int e = 0; e < 8; ++e) {
+          const float f = St<kBF16>::load(chunk_elem(xv[j], e));
+          p[j & 3] = fmaf(f, f, p[j & 3]);
+        }
+    float a = (p[0] + p[2]) + (p[1] + p[3]);
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
-    acc[r] = a;
+    for (int h = 32; h > 0; h >>= 1) a = a + __shfl_down(a, h);
+    const float sum = readlane(a, 0);
+    const float inv = 1.0f / sqrtf(sum / (float)k + eps);
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      uint16_t o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = St<kBF16>::load(chunk_elem(xv[j], e)) * inv;
+        o[e] = St<kBF16>::store(f * St<kBF16>::load(chunk_elem(nv[j], e)));
+      }
+      xv[j] = chunk_pack(o);
+    }
   }
-  if (lane == 0)  // (the sums in the order lane 0 adds them)
+  for (int n0 = wave * kOut; n0 < n_out; n0 += stride) {
+    uint4 wv[R][C];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int n = n0 + r;
-      if (n < n_rows) y[n] = St<kBF16>::store(res ? acc[r] + St<kBF16>::load(res[n]) : acc[r]);
+      // (rows past the end re-read the last one)
+      const int n = POST == kGemvSiluPair ? (r < kOut ? 0 : n_out) + min(n0 + r % kOut, n_out - 1)
+                                          : min(n0 + r, n_out - 1);
+      const uint16_t* const wr = w + (int64_t)n * k;
+#pragma unroll
+      for (int j = 0; j < C; ++j) {
+        const int c = lane + 64 * j;
+        wv[r][j] = c < nch ? *(const uint4*)(wr + 8 * c) : zero;
+      }
     }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float a = 0.0f;
+#pragma unroll
+      for (int j = 0; j < C; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          a = fmaf(St<kBF16>::load(chunk_elem(xv[j], e)), St<kBF16>::load(chunk_elem(wv[r][j], e)), a);
+      acc[r] = a;
+    }
+    // lanes l and l + 32, then 16-lane rows 2i and 2i + 1, then a row's 16 lanes
+    float s;
+    if constexpr (R == 4) {
+      const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0]), __float_as_uint(acc[2]),
+                                                        false, false);
+      const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[1]), __float_as_uint(acc[3]),
+                                                        false, false);
+      // h02: rows 0 (lanes < 32) and 2; h13: rows 1 and 3
+      const float h02 = __uint_as_float(s02[0]) + __uint_as_float(s02[1]);
+      const float h13 = __uint_as_float(s13[0]) + __uint_as_float(s13[1]);
+      const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(h02), __float_as_uint(h13), false, false);
+      s = __uint_as_float(q[0]) + __uint_as_float(q[1]);  // 16-lane row r: row r
+    } else if constexpr (R == 2) {
+      const auto s01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0]), __float_as_uint(acc[1]),
+                                                        false, false);
+      const float h = __uint_as_float(s01[0]) + __uint_as_float(s01[1]);  // lanes < 32: row 0
+      const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(h), __float_as_uint(h), false, false);
+      s = __uint_as_float(q[0]) + __uint_as_float(q[1]);  // lanes < 32: row 0; the rest: row 1
+    } else {
+      const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0]), __float_as_uint(acc[0]),
+                                                       false, false);
+      const float h = __uint_as_float(s0[0]) + __uint_as_float(s0[1]);
+      const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(h), __float_as_uint(h), false, false);
+      s = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+    }
+    s = row_sum16(s);
+    constexpr int kLanesPerRow = 64 / R;
+    if constexpr (POST == kGemvSiluPair) {
+      // the up rows' sums sit 32 lanes above their gate rows'
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+      if (lane < 32 && (lane & (kLanesPerRow - 1)) == 0) {
+        const int n = n0 + lane / kLanesPerRow;
+        if (n < n_out) {
+          const float g = St<kBF16>::load(St<kBF16>::store(s));
+          const float u = St<kBF16>::load(St<kBF16>::store(__uint_as_float(sw[1])));
+          const float sg = g / (1.0f + expf(-g));
+          y[n] = St<kBF16>::store(sg * u);
+        }
+      }
+    } else if ((lane & (kLanesPerRow - 1)) == 0) {
+      const int n = n0 + lane / kLanesPerRow;
+      if (n < n_out) y[n] = St<kBF16>::store(res ? s + St<kBF16>::load(res[n]) : s);
+    }
+  }
 }
 
 }  // namespace luc
 
-// Rows per wave and 8-element chunks per lane: four rows of up to 1024
-// elements (the 896-wide hidden state of the q/k/v, o, gate/up and lm_head
-// products) or one row of up to 8192 (the down product's 4864).
-extern "C" __global__ __launch_bounds__(256) void luc_gemv_bf16_r4(uint16_t* y, const uint16_t* x,
-                                                                   const uint16_t* w,
-                                                                   const uint16_t* res, int n, int k) {
-  luc::gemv_impl<4, 2>(y, x, w, res, n, k);
-}
-extern "C" __global__ __launch_bounds__(256) void luc_gemv_bf16_r1(uint16_t* y, const uint16_t* x,
-                                                                   const uint16_t* w,
-                                                                   const uint16_t* res, int n, int k) {
-  luc::gemv_impl<1, 16>(y, x, w, res, n, k);
-}
+// Rows per wave R and 8-element chunks per lane C (rows of up to 512 C
+// elements): four rows, or one, of up to 1024 elements (the 896-wide hidden
+// state of the q/k/v, o, gate/up and lm_head products; one row when there
+// are few rows), or one row of up to 8192 (the down product's 4864); the
+// gate/up pairs two or four rows (one or two outputs).
+#define LUC_GEMV_KERNEL(NAME, PRE, POST, R, C)                                                    \
+  extern "C" __global__ __launch_bounds__(256) void NAME(uint16_t* y, const uint16_t* in,         \
+                                                         const uint16_t* w, const uint16_t* res,  \
+                                                         const uint16_t* nw, float eps, int n,    \
+                                                         int k) {                                 \
+    luc::gemv_impl<R, C, PRE, POST>(y, in, w, res, nw, eps, n, k);                                \
+  }
+LUC_GEMV_KERNEL(luc_gemv_bf16_r4c2, luc::kGemvPlain, luc::kGemvStore, 4, 2)
+LUC_GEMV_KERNEL(luc_gemv_bf16_r1c2, luc::kGemvPlain, luc::kGemvStore, 1, 2)
+LUC_GEMV_KERNEL(luc_gemv_bf16_r1c16, luc::kGemvPlain, luc::kGemvStore, 1, 16)
+LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r4c2, luc::kGemvNorm, luc::kGemvStore, 4, 2)
+LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r1c2, luc::kGemvNorm, luc::kGemvStore, 1, 2)
+LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r1c16, luc::kGemvNorm, luc::kGemvStore, 1, 16)
+LUC_GEMV_KERNEL(luc_gate_up_silu_bf16_r4c2, luc::kGemvPlain, luc::kGemvSiluPair, 4, 2)
+LUC_GEMV_KERNEL(luc_gate_up_silu_bf16_r2c16, luc::kGemvPlain, luc::kGemvSiluPair, 2, 16)
+LUC_GEMV_KERNEL(luc_rmsnorm_gate_up_silu_bf16_r4c2, luc::kGemvNorm, luc::kGemvSiluPair, 4, 2)
+LUC_GEMV_KERNEL(luc_rmsnorm_gate_up_silu_bf16_r2c16, luc::kGemvNorm, luc::kGemvSiluPair, 2, 16)
 
 extern "C" __global__ __launch_bounds__(256) void luc_rmsnorm_bf16(uint16_t* out, const uint16_t* in,
                                                                    const uint16_t* weight, float eps,

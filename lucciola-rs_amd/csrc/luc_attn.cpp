@@ -454,10 +454,13 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
     ctx->modules.push_back(mod);
   }
   std::vector<std::string> names = {"luc_rmsnorm_bf16", "luc_silu_mul_bf16", "luc_embedding_bf16",
-                                    "luc_gemv_bf16_r4",  "luc_gemv_bf16_r1",
                                     "luc_argmax_bf16", "luc_gather_floor_d64",
                                     "luc_gather_floor_d128", "luc_stream_read"};
   for (int npl : {1, 2, 4, 8, 16}) names.push_back("luc_topk_filter_bf16_n" + std::to_string(npl));
+  for (const char* kind : {"luc_gemv", "luc_rmsnorm_gemv"})
+    for (const char* v : {"_bf16_r4c2", "_bf16_r1c2", "_bf16_r1c16"}) names.push_back(std::string(kind) + v);
+  for (const char* kind : {"luc_gate_up_silu", "luc_rmsnorm_gate_up_silu"})
+    for (const char* v : {"_bf16_r4c2", "_bf16_r2c16"}) names.push_back(std::string(kind) + v);
   for (int k = 32; k <= 1024; k *= 2) names.push_back("luc_top_p_sample_" + std::to_string(k));
   for (const char* dt : {"bf16", "f16"}) {
     names.push_back(std::string("luc_rope_append_") + dt);
@@ -772,23 +775,66 @@ int luc_rmsnorm(luc_ctx* ctx, void* stream, int dtype, void* out, const void* in
   return launch(fn, dim3(rows), dim3(256), stream, args);
 }
 
+namespace {
+// The one-row products: `kind` names the kernel family, all with the
+// arguments (y, in, w, res, norm weight, eps, outputs, k).  Variant by shape:
+// rows of k <= 1024 on four rows per wave when there are at least 4096 of them
+// (lm_head), else on one row per wave (q/k/v, o: four times the waves to fill
+// the chip with); rows of k <= 8192 on one row per wave.  The gate/up silu
+// pairs (`pair`) take two rows per output: four rows per wave for k <= 1024,
+// else two.  4 waves per workgroup, at most 8 workgroups per CU (the waves
+// then stride over the row groups).
+int gemv_launch(luc_ctx* ctx, void* stream, const char* kind, bool pair, void* y, const void* in,
+                const void* w, const void* residual, const void* norm_weight, float eps, int n, int k) {
+  if (n < 0) return fail(LUC_E_INVALID, "%s: n %d < 0", kind, n);
+  if (k < 8 || k > 8192 || k % 8 != 0)
+    return fail(LUC_E_UNSUPPORTED, "%s: k %d (a multiple of 8 in [8, 8192])", kind, k);
+  if (!y || !in || !w) return fail(LUC_E_INVALID, "%s: null operand", kind);
+  if (!aligned(in, 16) || !aligned(w, 16) || (norm_weight && !aligned(norm_weight, 16)) || !aligned(y, 2) ||
+      (residual && !aligned(residual, 2)))
+    return fail(LUC_E_INVALID, "%s: the input row, w and the norm weight must be 16-byte aligned", kind);
+  if (n == 0) return LUC_OK;
+  if (int rc = check_device(ctx)) return rc;
+  int outs_per_wave;
+  const char* variant;
+  if (pair) {
+    outs_per_wave = k <= 1024 ? 2 : 1;
+    variant = k <= 1024 ? "_bf16_r4c2" : "_bf16_r2c16";
+  } else {
+    outs_per_wave = k <= 1024 && n >= 4096 ? 4 : 1;
+    variant = k > 1024 ? "_bf16_r1c16" : outs_per_wave == 4 ? "_bf16_r4c2" : "_bf16_r1c2";
+  }
+  hipFunction_t fn;
+  if (int rc = get_fn(ctx, std::string(kind) + variant, &fn)) return rc;
+  const int64_t wgs = std::min<int64_t>(ceil_div(n, 4 * outs_per_wave), 8 * std::max(ctx->num_cus, 1));
+  void* args[] = {&y, const_cast<void**>(&in), const_cast<void**>(&w), const_cast<void**>(&residual),
+                  const_cast<void**>(&norm_weight), &eps, &n, &k};
+  return launch(fn, dim3((unsigned)wgs), dim3(256), stream, args);
+}
+}  // namespace
+
 int luc_gemv(luc_ctx* ctx, void* stream, int dtype, void* y, const void* x, const void* w,
              const void* residual, int n, int k) {
   if (!ctx) return fail(LUC_E_INVALID, "null context");
   if (dtype != LUC_BF16) return fail(LUC_E_UNSUPPORTED, "gemv: bf16 only");
-  if (n < 0) return fail(LUC_E_INVALID, "gemv: n %d < 0", n);
-  if (k < 8 || k > 8192 || k % 8 != 0)
-    return fail(LUC_E_UNSUPPORTED, "gemv: k %d (a multiple of 8 in [8, 8192])", k);
-  if (!y || !x || !w) return fail(LUC_E_INVALID, "gemv: null operand");
-  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 2) || (residual && !aligned(residual, 2)))
-    return fail(LUC_E_INVALID, "gemv: x and w must be 16-byte aligned");
-  if (n == 0) return LUC_OK;
-  const bool wide = k > 1024;  // one row of up to 8192 per wave, else four of up to 1024
-  hipFunction_t fn;
-  if (int rc = get_fn(ctx, wide ? "luc_gemv_bf16_r1" : "luc_gemv_bf16_r4", &fn)) return rc;
-  const int rows_per_wg = 4 * (wide ? 1 : 4);  // 4 waves per workgroup
-  void* args[] = {&y, const_cast<void**>(&x), const_cast<void**>(&w), const_cast<void**>(&residual), &n, &k};
-  return launch(fn, dim3((unsigned)ceil_div(n, rows_per_wg)), dim3(256), stream, args);
+  return gemv_launch(ctx, stream, "luc_gemv", false, y, x, w, residual, nullptr, 0.0f, n, k);
+}
+
+int luc_rmsnorm_gemv(luc_ctx* ctx, void* stream, int dtype, void* y, const void* x,
+                     const void* norm_weight, float eps, const void* w, const void* residual, int n,
+                     int k) {
+  if (!ctx) return fail(LUC_E_INVALID, "null context");
+  if (dtype != LUC_BF16) return fail(LUC_E_UNSUPPORTED, "rmsnorm_gemv: bf16 only");
+  if (!norm_weight) return fail(LUC_E_INVALID, "rmsnorm_gemv: null norm weight");
+  return gemv_launch(ctx, stream, "luc_rmsnorm_gemv", false, y, x, w, residual, norm_weight, eps, n, k);
+}
+
+int luc_gate_up_silu(luc_ctx* ctx, void* stream, int dtype, void* act, const void* x,
+                     const void* norm_weight, float eps, const void* w, int intermediate, int k) {
+  if (!ctx) return fail(LUC_E_INVALID, "null context");
+  if (dtype != LUC_BF16) return fail(LUC_E_UNSUPPORTED, "gate_up_silu: bf16 only");
+  return gemv_launch(ctx, stream, norm_weight ? "luc_rmsnorm_gate_up_silu" : "luc_gate_up_silu", true,
+                     act, x, w, nullptr, norm_weight, eps, intermediate, k);
 }
 
 int luc_silu_mul(luc_ctx* ctx, void* stream, int dtype, void* gate_up, int rows, int intermediate) {

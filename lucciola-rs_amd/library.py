@@ -54,6 +54,8 @@ SIGNATURES = {
     "luc_rmsnorm": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _f32, _i32, _i32]),
     "luc_silu_mul": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32]),
     "luc_gemv": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32]),
+    "luc_rmsnorm_gemv": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _f32, _vp, _vp, _i32, _i32]),
+    "luc_gate_up_silu": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _f32, _vp, _i32, _i32]),
     "luc_embedding": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32]),
     "luc_argmax": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp]),
     "luc_sort_and_sample": (_i32, [_vp, _vp, _i32, _vp, _i32, _f32, _i32, _f32, _vp, _sz, _vp]),
@@ -263,17 +265,42 @@ class LucAttn:
         self._check(self.lib.luc_rmsnorm(self.ctx, _stream(stream), dtype_code(x), _p(out), _p(x),
                                          _p(weight), eps, x.numel() // cols, cols))
 
-    def gemv(self, y, x, w, residual=None, stream=None):
-        """luc_gemv: y = x w^T (+ residual) for one row x [k] (or [1, k]) and
-        w [n, k] bf16; residual may be y (an in-place residual add)."""
+    @staticmethod
+    def _gemv_shapes(name, y, x, w, residual):
         n, k = w.shape
         if not (w.is_contiguous() and x.is_contiguous() and y.is_contiguous()) or \
                 x.numel() != k or y.numel() != n or \
                 (residual is not None and (residual.numel() != n or not residual.is_contiguous())):
-            raise ValueError(f"gemv: w {tuple(w.shape)}, x {tuple(x.shape)}, y {tuple(y.shape)}: "
+            raise ValueError(f"{name}: w {tuple(w.shape)}, x {tuple(x.shape)}, y {tuple(y.shape)}: "
                              "want contiguous x [k], y [n] (and residual [n]) for w [n, k]")
+        return n, k
+
+    def gemv(self, y, x, w, residual=None, stream=None):
+        """luc_gemv: y = x w^T (+ residual) for one row x [k] (or [1, k]) and
+        w [n, k] bf16; residual may be y (an in-place residual add)."""
+        n, k = self._gemv_shapes("gemv", y, x, w, residual)
         self._check(self.lib.luc_gemv(self.ctx, _stream(stream), dtype_code(w), _p(y), _p(x), _p(w),
                                       _p(residual), n, k))
+
+    def rmsnorm_gemv(self, y, x, norm_weight, eps, w, residual=None, stream=None):
+        """luc_rmsnorm_gemv: y = rmsnorm(x) w^T (+ residual), one row x [k]."""
+        n, k = self._gemv_shapes("rmsnorm_gemv", y, x, w, residual)
+        if norm_weight.numel() != k:
+            raise ValueError(f"rmsnorm_gemv: norm weight of {norm_weight.numel()}, k {k}")
+        self._check(self.lib.luc_rmsnorm_gemv(self.ctx, _stream(stream), dtype_code(w), _p(y), _p(x),
+                                              _p(norm_weight), eps, _p(w), _p(residual), n, k))
+
+    def gate_up_silu(self, act, x, norm_weight, eps, w, stream=None):
+        """luc_gate_up_silu: act [I] = silu(g) * u of [g | u] = rmsnorm(x) w^T
+        (x itself when norm_weight is None), w [2 I, k] = [gate; up]."""
+        two_i, k = w.shape
+        if two_i % 2 or not (w.is_contiguous() and x.is_contiguous() and act.is_contiguous()) or \
+                x.numel() != k or act.numel() != two_i // 2 or \
+                (norm_weight is not None and norm_weight.numel() != k):
+            raise ValueError(f"gate_up_silu: w {tuple(w.shape)}, x {tuple(x.shape)}, act {tuple(act.shape)}: "
+                             "want contiguous x [k], act [I] for w [2 I, k]")
+        self._check(self.lib.luc_gate_up_silu(self.ctx, _stream(stream), dtype_code(w), _p(act), _p(x),
+                                              _p(norm_weight), eps, _p(w), two_i // 2, k))
 
     def silu_mul(self, gate_up, intermediate, stream=None):
         """luc_silu_mul in place on [rows, 2*intermediate] (gate | up) rows."""

@@ -4,7 +4,7 @@ library's kernels.
 
 Per layer (Qwen2Model::forward_layer, models.rs:434-691):
   norm   = rmsnorm(h, input_layernorm)                  luc_rmsnorm
-  qkv    = norm @ qkv_proj^T                            GEMM, bf16 out (one row: luc_gemv)
+  qkv    = norm @ qkv_proj^T                            GEMM, bf16 out
   att    = rope + cache write + attention               luc_decode_step (one token)
                                                         / luc_paged_prefill (prompt)
   h      = att @ o_proj^T + h                           GEMM, beta = 1 (one rounding)
@@ -12,6 +12,10 @@ Per layer (Qwen2Model::forward_layer, models.rs:434-691):
   gu     = norm @ gate_up_proj^T                        GEMM
   gate   = silu(gate) * up                              luc_silu_mul
   h      = gate @ down_proj^T + h                       GEMM, beta = 1
+For one row (a decode step) the products are GEMVs with the norms and silu * up
+fused into them, five launches a layer with the same bits as the unfused ones:
+luc_rmsnorm_gemv (q/k/v), luc_decode_step, luc_gemv (o, + h),
+luc_gate_up_silu (norm, gate/up, silu * up), luc_gemv (down, + h).
 then h = rmsnorm(h, norm) (models.rs:765-771, 815-822), logits = h @ lm_head^T
 (bf16, models.rs:295-342) and greedy sampling by luc_argmax (models.rs:344-360).
 The q/k biases enter in the RoPE step and the v bias in the cache write, as in
@@ -183,23 +187,22 @@ class Qwen2Model:
         cfg = self.cfg
         L = self.layers[li]
         I = cfg.intermediate_size
-        norm = torch.empty_like(h)
-        self.lib.rmsnorm(norm, h, L["in_norm"], cfg.rms_norm_eps)
-        if h.shape[0] == 1:
+        eps = cfg.rms_norm_eps
+        if h.shape[0] == 1:  # the norms and silu * up fused into the products
             qkv = torch.empty(1, L["qkv_w"].shape[0], dtype=h.dtype, device=h.device)
-            self.lib.gemv(qkv, norm, L["qkv_w"])
+            self.lib.rmsnorm_gemv(qkv, h, L["in_norm"], eps, L["qkv_w"])
             att = attention(li, qkv)
             self.lib.gemv(h, att, L["o_w"], residual=h)
-            self.lib.rmsnorm(norm, h, L["post_norm"], cfg.rms_norm_eps)
-            gate_up = torch.empty(1, 2 * I, dtype=h.dtype, device=h.device)
-            self.lib.gemv(gate_up, norm, L["gate_up_w"])
-            self.lib.silu_mul(gate_up, I)
-            self.lib.gemv(h, gate_up[:, :I], L["down_w"], residual=h)
+            act = torch.empty(1, I, dtype=h.dtype, device=h.device)
+            self.lib.gate_up_silu(act, h, L["post_norm"], eps, L["gate_up_w"])
+            self.lib.gemv(h, act, L["down_w"], residual=h)
             return h
+        norm = torch.empty_like(h)
+        self.lib.rmsnorm(norm, h, L["in_norm"], eps)
         qkv = torch.mm(norm, L["qkv_t"])
         att = attention(li, qkv)
         h.addmm_(att, L["o_t"])
-        self.lib.rmsnorm(norm, h, L["post_norm"], cfg.rms_norm_eps)
+        self.lib.rmsnorm(norm, h, L["post_norm"], eps)
         gate_up = torch.mm(norm, L["gate_up_t"])
         self.lib.silu_mul(gate_up, I)
         return h.addmm_(gate_up[:, :I], L["down_t"])

@@ -94,6 +94,62 @@ def test_gemv_against_f64(luc, n, k, res):
     assert d.max() <= 1 and np.count_nonzero(d) <= max(2, d.size // 100)
 
 
+@pytest.mark.parametrize("n,k,res", [
+    (1152, 896, False), (9728, 896, True), (37, 4864, False), (5, 8192, True), (3, 8, False),
+    (4096, 1024, False), (7, 1032, True),
+])
+def test_rmsnorm_gemv_equals_unfused(luc, n, k, res):
+    """luc_rmsnorm_gemv forms RMSNorm(x) in each wave with luc_rmsnorm's
+    arithmetic order, so it must give luc_rmsnorm then luc_gemv bit for bit."""
+    rng = np.random.default_rng(n * 7 + k)
+    x = to_bf16_bits(rng.standard_normal(k) * rng.uniform(0.1, 30))
+    nw = to_bf16_bits(1 + 0.1 * rng.standard_normal(k))
+    w = to_bf16_bits(rng.standard_normal((n, k)) * 0.05)
+    r = to_bf16_bits(rng.standard_normal(n)) if res else np.zeros(n, np.uint16)
+    tx, tn, tw = to_dev(x, "bf16"), to_dev(nw, "bf16"), to_dev(w, "bf16")
+    y1, y2 = to_dev(r, "bf16"), to_dev(r, "bf16")
+    norm = torch.empty_like(tx)
+    say(f"  [gpu] rmsnorm_gemv n={n} k={k} residual={res}")
+    luc.rmsnorm(norm, tx, tn, 1e-6)
+    luc.gemv(y1, norm, tw, residual=y1 if res else None)
+    luc.rmsnorm_gemv(y2, tx, tn, 1e-6, tw, residual=y2 if res else None)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_dev(y1), from_dev(y2))
+
+
+@pytest.mark.parametrize("inter,k,norm", [
+    (4864, 896, True),     # Qwen2.5-0.5B's gate/up
+    (4864, 896, False), (1001, 1024, True), (3, 8, True), (37, 1032, False), (5, 8192, True),
+])
+def test_gate_up_silu_equals_unfused(luc, inter, k, norm):
+    """luc_gate_up_silu rounds each gate and up product to bf16 and applies
+    luc_silu_mul's arithmetic to the pair, so it must give luc_rmsnorm (or
+    nothing), luc_gemv into [gate | up] and luc_silu_mul bit for bit.  (The
+    unfused pair runs on gate and up padded to a multiple of 8 rows, which
+    luc_silu_mul needs.)"""
+    rng = np.random.default_rng(inter * 3 + k)
+    x = to_bf16_bits(rng.standard_normal(k) * rng.uniform(0.1, 30))
+    nw = to_bf16_bits(1 + 0.1 * rng.standard_normal(k))
+    pad = -(-inter // 8) * 8
+    w = to_bf16_bits(rng.standard_normal((2, pad, k)) * (2.0 / np.sqrt(k)))
+    tx, tn = to_dev(x, "bf16"), to_dev(nw, "bf16")
+    tw, tw_pad = to_dev(w[:, :inter].reshape(2 * inter, k), "bf16"), to_dev(w.reshape(2 * pad, k), "bf16")
+    dev = dict(dtype=torch.bfloat16, device="cuda")
+    say(f"  [gpu] gate_up_silu inter={inter} k={k} norm={norm}")
+    xn = torch.empty_like(tx)
+    if norm:
+        luc.rmsnorm(xn, tx, tn, 1e-6)
+    else:
+        xn.copy_(tx)
+    gu = torch.empty(2 * pad, **dev)
+    luc.gemv(gu, xn, tw_pad)
+    luc.silu_mul(gu, pad)
+    act = torch.full((inter,), float("nan"), **dev)
+    luc.gate_up_silu(act, tx, tn if norm else None, 1e-6, tw)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_dev(act), from_dev(gu[:inter]))
+
+
 def test_gemv_rejects_bad_shapes(luc):
     """k outside [8, 8192] or not a multiple of 8, and mismatched operands,
     are refused before any launch."""
