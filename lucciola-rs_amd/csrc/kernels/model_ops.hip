@@ -208,19 +208,33 @@ __device__ void argmax_impl(const uint16_t* x, int n, uint32_t* out) {
 // [gate | up] output.  So a fused launch gives the unfused kernels' bits
 // (the reference's apply_rmsnorm + matmul_bf16, models.rs:455-482 and
 // :568-590, and apply_activation_fused, :671).
-// One wave per R rows of w at a time (HBM-bound: every byte of w read once,
-// 16 bytes per lane and load, all of a wave's loads of a group in flight
-// together); the waves stride over the row groups.  Lane l takes the 8-element
+// One wave per R rows of w (HBM-bound: every byte of w read once, 16 bytes
+// per lane and load, all of a wave's loads in flight together, the rows'
+// while x is formed).  Lane l takes the 8-element
 // chunks c = l, l + 64, ... (C of them at most); a row's products add in chunk
 // order per lane, element order within a chunk, then over the lanes: the
 // upper 32 lanes onto the lower (permlane32 swap), the odd 16-lane rows onto
 // the even (permlane16 swap), then the 16 lanes of a row (quad xor 1, quad
 // xor 2, half mirror, mirror) -- a fixed order.  With R = 4 (R = 2) the swaps
 // also gather the rows: lanes [64 r / R, 64 (r + 1) / R) end holding the sum
-// of the wave's row r.  res may alias y (a row's value is read before it is
-// written, by the same lane); in must not.
+// of the wave's row r.  res may alias y (a wave reads the residuals of its
+// own rows only, before it writes them); in must not.
+constexpr int kGemvThreads = 256;
 enum GemvPre { kGemvPlain = 0, kGemvNorm = 1 };
 enum GemvPost { kGemvStore = 0, kGemvSiluPair = 1 };
+
+// Chunk c = lane + 64 j of a row of nch chunks, zero past the end: an
+// unconditional 16-byte load from a clamped address, then an AND with a mask
+// the compiler cannot see through (an empty asm) -- otherwise it turns the
+// select into a load under an exec-masked branch, and the loads of a wave's
+// branches are then all waited for at once (vmcnt(0) where they join).
+__device__ inline uint4 row_chunk(const uint16_t* row, int lane, int j, int nch) {
+  const int c = lane + 64 * j;
+  const uint4 v = *(const uint4*)(row + 8 * min(c, nch - 1));
+  uint32_t m = c < nch ? 0xffffffffu : 0u;
+  asm volatile("" : "+v"(m));
+  return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+}
 
 template <int R, int C, int PRE, int POST>
 __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, const uint16_t* res,
@@ -229,26 +243,37 @@ __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, co
   static_assert(R == 1 || R == 2 || R == 4, "rows per wave");
   static_assert(POST == kGemvStore || R >= 2, "a silu pair takes two rows");
   constexpr int kOut = POST == kGemvSiluPair ? R / 2 : R;  // outputs per wave and group
+  constexpr int wpg = kGemvThreads / 64;  // waves per workgroup
   const int lane = threadIdx.x & 63;
-  const int wpg = blockDim.x >> 6;
-  const int wave = blockIdx.x * wpg + (threadIdx.x >> 6);
-  const int stride = gridDim.x * wpg * kOut;
-  if (wave * kOut >= n_out) return;  // wave-uniform
+  const int n0 = (blockIdx.x * wpg + (threadIdx.x >> 6)) * kOut;  // the wave's first output
+  if (n0 >= n_out) return;  // wave-uniform
   const int nch = k / 8;
-  const uint4 zero = make_uint4(0, 0, 0, 0);
-  uint4 xv[C];
+  uint4 xv[C], nv[PRE == kGemvNorm ? C : 1];
 #pragma unroll
-  for (int j = 0; j < C; ++j) {
-    const int c = lane + 64 * j;
-    xv[j] = c < nch ? *(const uint4*)(in + 8 * c) : zero;
-  }
+  for (int j = 0; j < C; ++j) xv[j] = row_chunk(in, lane, j, nch);
   if constexpr (PRE == kGemvNorm) {
-    uint4 nv[C];
 #pragma unroll
-    for (int j = 0; j < C; ++j) {
-      const int c = lane + 64 * j;
-      nv[j] = c < nch ? *(const uint4*)(nw + 8 * c) : zero;
-    }
+    for (int j = 0; j < C; ++j) nv[j] = row_chunk(nw, lane, j, nch);
+  }
+  // the wave's rows (rows past the end re-read the last one), in flight while
+  // x is formed: issued after x, so x's wait leaves them out
+  uint4 wv[R][C];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = POST == kGemvSiluPair ? (r < kOut ? 0 : n_out) + min(n0 + r % kOut, n_out - 1)
+                                        : min(n0 + r, n_out - 1);
+    const uint16_t* const wr = w + (int64_t)n * k;
+#pragma unroll
+    for (int j = 0; j < C; ++j) wv[r][j] = row_chunk(wr, lane, j, nch);
+  }
+  constexpr int kLanesPerRow = 64 / R;
+  // the residual of the lane's row (lane / kLanesPerRow), read now -- before
+  // any write of y, and only rows of this wave's group; unconditionally (from
+  // y when there is none: an unused value), so no branch waits for it
+  uint16_t rbits = 0;
+  if constexpr (POST == kGemvStore) rbits = (res ? res : y)[min(n0 + lane / kLanesPerRow, n_out - 1)];
+  __builtin_amdgcn_sched_barrier(0);  // every load above issues before the first wait
+  if constexpr (PRE == kGemvNorm) {
     float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // rmsnorm_impl's threads lane + 64 i
 #pragma unroll
     for (int j = 0; j < C; ++j)
@@ -274,20 +299,7 @@ __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, co
       xv[j] = chunk_pack(o);
     }
   }
-  for (int n0 = wave * kOut; n0 < n_out; n0 += stride) {
-    uint4 wv[R][C];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      // (rows past the end re-read the last one)
-      const int n = POST == kGemvSiluPair ? (r < kOut ? 0 : n_out) + min(n0 + r % kOut, n_out - 1)
-                                          : min(n0 + r, n_out - 1);
-      const uint16_t* const wr = w + (int64_t)n * k;
-#pragma unroll
-      for (int j = 0; j < C; ++j) {
-        const int c = lane + 64 * j;
-        wv[r][j] = c < nch ? *(const uint4*)(wr + 8 * c) : zero;
-      }
-    }
+  {
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -325,7 +337,6 @@ __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, co
       s = __uint_as_float(q[0]) + __uint_as_float(q[1]);
     }
     s = row_sum16(s);
-    constexpr int kLanesPerRow = 64 / R;
     if constexpr (POST == kGemvSiluPair) {
       // the up rows' sums sit 32 lanes above their gate rows'
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
@@ -340,7 +351,7 @@ __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, co
       }
     } else if ((lane & (kLanesPerRow - 1)) == 0) {
       const int n = n0 + lane / kLanesPerRow;
-      if (n < n_out) y[n] = St<kBF16>::store(res ? s + St<kBF16>::load(res[n]) : s);
+      if (n < n_out) y[n] = St<kBF16>::store(res ? s + St<kBF16>::load(rbits) : s);
     }
   }
 }
@@ -350,10 +361,10 @@ __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, co
 // Rows per wave R and 8-element chunks per lane C (rows of up to 512 C
 // elements): four rows, or one, of up to 1024 elements (the 896-wide hidden
 // state of the q/k/v, o, gate/up and lm_head products; one row when there
-// are few rows), or one row of up to 8192 (the down product's 4864); the
-// gate/up pairs two or four rows (one or two outputs).
+// are few rows), or one row of up to 5120 (the down product's 4864) or 8192;
+// the gate/up pairs take two or four rows (one or two outputs).
 #define LUC_GEMV_KERNEL(NAME, PRE, POST, R, C)                                                    \
-  extern "C" __global__ __launch_bounds__(256) void NAME(uint16_t* y, const uint16_t* in,         \
+  extern "C" __global__ __launch_bounds__(luc::kGemvThreads) void NAME(uint16_t* y, const uint16_t* in, \
                                                          const uint16_t* w, const uint16_t* res,  \
                                                          const uint16_t* nw, float eps, int n,    \
                                                          int k) {                                 \
@@ -361,9 +372,11 @@ __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, co
   }
 LUC_GEMV_KERNEL(luc_gemv_bf16_r4c2, luc::kGemvPlain, luc::kGemvStore, 4, 2)
 LUC_GEMV_KERNEL(luc_gemv_bf16_r1c2, luc::kGemvPlain, luc::kGemvStore, 1, 2)
+LUC_GEMV_KERNEL(luc_gemv_bf16_r1c10, luc::kGemvPlain, luc::kGemvStore, 1, 10)
 LUC_GEMV_KERNEL(luc_gemv_bf16_r1c16, luc::kGemvPlain, luc::kGemvStore, 1, 16)
 LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r4c2, luc::kGemvNorm, luc::kGemvStore, 4, 2)
 LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r1c2, luc::kGemvNorm, luc::kGemvStore, 1, 2)
+LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r1c10, luc::kGemvNorm, luc::kGemvStore, 1, 10)
 LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r1c16, luc::kGemvNorm, luc::kGemvStore, 1, 16)
 LUC_GEMV_KERNEL(luc_gate_up_silu_bf16_r4c2, luc::kGemvPlain, luc::kGemvSiluPair, 4, 2)
 LUC_GEMV_KERNEL(luc_gate_up_silu_bf16_r2c16, luc::kGemvPlain, luc::kGemvSiluPair, 2, 16)

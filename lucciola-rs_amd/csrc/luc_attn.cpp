@@ -458,7 +458,8 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
                                     "luc_gather_floor_d128", "luc_stream_read"};
   for (int npl : {1, 2, 4, 8, 16}) names.push_back("luc_topk_filter_bf16_n" + std::to_string(npl));
   for (const char* kind : {"luc_gemv", "luc_rmsnorm_gemv"})
-    for (const char* v : {"_bf16_r4c2", "_bf16_r1c2", "_bf16_r1c16"}) names.push_back(std::string(kind) + v);
+    for (const char* v : {"_bf16_r4c2", "_bf16_r1c2", "_bf16_r1c10", "_bf16_r1c16"})
+      names.push_back(std::string(kind) + v);
   for (const char* kind : {"luc_gate_up_silu", "luc_rmsnorm_gate_up_silu"})
     for (const char* v : {"_bf16_r4c2", "_bf16_r2c16"}) names.push_back(std::string(kind) + v);
   for (int k = 32; k <= 1024; k *= 2) names.push_back("luc_top_p_sample_" + std::to_string(k));
@@ -780,10 +781,10 @@ namespace {
 // arguments (y, in, w, res, norm weight, eps, outputs, k).  Variant by shape:
 // rows of k <= 1024 on four rows per wave when there are at least 4096 of them
 // (lm_head), else on one row per wave (q/k/v, o: four times the waves to fill
-// the chip with); rows of k <= 8192 on one row per wave.  The gate/up silu
-// pairs (`pair`) take two rows per output: four rows per wave for k <= 1024,
-// else two.  4 waves per workgroup, at most 8 workgroups per CU (the waves
-// then stride over the row groups).
+// the chip with); rows of k <= 5120 or <= 8192 on one row per wave (ten or
+// sixteen 8-element chunks per lane).  The gate/up silu pairs (`pair`) take
+// two rows per output: four rows per wave for k <= 1024, else two.  4 waves
+// per workgroup, one row group per wave.
 int gemv_launch(luc_ctx* ctx, void* stream, const char* kind, bool pair, void* y, const void* in,
                 const void* w, const void* residual, const void* norm_weight, float eps, int n, int k) {
   if (n < 0) return fail(LUC_E_INVALID, "%s: n %d < 0", kind, n);
@@ -802,11 +803,11 @@ int gemv_launch(luc_ctx* ctx, void* stream, const char* kind, bool pair, void* y
     variant = k <= 1024 ? "_bf16_r4c2" : "_bf16_r2c16";
   } else {
     outs_per_wave = k <= 1024 && n >= 4096 ? 4 : 1;
-    variant = k > 1024 ? "_bf16_r1c16" : outs_per_wave == 4 ? "_bf16_r4c2" : "_bf16_r1c2";
+    variant = k > 5120 ? "_bf16_r1c16" : k > 1024 ? "_bf16_r1c10" : outs_per_wave == 4 ? "_bf16_r4c2" : "_bf16_r1c2";
   }
   hipFunction_t fn;
   if (int rc = get_fn(ctx, std::string(kind) + variant, &fn)) return rc;
-  const int64_t wgs = std::min<int64_t>(ceil_div(n, 4 * outs_per_wave), 8 * std::max(ctx->num_cus, 1));
+  const int64_t wgs = ceil_div(n, 4 * outs_per_wave);
   void* args[] = {&y, const_cast<void**>(&in), const_cast<void**>(&w), const_cast<void**>(&residual),
                   const_cast<void**>(&norm_weight), &eps, &n, &k};
   return launch(fn, dim3((unsigned)wgs), dim3(256), stream, args);
