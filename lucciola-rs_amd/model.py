@@ -102,6 +102,9 @@ def _dev(bits: np.ndarray, device) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(device)
 
 
+GEMV_MAX_K = 8192  # the longest weight row luc_gemv / luc_rmsnorm_gemv / luc_gate_up_silu take
+
+
 class Qwen2Model:
     """One sequence through the decoder: `forward(ids, cache_pos)` then
     `sample_greedy()`, or `generate` (models.rs:184-243).  The products of a
@@ -115,6 +118,9 @@ class Qwen2Model:
         self.lib = lib if lib is not None else library.default(torch.cuda.current_device())
         self.device = torch.device(device)
         d = cfg.head_dim
+        if cfg.hidden_size > GEMV_MAX_K:
+            raise ValueError(f"hidden_size {cfg.hidden_size} > {GEMV_MAX_K}: the one-row products "
+                             "(luc_gemv) take rows of at most that many elements")
         if cfg.hidden_size % cfg.num_attention_heads or d not in (64, 128):
             raise ValueError(f"unsupported head_dim {d}")
         T = lambda bits: _dev(bits, self.device).t().contiguous()  # noqa: E731  [in, out]
@@ -195,7 +201,10 @@ class Qwen2Model:
             self.lib.gemv(h, att, L["o_w"], residual=h)
             act = torch.empty(1, I, dtype=h.dtype, device=h.device)
             self.lib.gate_up_silu(act, h, L["post_norm"], eps, L["gate_up_w"])
-            self.lib.gemv(h, act, L["down_w"], residual=h)
+            if I <= GEMV_MAX_K:
+                self.lib.gemv(h, act, L["down_w"], residual=h)
+            else:  # rows longer than the GEMV takes (Qwen2-1.5B's 8960): a GEMM
+                h.addmm_(act, L["down_t"])
             return h
         norm = torch.empty_like(h)
         self.lib.rmsnorm(norm, h, L["in_norm"], eps)
