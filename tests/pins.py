@@ -345,7 +345,7 @@ def argmax_cases(rng):
     149509 (thread 5 both, the first in a thread's blocks of sixteen loads and
     the second past them: 3077 wins), and a row with nothing above -1e30."""
     out = []
-    for n in (1, 7, 1000, 2100, 151936):
+    for n in (1, 7, 1000, 2100, 8200, 151936):
         x = bits(rng.standard_normal(n), "bf16")
         out.append(x)
         if n > 3:

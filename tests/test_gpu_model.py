@@ -190,12 +190,16 @@ def test_argmax_ties_nan_and_floor(orc, luc):
     rng = np.random.default_rng(4)
     idx = torch.zeros(1, dtype=torch.int32, device="cuda")
     for c in pins.argmax_cases(rng):
-        say(f"  [gpu] argmax n={c.size}")
-        luc.argmax(to_dev(c, "bf16"), idx)
-        torch.cuda.synchronize()
         want = pins.argmax_tie_order(orc.to_f32(c, "bf16"))
         assert orc.argmax(c) == want
-        assert int(idx.cpu().item()) == want
+        # the row at the start of its buffer and one element in
+        padded = to_dev(np.concatenate([np.zeros(1, np.uint16), c]), "bf16")
+        for row in (to_dev(c, "bf16"), padded[1:]):
+            say(f"  [gpu] argmax n={c.size} offset={(row.data_ptr() % 16) // 2}")
+            idx.fill_(-7)
+            luc.argmax(row, idx)
+            torch.cuda.synchronize()
+            assert int(idx.cpu().item()) == want
 
 
 @pytest.fixture(scope="module")
@@ -476,16 +480,18 @@ def test_teacher_forced_logits_random_tokens(orc, qwen):
     assert flips == 0
 
 
-def test_greedy_from_checkpoint_second_shape(orc, tmp_path):
+@pytest.mark.parametrize("inter", [512, 8200])
+def test_greedy_from_checkpoint_second_shape(orc, tmp_path, inter):
     """A written-then-loaded checkpoint at another head shape (hidden 256, 4q/2kv,
     3 layers, vocab 1000, untied lm_head, rope scaling 2): the GPU loop and the
     oracle in lockstep for a 20-token prompt and 48 greedy steps, with the same
-    near-tie rule as above."""
+    near-tie rule as above.  Intermediate 8200 takes the down projection of a
+    decode step past the GEMV's 8192 onto a GEMM."""
     from oracle.model import OracleQwen2
     from lucciola_rs_amd.checkpoint import load_checkpoint, write_checkpoint
     from lucciola_rs_amd.model import Qwen2Config
     cfg = Qwen2Config(vocab_size=1000, hidden_size=256, num_hidden_layers=3, num_attention_heads=4,
-                      num_key_value_heads=2, intermediate_size=512, max_position_embeddings=4096,
+                      num_key_value_heads=2, intermediate_size=inter, max_position_embeddings=4096,
                       tie_word_embeddings=False, rope_scaling_factor=2.0, eos_token_id=999,
                       bos_token_id=998)
     write_checkpoint(str(tmp_path), cfg, random_weights(cfg, seed=31, std=0.08), shards=2)
