@@ -210,8 +210,8 @@ __device__ void argmax_impl(const uint16_t* x, int n, uint32_t* out) {
 // :568-590, and apply_activation_fused, :671).
 // One wave per R rows of w (HBM-bound: every byte of w read once, 16 bytes
 // per lane and load, all of a wave's loads in flight together, the rows'
-// while x is formed).  Lane l takes the 8-element
-// chunks c = l, l + 64, ... (C of them at most); a row's products add in chunk
+// loads while x is formed).  Lane l takes the 8-element chunks c = l, l + 64,
+// ... (C of them at most); a row's products add in chunk
 // order per lane, element order within a chunk, then over the lanes: the
 // upper 32 lanes onto the lower (permlane32 swap), the odd 16-lane rows onto
 // the even (permlane16 swap), then the 16 lanes of a row (quad xor 1, quad

@@ -17,7 +17,8 @@ fused into them, five launches a layer with the same bits as the unfused ones:
 luc_rmsnorm_gemv (q/k/v), luc_decode_step, luc_gemv (o, + h),
 luc_gate_up_silu (norm, gate/up, silu * up), luc_gemv (down, + h).
 then h = rmsnorm(h, norm) (models.rs:765-771, 815-822), logits = h @ lm_head^T
-(bf16, models.rs:295-342) and greedy sampling by luc_argmax (models.rs:344-360).
+(bf16, models.rs:295-342; one luc_rmsnorm_gemv) and greedy sampling by
+luc_argmax (models.rs:344-360).
 The q/k biases enter in the RoPE step and the v bias in the cache write, as in
 the reference (models.rs:505-534).
 
@@ -186,10 +187,12 @@ class Qwen2Model:
                                cfg.num_key_value_heads, cfg.head_dim, sm_scale(cfg.head_dim), att)
         return att
 
-    def _layer(self, li, h, attention):
+    def _layer(self, li, h, attention, out=None):
         """One decoder layer on the hidden rows h, which it updates in place
         (the residual adds are products with beta = 1 into h: one rounding, and
-        no copy of h into a new output).  One row: luc_gemv; more: GEMMs."""
+        no copy of h into a new output).  One row: luc_gemv; more: GEMMs.  With
+        `out` (one row) the layer's result goes there instead and h keeps the
+        layer's input."""
         cfg = self.cfg
         L = self.layers[li]
         I = cfg.intermediate_size
@@ -202,10 +205,15 @@ class Qwen2Model:
             act = torch.empty(1, I, dtype=h.dtype, device=h.device)
             self.lib.gate_up_silu(act, h, L["post_norm"], eps, L["gate_up_w"])
             if I <= GEMV_MAX_K:
-                self.lib.gemv(h, act, L["down_w"], residual=h)
-            else:  # rows longer than the GEMV takes (Qwen2-1.5B's 8960): a GEMM
-                h.addmm_(act, L["down_t"])
-            return h
+                y = h if out is None else out
+                self.lib.gemv(y, act, L["down_w"], residual=h)
+                return y
+            # rows longer than the GEMV takes (Qwen2-1.5B's 8960): a GEMM
+            h.addmm_(act, L["down_t"])
+            if out is None:
+                return h
+            out.copy_(h)
+            return out
         norm = torch.empty_like(h)
         self.lib.rmsnorm(norm, h, L["in_norm"], eps)
         qkv = torch.mm(norm, L["qkv_t"])
@@ -219,7 +227,8 @@ class Qwen2Model:
     # ---- forward (models.rs:693-830) ----
     def forward(self, input_ids, cache_pos: int) -> None:
         """Run the decoder over `input_ids` at positions cache_pos...; leaves the
-        last row's final-normed hidden state in self.hidden."""
+        last row's hidden state (before the final norm, which logits() applies
+        fused into lm_head) in self.hidden."""
         cfg = self.cfg
         S = len(input_ids)
         if S == 0:
@@ -238,15 +247,21 @@ class Qwen2Model:
             cu = torch.tensor([0, S], dtype=torch.int32, device=self.device)
             start = torch.tensor([cache_pos], dtype=torch.int32, device=self.device)
             attention = lambda li, qkv: self._attention_prefill(li, qkv, cache_pos, cu, start)  # noqa: E731
-        for li in range(cfg.num_hidden_layers):
+        n = cfg.num_hidden_layers
+        for li in range(n - 1):
             h = self._layer(li, h, attention)
-        last = h[S - 1:].contiguous()
-        self.lib.rmsnorm(self.hidden, last, self.final_norm, cfg.rms_norm_eps)
+        if S == 1:  # the last down product writes self.hidden
+            self._layer(n - 1, h, attention, out=self.hidden)
+        else:
+            h = self._layer(n - 1, h, attention)
+            self.hidden.copy_(h[S - 1:])
 
     def logits(self) -> torch.Tensor:
-        """bf16 logits [1, vocab] of the current hidden state (models.rs:295-342)."""
+        """bf16 logits [1, vocab] of the current hidden state: the final norm
+        (models.rs:765-771) and lm_head (models.rs:295-342) as one
+        luc_rmsnorm_gemv, the bits of the two in turn."""
         out = torch.empty(1, self.lm_head_w.shape[0], dtype=torch.bfloat16, device=self.device)
-        self.lib.gemv(out, self.hidden, self.lm_head_w)
+        self.lib.rmsnorm_gemv(out, self.hidden, self.final_norm, self.cfg.rms_norm_eps, self.lm_head_w)
         return out
 
     def sample_greedy(self) -> int:
@@ -293,9 +308,9 @@ class Qwen2Model:
         with torch.cuda.graph(graph):
             h = torch.empty(1, cfg.hidden_size, dtype=torch.bfloat16, device=self.device)
             self.lib.embedding(h, self.embed, self.idx)
-            for li in range(cfg.num_hidden_layers):
+            for li in range(cfg.num_hidden_layers - 1):
                 h = self._layer(li, h, attention)
-            self.lib.rmsnorm(self.hidden, h, self.final_norm, cfg.rms_norm_eps)
+            self._layer(cfg.num_hidden_layers - 1, h, attention, out=self.hidden)
             self.lib.argmax(self.logits(), self.idx)
             self.pos.add_(1)
         return graph
