@@ -16,7 +16,7 @@ For one row (a decode step) the products are GEMVs with the norms and silu * up
 fused into them, five launches a layer with the same bits as the unfused ones:
 luc_rmsnorm_gemv (q/k/v), luc_decode_step, luc_gemv (o, + h),
 luc_gate_up_silu (norm, gate/up, silu * up), luc_gemv (down, + h).
-then h = rmsnorm(h, norm) (models.rs:765-771, 815-822), logits = h @ lm_head^T
+then h = rmsnorm(h, norm) (models.rs:755-761, 814-820), logits = h @ lm_head^T
 (bf16, models.rs:295-342; one luc_rmsnorm_gemv) and greedy sampling by
 luc_argmax (models.rs:344-360).
 The q/k biases enter in the RoPE step and the v bias in the cache write, as in
@@ -258,7 +258,7 @@ class Qwen2Model:
 
     def logits(self) -> torch.Tensor:
         """bf16 logits [1, vocab] of the current hidden state: the final norm
-        (models.rs:765-771) and lm_head (models.rs:295-342) as one
+        (models.rs:755-761, 814-820) and lm_head (models.rs:344-383) as one
         luc_rmsnorm_gemv, the bits of the two in turn."""
         out = torch.empty(1, self.lm_head_w.shape[0], dtype=torch.bfloat16, device=self.device)
         self.lib.rmsnorm_gemv(out, self.hidden, self.final_norm, self.cfg.rms_norm_eps, self.lm_head_w)
