@@ -17,8 +17,8 @@ fused into them, five launches a layer with the same bits as the unfused ones:
 luc_rmsnorm_gemv (q/k/v), luc_decode_step, luc_gemv (o, + h),
 luc_gate_up_silu (norm, gate/up, silu * up), luc_gemv (down, + h).
 then h = rmsnorm(h, norm) (models.rs:755-761, 814-820), logits = h @ lm_head^T
-(bf16, models.rs:295-342; one luc_rmsnorm_gemv) and greedy sampling by
-luc_argmax (models.rs:344-360).
+(bf16, compute_logits, models.rs:344-383; one luc_rmsnorm_gemv) and greedy
+sampling by luc_argmax (models.rs:385-405).
 The q/k biases enter in the RoPE step and the v bias in the cache write, as in
 the reference (models.rs:505-534).
 

@@ -72,7 +72,7 @@ def test_silu_mul_matches_oracle(orc, luc):
     (3, 8, True),          # the narrowest k
 ])
 def test_gemv_against_f64(luc, n, k, res):
-    """y = x w^T (+ residual) for one bf16 row (models.rs:251-292 at M = 1):
+    """y = x w^T (+ residual) for one bf16 row (models.rs:252-295 at M = 1):
     f32 products summed in a fixed order, one rounding to bf16.  Against the
     f64 sum rounded once, an f32 sum of k <= 8192 terms can differ only where
     the exact result lies within ~k * 2^-24 (relative) of a bf16 rounding
