@@ -192,6 +192,45 @@ def test_decode_step_argument_checks(cdll):
     assert call(ws=ctypes.c_void_p(4096), ws_bytes=need - 4) == -5   # too small
 
 
+def test_gemv_argument_checks(cdll):
+    """The one-row products reject on the host, before touching the context:
+    dtype, k outside [8, 8192] or not a multiple of 8, negative rows, null or
+    misaligned operands, a null norm weight; no rows is a no-op."""
+    p = ctypes.c_void_p
+    def gemv(**kw):
+        args = dict(ctx=p(1), stream=None, dtype=0, y=p(256), x=p(256), w=p(512), res=None,
+                    n=896, k=896)
+        args.update(kw)
+        return cdll.luc_gemv(*args.values())
+    assert gemv(dtype=1) == -2
+    for k in (0, 12, 8200):
+        assert gemv(k=k) == -2
+    assert gemv(n=-1) == -1
+    assert gemv(x=None) == -1
+    assert gemv(x=p(258)) == -1               # 16-byte loads of x
+    assert gemv(w=p(520)) == -1               # and of w
+    assert gemv(n=0) == 0
+    def norm_gemv(**kw):
+        args = dict(ctx=p(1), stream=None, dtype=0, y=p(256), x=p(256), nw=p(768), eps=1e-6,
+                    w=p(512), res=None, n=896, k=896)
+        args.update(kw)
+        return cdll.luc_rmsnorm_gemv(*args.values())
+    assert norm_gemv(nw=None) == -1
+    assert norm_gemv(nw=p(776)) == -1
+    assert norm_gemv(k=900) == -2
+    assert norm_gemv(n=0) == 0
+    def gate_up(**kw):
+        args = dict(ctx=p(1), stream=None, dtype=0, act=p(256), x=p(256), nw=None, eps=1e-6,
+                    w=p(512), inter=4864, k=896)
+        args.update(kw)
+        return cdll.luc_gate_up_silu(*args.values())
+    assert gate_up(dtype=1) == -2
+    assert gate_up(k=8208) == -2
+    assert gate_up(w=None) == -1
+    assert gate_up(inter=0) == 0
+    assert gemv(ctx=None) == norm_gemv(ctx=None) == gate_up(ctx=None) == -1
+
+
 def test_prefill_argument_checks(cdll):
     """luc_paged_prefill rejects bad arguments on the host (no GPU call): the
     alignment its vector loads need, row strides, head sizes, missing arrays
