@@ -337,6 +337,16 @@ def model_bench(lib, torch, prompt_len=128, steps=128, eager_steps=8):
     mean_ctx = ctx0 + (steps + 1) / 2
     kv = int(mean_ctx) * cfg.num_hidden_layers * 2 * cfg.num_key_value_heads * cfg.head_dim * 2
     per_token = weights + kv
+    # the largest one-row product alone: the final norm + lm_head GEMV
+    # (luc_rmsnorm_gemv, 151936 x 896), 20 calls per graph, median of
+    # replays; alternate calls read a copy of the weights, so that no call
+    # finds the previous one's 272 MB in the 256 MB last-level cache
+    logits = torch.empty(1, m.lm_head_w.shape[0], dtype=torch.bfloat16, device=m.device)
+    heads = [m.lm_head_w, m.lm_head_w.clone()]
+    lm_us = graph_us(torch, lambda i: lib.rmsnorm_gemv(logits, m.hidden, m.final_norm,
+                                                       cfg.rms_norm_eps, heads[i % 2]), 20)
+    del heads
+    lm_bytes = (m.lm_head_w.numel() + logits.numel() + 2 * m.hidden.numel()) * 2
     del graph, m
     torch.cuda.empty_cache()
     return {"workload": "qwen2.5-0.5b greedy decode (random init, bf16, B=1, 24 layers)",
@@ -345,7 +355,10 @@ def model_bench(lib, torch, prompt_len=128, steps=128, eager_steps=8):
             "ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
             "bytes_per_token": int(per_token), "achieved_gbs": round(per_token / (ms * 1e-3) / 1e9, 1),
             "frac": round(per_token / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-            "eager_ms_per_token": round(eager_ms, 3)}
+            "eager_ms_per_token": round(eager_ms, 3),
+            "lm_head_gemv": {"kernel": "luc_rmsnorm_gemv_bf16_r4c2", "us_per_call": round(lm_us, 2),
+                             "bytes": int(lm_bytes), "achieved_gbs": round(lm_bytes / (lm_us * 1e-6) / 1e9, 1),
+                             "frac": round(lm_bytes / (lm_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}}
 
 
 def graph_us(torch, fn, n, reps=5, warm=3):
