@@ -362,7 +362,8 @@ __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, co
 // elements): four rows, or one, of up to 1024 elements (the 896-wide hidden
 // state of the q/k/v, o, gate/up and lm_head products; one row when there
 // are few rows), or one row of up to 5120 (the down product's 4864) or 8192;
-// the gate/up pairs take two or four rows (one or two outputs).
+// the gate/up pairs take four rows of up to 1024 or two of up to 5120 or 8192
+// (two outputs or one).
 #define LUC_GEMV_KERNEL(NAME, PRE, POST, R, C)                                                    \
   extern "C" __global__ __launch_bounds__(luc::kGemvThreads) void NAME(uint16_t* y, const uint16_t* in, \
                                                          const uint16_t* w, const uint16_t* res,  \
@@ -379,8 +380,10 @@ LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r1c2, luc::kGemvNorm, luc::kGemvStore, 1, 
 LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r1c10, luc::kGemvNorm, luc::kGemvStore, 1, 10)
 LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r1c16, luc::kGemvNorm, luc::kGemvStore, 1, 16)
 LUC_GEMV_KERNEL(luc_gate_up_silu_bf16_r4c2, luc::kGemvPlain, luc::kGemvSiluPair, 4, 2)
+LUC_GEMV_KERNEL(luc_gate_up_silu_bf16_r2c10, luc::kGemvPlain, luc::kGemvSiluPair, 2, 10)
 LUC_GEMV_KERNEL(luc_gate_up_silu_bf16_r2c16, luc::kGemvPlain, luc::kGemvSiluPair, 2, 16)
 LUC_GEMV_KERNEL(luc_rmsnorm_gate_up_silu_bf16_r4c2, luc::kGemvNorm, luc::kGemvSiluPair, 4, 2)
+LUC_GEMV_KERNEL(luc_rmsnorm_gate_up_silu_bf16_r2c10, luc::kGemvNorm, luc::kGemvSiluPair, 2, 10)
 LUC_GEMV_KERNEL(luc_rmsnorm_gate_up_silu_bf16_r2c16, luc::kGemvNorm, luc::kGemvSiluPair, 2, 16)
 
 extern "C" __global__ __launch_bounds__(256) void luc_rmsnorm_bf16(uint16_t* out, const uint16_t* in,

@@ -461,7 +461,7 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
     for (const char* v : {"_bf16_r4c2", "_bf16_r1c2", "_bf16_r1c10", "_bf16_r1c16"})
       names.push_back(std::string(kind) + v);
   for (const char* kind : {"luc_gate_up_silu", "luc_rmsnorm_gate_up_silu"})
-    for (const char* v : {"_bf16_r4c2", "_bf16_r2c16"}) names.push_back(std::string(kind) + v);
+    for (const char* v : {"_bf16_r4c2", "_bf16_r2c10", "_bf16_r2c16"}) names.push_back(std::string(kind) + v);
   for (int k = 32; k <= 1024; k *= 2) names.push_back("luc_top_p_sample_" + std::to_string(k));
   for (const char* dt : {"bf16", "f16"}) {
     names.push_back(std::string("luc_rope_append_") + dt);
@@ -783,7 +783,8 @@ namespace {
 // (lm_head), else on one row per wave (q/k/v, o: four times the waves to fill
 // the chip with); rows of k <= 5120 or <= 8192 on one row per wave (ten or
 // sixteen 8-element chunks per lane).  The gate/up silu pairs (`pair`) take
-// two rows per output: four rows per wave for k <= 1024, else two.  4 waves
+// two rows per output: four rows per wave for k <= 1024, else two (ten or
+// sixteen chunks per lane).  4 waves
 // per workgroup, one row group per wave.
 int gemv_launch(luc_ctx* ctx, void* stream, const char* kind, bool pair, void* y, const void* in,
                 const void* w, const void* residual, const void* norm_weight, float eps, int n, int k) {
@@ -800,7 +801,7 @@ int gemv_launch(luc_ctx* ctx, void* stream, const char* kind, bool pair, void* y
   const char* variant;
   if (pair) {
     outs_per_wave = k <= 1024 ? 2 : 1;
-    variant = k <= 1024 ? "_bf16_r4c2" : "_bf16_r2c16";
+    variant = k <= 1024 ? "_bf16_r4c2" : k <= 5120 ? "_bf16_r2c10" : "_bf16_r2c16";
   } else {
     outs_per_wave = k <= 1024 && n >= 4096 ? 4 : 1;
     variant = k > 5120 ? "_bf16_r1c16" : k > 1024 ? "_bf16_r1c10" : outs_per_wave == 4 ? "_bf16_r4c2" : "_bf16_r1c2";

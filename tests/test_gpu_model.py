@@ -120,6 +120,8 @@ def test_rmsnorm_gemv_equals_unfused(luc, n, k, res):
 @pytest.mark.parametrize("inter,k,norm", [
     (4864, 896, True),     # Qwen2.5-0.5B's gate/up
     (4864, 896, False), (1001, 1024, True), (3, 8, True), (37, 1032, False), (5, 8192, True),
+    (8960, 1536, True),    # Qwen2.5-1.5B's gate/up
+    (11, 5128, False),     # the narrowest k of the sixteen-chunk pair
 ])
 def test_gate_up_silu_equals_unfused(luc, inter, k, norm):
     """luc_gate_up_silu rounds each gate and up product to bf16 and applies
