@@ -217,7 +217,7 @@ __device__ void argmax_impl(const uint16_t* x, int n, uint32_t* out) {
 // the even (permlane16 swap), then the 16 lanes of a row (quad xor 1, quad
 // xor 2, half mirror, mirror) -- a fixed order.  With R = 4 (R = 2) the swaps
 // also gather the rows: lanes [64 r / R, 64 (r + 1) / R) end holding the sum
-// of the wave's row r.  res may alias y (a wave reads the residuals of its
+// of the wave's row r; R = 8 is two such groups of four.  res may alias y (a wave reads the residuals of its
 // own rows only, before it writes them); in must not.
 constexpr int kGemvThreads = 256;
 enum GemvPre { kGemvPlain = 0, kGemvNorm = 1 };
@@ -240,8 +240,11 @@ template <int R, int C, int PRE, int POST>
 __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, const uint16_t* res,
                           const uint16_t* nw, float eps, int n_out, int k) {
 #pragma clang fp contract(off)
-  static_assert(R == 1 || R == 2 || R == 4, "rows per wave");
+  static_assert(R == 1 || R == 2 || R == 4 || R == 8, "rows per wave");
   static_assert(POST == kGemvStore || R >= 2, "a silu pair takes two rows");
+  static_assert(POST == kGemvStore || R <= 4, "a silu pair takes at most four rows");
+  constexpr int NG = R > 4 ? R / 4 : 1;  // groups of (up to) four rows, each reduced alone
+  constexpr int RG = R / NG;             // rows per group
   constexpr int kOut = POST == kGemvSiluPair ? R / 2 : R;  // outputs per wave and group
   constexpr int wpg = kGemvThreads / 64;  // waves per workgroup
   const int lane = threadIdx.x & 63;
@@ -266,12 +269,15 @@ __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, co
 #pragma unroll
     for (int j = 0; j < C; ++j) wv[r][j] = row_chunk(wr, lane, j, nch);
   }
-  constexpr int kLanesPerRow = 64 / R;
-  // the residual of the lane's row (lane / kLanesPerRow), read now -- before
-  // any write of y, and only rows of this wave's group; unconditionally (from
-  // y when there is none: an unused value), so no branch waits for it
-  uint16_t rbits = 0;
-  if constexpr (POST == kGemvStore) rbits = (res ? res : y)[min(n0 + lane / kLanesPerRow, n_out - 1)];
+  constexpr int kLanesPerRow = 64 / RG;
+  // the residual of the lane's row in each group (lane / kLanesPerRow), read
+  // now -- before any write of y, and only rows of this wave; unconditionally
+  // (from y when there is none: an unused value), so no branch waits for it
+  uint16_t rbits[NG] = {};
+  if constexpr (POST == kGemvStore)
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi)
+      rbits[gi] = (res ? res : y)[min(n0 + gi * RG + lane / kLanesPerRow, n_out - 1)];
   __builtin_amdgcn_sched_barrier(0);  // every load above issues before the first wait
   if constexpr (PRE == kGemvNorm) {
     float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // rmsnorm_impl's threads lane + 64 i
@@ -311,26 +317,29 @@ __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, co
           a = fmaf(St<kBF16>::load(chunk_elem(xv[j], e)), St<kBF16>::load(chunk_elem(wv[r][j], e)), a);
       acc[r] = a;
     }
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    const float* const ga = acc + gi * RG;  // the group's rows
     // lanes l and l + 32, then 16-lane rows 2i and 2i + 1, then a row's 16 lanes
     float s;
-    if constexpr (R == 4) {
-      const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0]), __float_as_uint(acc[2]),
+    if constexpr (RG == 4) {
+      const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ga[0]), __float_as_uint(ga[2]),
                                                         false, false);
-      const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[1]), __float_as_uint(acc[3]),
+      const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ga[1]), __float_as_uint(ga[3]),
                                                         false, false);
       // h02: rows 0 (lanes < 32) and 2; h13: rows 1 and 3
       const float h02 = __uint_as_float(s02[0]) + __uint_as_float(s02[1]);
       const float h13 = __uint_as_float(s13[0]) + __uint_as_float(s13[1]);
       const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(h02), __float_as_uint(h13), false, false);
       s = __uint_as_float(q[0]) + __uint_as_float(q[1]);  // 16-lane row r: row r
-    } else if constexpr (R == 2) {
-      const auto s01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0]), __float_as_uint(acc[1]),
+    } else if constexpr (RG == 2) {
+      const auto s01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ga[0]), __float_as_uint(ga[1]),
                                                         false, false);
       const float h = __uint_as_float(s01[0]) + __uint_as_float(s01[1]);  // lanes < 32: row 0
       const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(h), __float_as_uint(h), false, false);
       s = __uint_as_float(q[0]) + __uint_as_float(q[1]);  // lanes < 32: row 0; the rest: row 1
     } else {
-      const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0]), __float_as_uint(acc[0]),
+      const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ga[0]), __float_as_uint(ga[0]),
                                                        false, false);
       const float h = __uint_as_float(s0[0]) + __uint_as_float(s0[1]);
       const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(h), __float_as_uint(h), false, false);
@@ -350,18 +359,19 @@ __device__ void gemv_impl(uint16_t* y, const uint16_t* in, const uint16_t* w, co
         }
       }
     } else if ((lane & (kLanesPerRow - 1)) == 0) {
-      const int n = n0 + lane / kLanesPerRow;
-      if (n < n_out) y[n] = St<kBF16>::store(res ? s + St<kBF16>::load(rbits) : s);
+      const int n = n0 + gi * RG + lane / kLanesPerRow;
+      if (n < n_out) y[n] = St<kBF16>::store(res ? s + St<kBF16>::load(rbits[gi]) : s);
     }
+  }
   }
 }
 
 }  // namespace luc
 
 // Rows per wave R and 8-element chunks per lane C (rows of up to 512 C
-// elements): four rows, or one, of up to 1024 elements (the 896-wide hidden
-// state of the q/k/v, o, gate/up and lm_head products; one row when there
-// are few rows), or one row of up to 5120 (the down product's 4864) or 8192;
+// elements): eight, four or one row of up to 1024 elements (the 896-wide
+// hidden state of the lm_head, gate/up, q/k/v and o products; fewer rows per
+// wave when there are fewer rows), or one row of up to 5120 (the down product's 4864) or 8192;
 // the gate/up pairs take four rows of up to 1024 or two of up to 5120 or 8192
 // (two outputs or one).
 #define LUC_GEMV_KERNEL(NAME, PRE, POST, R, C)                                                    \
@@ -376,6 +386,7 @@ LUC_GEMV_KERNEL(luc_gemv_bf16_r1c2, luc::kGemvPlain, luc::kGemvStore, 1, 2)
 LUC_GEMV_KERNEL(luc_gemv_bf16_r1c10, luc::kGemvPlain, luc::kGemvStore, 1, 10)
 LUC_GEMV_KERNEL(luc_gemv_bf16_r1c16, luc::kGemvPlain, luc::kGemvStore, 1, 16)
 LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r4c2, luc::kGemvNorm, luc::kGemvStore, 4, 2)
+LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r8c2, luc::kGemvNorm, luc::kGemvStore, 8, 2)
 LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r1c2, luc::kGemvNorm, luc::kGemvStore, 1, 2)
 LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r1c10, luc::kGemvNorm, luc::kGemvStore, 1, 10)
 LUC_GEMV_KERNEL(luc_rmsnorm_gemv_bf16_r1c16, luc::kGemvNorm, luc::kGemvStore, 1, 16)

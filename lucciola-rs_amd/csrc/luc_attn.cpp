@@ -460,6 +460,7 @@ int luc_init(int device, const char* code_object_dir, luc_ctx** out_ctx) {
   for (const char* kind : {"luc_gemv", "luc_rmsnorm_gemv"})
     for (const char* v : {"_bf16_r4c2", "_bf16_r1c2", "_bf16_r1c10", "_bf16_r1c16"})
       names.push_back(std::string(kind) + v);
+  names.push_back("luc_rmsnorm_gemv_bf16_r8c2");
   for (const char* kind : {"luc_gate_up_silu", "luc_rmsnorm_gate_up_silu"})
     for (const char* v : {"_bf16_r4c2", "_bf16_r2c10", "_bf16_r2c16"}) names.push_back(std::string(kind) + v);
   for (int k = 32; k <= 1024; k *= 2) names.push_back("luc_top_p_sample_" + std::to_string(k));
@@ -779,9 +780,10 @@ int luc_rmsnorm(luc_ctx* ctx, void* stream, int dtype, void* out, const void* in
 namespace {
 // The one-row products: `kind` names the kernel family, all with the
 // arguments (y, in, w, res, norm weight, eps, outputs, k).  Variant by shape:
-// rows of k <= 1024 on four rows per wave when there are at least 4096 of them
-// (lm_head), else on one row per wave (q/k/v, o: four times the waves to fill
-// the chip with); rows of k <= 5120 or <= 8192 on one row per wave (ten or
+// rows of k <= 1024 on four rows per wave when there are at least 4096 of them,
+// eight with the norm when there are at least 65536 (the final norm + lm_head:
+// 47.0 against 48.0 us at 151936 x 896), else on one row per wave (q/k/v, o:
+// four times the waves to fill the chip with); rows of k <= 5120 or <= 8192 on one row per wave (ten or
 // sixteen 8-element chunks per lane).  The gate/up silu pairs (`pair`) take
 // two rows per output: four rows per wave for k <= 1024, else two (ten or
 // sixteen chunks per lane).  4 waves
@@ -804,7 +806,9 @@ int gemv_launch(luc_ctx* ctx, void* stream, const char* kind, bool pair, void* y
     variant = k <= 1024 ? "_bf16_r4c2" : k <= 5120 ? "_bf16_r2c10" : "_bf16_r2c16";
   } else {
     outs_per_wave = k <= 1024 && n >= 4096 ? 4 : 1;
-    variant = k > 5120 ? "_bf16_r1c16" : k > 1024 ? "_bf16_r1c10" : outs_per_wave == 4 ? "_bf16_r4c2" : "_bf16_r1c2";
+    if (norm_weight && k <= 1024 && n >= 65536) outs_per_wave = 8;
+    variant = k > 5120 ? "_bf16_r1c16" : k > 1024 ? "_bf16_r1c10" : outs_per_wave == 8 ? "_bf16_r8c2"
+              : outs_per_wave == 4 ? "_bf16_r4c2" : "_bf16_r1c2";
   }
   hipFunction_t fn;
   if (int rc = get_fn(ctx, std::string(kind) + variant, &fn)) return rc;

@@ -97,6 +97,7 @@ def test_gemv_against_f64(luc, n, k, res):
 @pytest.mark.parametrize("n,k,res", [
     (1152, 896, False), (9728, 896, True), (37, 4864, False), (5, 8192, True), (3, 8, False),
     (4096, 1024, False), (7, 1032, True),
+    (65537, 896, True), (70001, 1024, False),   # eight rows a wave (lm_head's shape class)
 ])
 def test_rmsnorm_gemv_equals_unfused(luc, n, k, res):
     """luc_rmsnorm_gemv forms RMSNorm(x) in each wave with luc_rmsnorm's
